@@ -1,0 +1,373 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 TORQ-Tile quantized micro-kernels on one MI355X.
+
+Headline (BASELINE.json metric "W4A8 GEMV HBM GB/s (M=1) + W8A8 GEMM int8 TOPS (M=512),
+% roofline"):
+  * value   = W8A8 GEMM int8 TOPS on configs[1] (gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt,
+              M=512, K=4096, N=4096), with its MFMA roofline;
+  * w4a8    = W4A8 decode GEMV HBM GB/s on configs[2] at M=1 (K=4096, N=11008), with its HBM
+              roofline; M=4 and M=8 are reported beside it.
+The remaining configurations (int8->int32 GEMM, W4A16, int8 implicit-GEMM conv) are timed the
+same way and reported under "configs".
+
+A step is one launch of the kernel over one batch of synthetic inputs already resident in
+HBM. Each launch reads a different copy of the weights (and activations): the copies together
+exceed the 256 MB Infinity Cache, so the GB/s figures are HBM figures. Kernel time comes from
+HIP events recorded on the stream the kernels are launched on, around exactly `--steps`
+back-to-back launches after `--warmup` untimed ones.
+
+cpu_baseline: the portable C restatement of the reference kernel (oracle/, the same tile loop
+the reference runs with VLENB = 16), timed on this host's cores over a bounded sample.
+"""
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
+CACHE_BYTES = 256 << 20      # Infinity Cache (MALL)
+
+W8A8 = dict(m=512, n=4096, k=4096)
+W4A8 = dict(m=1, n=11008, k=4096)
+W4A16 = dict(m=32, n=14336, k=4096, bl=32)
+CONV = dict(ID=8, IH=56, IW=56, IC=128, OC=128, KH=3, KW=3, pad=1)
+CLAMP = dict(m=64, n=256, k=512)
+
+
+def load_lib():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location(
+        "tqt_gfx950", os.path.join(ROOT, "torq-tile_amd", "tqt_gfx950.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod, mod.load()
+
+
+def copies_for(bytes_per_copy):
+    return max(2, int(math.ceil(1.25 * CACHE_BYTES / max(1, bytes_per_copy))) + 1)
+
+
+class Timer:
+    """HIP events on the launch stream around `steps` launches."""
+
+    def __init__(self, torch, stream):
+        self.torch = torch
+        self.stream = stream
+
+    def run(self, launch, copies, warmup, steps):
+        torch = self.torch
+        for i in range(warmup):
+            launch(i % copies)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(self.stream)
+        for i in range(steps):
+            launch((warmup + i) % copies)
+        end.record(self.stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps  # ms per launch
+
+
+# ------------------------------------------------------------------------------------------
+# Synthetic inputs (BASELINE.json recipes; numpy only, seeded)
+# ------------------------------------------------------------------------------------------
+
+def inputs_w8a8(rng, m, n, k):
+    zp_a = int(rng.integers(-20, 21))
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    A = np.clip(np.rint(x / np.float32(0.02)) + zp_a, -128, 127).astype(np.int8)
+    B = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    scale_b = rng.uniform(0.001, 0.01, size=n).astype(np.float32)
+    bias = rng.integers(-1000, 1001, size=n).astype(np.int64)
+    fused = (bias - zp_a * B.astype(np.int64).sum(axis=1)).astype(np.int32)
+    return A, B, scale_b, fused, zp_a
+
+
+def inputs_w4a8(rng, m, n, k):
+    Af = rng.standard_normal((m, k), dtype=np.float32)
+    fmax = np.maximum(Af.max(axis=1), 0).astype(np.float32)
+    fmin = np.minimum(Af.min(axis=1), 0).astype(np.float32)
+    s = ((fmax - fmin) / np.float32(255.0)).astype(np.float32)
+    zp = np.clip(np.rint(np.float32(-128.0) - fmin / s), -128, 127).astype(np.int32)
+    A = np.clip(np.rint(Af / s[:, None]) + zp[:, None], -128, 127).astype(np.int8)
+    Bp = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    sb = rng.uniform(0.005, 0.02, size=n).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    return A, Bp, s, zp, sb, bias
+
+
+# ------------------------------------------------------------------------------------------
+# Per-config measurements
+# ------------------------------------------------------------------------------------------
+
+def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng):
+    m, n, k = W8A8["m"], W8A8["n"], W8A8["k"]
+    A, B, sb, bias, zp_a = inputs_w8a8(rng, m, n, k)
+    per_copy = A.nbytes + B.nbytes
+    nc = copies_for(per_copy)
+    dA = [torch.from_numpy(A).cuda()]
+    dB = [torch.from_numpy(B).cuda()]
+    for _ in range(nc - 1):
+        dA.append(dA[0].clone())
+        dB.append(dB[0].clone())
+    dsb = torch.from_numpy(sb).cuda()
+    dbias = torch.from_numpy(bias).cuda()
+    dD = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    p = mod.QAI8QSI8CXParams(0.02, zp_a, dsb.data_ptr(), n, 0.05, 0)
+    f = lib.fn("w8a8", "run_async")
+    s = timer.stream.cuda_stream
+
+    def launch(i):
+        f(m, n, k, dA[i].data_ptr(), k, 0, dB[i].data_ptr(), k, 0, None, n, dD.data_ptr(), n,
+          dbias.data_ptr(), -128, 127, ctypes.byref(p), s)
+
+    ms = timer.run(launch, nc, warmup, steps)
+    ops = 2.0 * m * n * k
+    algo_bytes = A.nbytes + B.nbytes + 4 * n + 4 * n + m * n
+    tops = ops / (ms * 1e-3) / 1e12
+    return dict(ms=ms, tops=tops, gbs=algo_bytes / (ms * 1e-3) / 1e9, ops=ops,
+                bytes=algo_bytes, copies=nc, inputs=(A, B, sb, bias, zp_a))
+
+
+def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m):
+    n, k = W4A8["n"], W4A8["k"]
+    A, Bp, sa, za, sb, bias = inputs_w4a8(rng, m, n, k)
+    nc = copies_for(Bp.nbytes)
+    dB = [torch.from_numpy(Bp).cuda()]
+    for _ in range(nc - 1):
+        dB.append(dB[0].clone())
+    dA = [torch.from_numpy(A).cuda() for _ in range(nc)]
+    dsa, dza, dsb = (torch.from_numpy(x).cuda() for x in (sa, za, sb))
+    dbias = torch.from_numpy(bias).cuda()
+    dD = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    p = mod.QAI8DXQSI4CXParams(dsa.data_ptr(), dza.data_ptr(), dsb.data_ptr())
+    f = lib.fn("w4a8", "run_async")
+    s = timer.stream.cuda_stream
+
+    def launch(i):
+        f(m, n, k, dA[i].data_ptr(), k, 0, dB[i].data_ptr(), k, 0, None, n, dD.data_ptr(), n,
+          dbias.data_ptr(), -math.inf, math.inf, ctypes.byref(p), s)
+
+    ms = timer.run(launch, nc, warmup, steps)
+    # B n*k/2 + scale_b 4n + bias 4n + A m*k + scale_a/zp_a 8m + D 4mn
+    algo_bytes = n * k // 2 + 4 * n + 4 * n + m * k + 8 * m + 4 * m * n
+    return dict(ms=ms, gbs=algo_bytes / (ms * 1e-3) / 1e9, bytes=algo_bytes,
+                ops=2.0 * m * n * k, copies=nc, inputs=(A, Bp, sa, za, sb, bias))
+
+
+def bench_w4a16(torch, mod, lib, timer, warmup, steps, rng):
+    m, n, k, bl = W4A16["m"], W4A16["n"], W4A16["k"], W4A16["bl"]
+    A = rng.standard_normal((m, k)).astype(np.float16)
+    Bp = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    S = rng.uniform(0.005, 0.02, size=(n, k // bl)).astype(np.float16)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float16)
+    nc = copies_for(Bp.nbytes + S.nbytes)
+    dB = [torch.from_numpy(Bp).cuda()]
+    dS = [torch.from_numpy(S).cuda()]
+    for _ in range(nc - 1):
+        dB.append(dB[0].clone())
+        dS.append(dS[0].clone())
+    dA = torch.from_numpy(A).cuda()
+    dbias = torch.from_numpy(bias).cuda()
+    dD = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    shim = ctypes.CDLL(os.path.join(ROOT, "tests", "abi_shim", "libtqt_test_shim.so"))
+    f = shim.tqts_run_w4a16_async
+    f.restype = None
+    f.argtypes = [ctypes.c_size_t] * 4 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                          ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
+                                          ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                          ctypes.c_size_t, ctypes.c_void_p, ctypes.c_uint16,
+                                          ctypes.c_uint16, ctypes.c_void_p]
+    cmin = int(np.float16(-65504.0).view(np.uint16))
+    cmax = int(np.float16(65504.0).view(np.uint16))
+    s = timer.stream.cuda_stream
+
+    def launch(i):
+        f(m, n, k, bl, dA.data_ptr(), k, dB[i].data_ptr(), k, dS[i].data_ptr(), k // bl, None, n,
+          dD.data_ptr(), n, dbias.data_ptr(), cmin, cmax, s)
+
+    ms = timer.run(launch, nc, warmup, steps)
+    algo_bytes = Bp.nbytes + S.nbytes + A.nbytes + bias.nbytes + 2 * m * n
+    flops = 2.0 * m * n * k
+    return dict(ms=ms, gbs=algo_bytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
+                bytes=algo_bytes, ops=flops, copies=nc)
+
+
+def bench_conv(torch, mod, lib, timer, warmup, steps, rng):
+    c = CONV
+    ID, IH, IW, IC, OC, KH, KW, pad = (c["ID"], c["IH"], c["IW"], c["IC"], c["OC"], c["KH"],
+                                       c["KW"], c["pad"])
+    K = KH * KW * IC
+    inp = rng.integers(-128, 128, size=(ID, IH, IW, IC), dtype=np.int8)
+    W = rng.integers(-127, 128, size=(OC, K), dtype=np.int8)
+    sb = rng.uniform(0.001, 0.01, size=OC).astype(np.float32)
+    bias = (rng.integers(-1000, 1001, size=OC) - 3 * W.astype(np.int64).sum(axis=1)).astype(
+        np.int32)
+    conv = mod.conv_params((ID, IH, IW), (1, KH, KW), (1, 1, 1), (1, 1, 1), (0, pad, pad), IC, OC)
+    M = conv.output_shape[0] * conv.output_shape[1] * conv.output_shape[2]
+    nc = copies_for(inp.nbytes + W.nbytes)
+    din = [torch.from_numpy(inp).cuda()]
+    for _ in range(nc - 1):
+        din.append(din[0].clone())
+    dW = torch.from_numpy(W).cuda()
+    dsb = torch.from_numpy(sb).cuda()
+    dbias = torch.from_numpy(bias).cuda()
+    dD = torch.empty((M, OC), dtype=torch.int8, device="cuda")
+    p = mod.QAI8QSI8CXParams(0.02, 3, dsb.data_ptr(), OC, 0.05, 0)
+    f = lib.fn("igemmcl", "run_async")
+    s = timer.stream.cuda_stream
+
+    def launch(i):
+        f(M, OC, K, din[i].data_ptr(), 0, 0, 0, dW.data_ptr(), K, 0, None, 0, dD.data_ptr(), OC,
+          dbias.data_ptr(), -128, 127, ctypes.byref(conv), ctypes.byref(p), s)
+
+    ms = timer.run(launch, nc, warmup, steps)
+    ops = 2.0 * OC * M * K
+    algo_bytes = inp.nbytes + W.nbytes + 4 * OC + 4 * OC + M * OC
+    return dict(ms=ms, tops=ops / (ms * 1e-3) / 1e12, gbs=algo_bytes / (ms * 1e-3) / 1e9,
+                bytes=algo_bytes, ops=ops, copies=nc)
+
+
+def bench_clamp(torch, mod, lib, timer, warmup, steps, rng):
+    m, n, k = CLAMP["m"], CLAMP["n"], CLAMP["k"]
+    A = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    B = rng.integers(-128, 128, size=(k, n), dtype=np.int8)
+    dA = torch.from_numpy(A).cuda()
+    dB = torch.from_numpy(B).cuda()
+    dD = torch.empty((m, n), dtype=torch.int32, device="cuda")
+    f = lib.fn("clamp", "run_async")
+    s = timer.stream.cuda_stream
+
+    def launch(i):
+        f(m, n, k, dA.data_ptr(), k, 0, dB.data_ptr(), n, 0, None, n, dD.data_ptr(), n,
+          -2**31, 2**31 - 1, s)
+
+    ms = timer.run(launch, 1, warmup, steps)
+    ops = 2.0 * m * n * k
+    return dict(ms=ms, tops=ops / (ms * 1e-3) / 1e12, bytes=A.nbytes + B.nbytes + 4 * m * n,
+                ops=ops, copies=1)
+
+
+# ------------------------------------------------------------------------------------------
+# CPU baseline (oracle restatement of the reference kernel; bounded sample)
+# ------------------------------------------------------------------------------------------
+
+def cpu_baseline(w8, budget_s=10.0):
+    import tqt_testlib as T
+
+    o = T.oracle()
+    cores = min(16, os.cpu_count() or 1)
+    o.tqto_set_threads(cores)
+    A, B, sb, bias, _ = w8["inputs"]
+    m, n, k = W8A8["m"], W8A8["n"], W8A8["k"]
+    D = np.empty((m, n), np.int8)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        o.tqto_gemm_qai8_qai8_qsi8cxt(m, n, k, T.ptr(A), k, T.ptr(B), k, None, n, T.ptr(D), n,
+                                      T.ptr(bias), -128, 127, 0.02, T.ptr(sb), n, 0.05, 0)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    tops = reps * 2.0 * m * n * k / el / 1e12
+    return dict(value=round(tops, 4), unit="TOPS", cores=cores, kind="port",
+                sample="%d full W8A8 M=512 K=4096 N=4096 GEMMs (portable C, reference 4x16 "
+                       "tile loop, OpenMP over tiles) in %.1f s" % (reps, el))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: these kernels run on a single MI355X and this "
+              "build has no multi-GPU path (use --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    mod, lib = load_lib()
+    stream = torch.cuda.Stream()
+    timer = Timer(torch, stream)
+    rng = np.random.default_rng(42)
+    K, W = args.steps, args.warmup
+
+    with torch.cuda.stream(stream):
+        w8 = bench_w8a8(torch, mod, lib, timer, W, K, rng)
+        w4 = {mm: bench_w4a8(torch, mod, lib, timer, W, K, rng, mm) for mm in (1, 4, 8)}
+        w416 = bench_w4a16(torch, mod, lib, timer, W, K, rng)
+        cv = bench_conv(torch, mod, lib, timer, W, K, rng)
+        cl = bench_clamp(torch, mod, lib, timer, W, K, rng)
+
+    w41 = w4[1]
+    out = {
+        "metric": "W4A8 GEMV HBM GB/s (M=1) + W8A8 GEMM int8 TOPS (M=512), % roofline",
+        "value": round(w8["tops"], 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(w8["ms"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded BASELINE.json recipes), %d rotating weight copies > 256 MB "
+                "MALL" % w8["copies"],
+        "config": {"workload": "gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt M=512 K=4096 "
+                               "N=4096 (W8A8 prefill, int8 requantized out)",
+                   "M": 512, "K": 4096, "N": 4096},
+        "roofline": {"bound": "mfma", "achieved": round(w8["tops"], 3), "peak": INT8_PEAK_TOPS,
+                     "unit": "TOPS", "frac": round(w8["tops"] / INT8_PEAK_TOPS, 4),
+                     "traffic": None},
+        "w4a8": {
+            "workload": "gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt M=1 K=4096 N=11008 (W4A8 decode)",
+            "value": round(w41["gbs"], 2), "unit": "GB/s", "us_per_launch": round(w41["ms"] * 1e3, 3),
+            "roofline": {"bound": "hbm", "achieved": round(w41["gbs"], 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(w41["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": None},
+            "M4": {"GB/s": round(w4[4]["gbs"], 2), "us": round(w4[4]["ms"] * 1e3, 3),
+                   "frac": round(w4[4]["gbs"] / HBM_PEAK_GBS, 4)},
+            "M8": {"GB/s": round(w4[8]["gbs"], 2), "us": round(w4[8]["ms"] * 1e3, 3),
+                   "frac": round(w4[8]["gbs"] / HBM_PEAK_GBS, 4)},
+            "copies": w41["copies"],
+        },
+        "configs": {
+            "gemm_clamp_i32_i8_i8 64x256x512": {"us": round(cl["ms"] * 1e3, 3),
+                                                "TOPS": round(cl["tops"], 3)},
+            "w4a16 32x14336x4096 bl32": {"us": round(w416["ms"] * 1e3, 3),
+                                         "GB/s": round(w416["gbs"], 2),
+                                         "hbm_frac": round(w416["gbs"] / HBM_PEAK_GBS, 4),
+                                         "TFLOP/s": round(w416["tflops"], 2)},
+            "igemmcl 8x56x56x128 3x3 OC128": {"us": round(cv["ms"] * 1e3, 3),
+                                              "TOPS": round(cv["tops"], 3),
+                                              "mfma_frac": round(cv["tops"] / INT8_PEAK_TOPS, 4)},
+        },
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(w8)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

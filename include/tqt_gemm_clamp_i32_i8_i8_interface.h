@@ -1,0 +1,41 @@
+/*
+ * Interface of micro-kernel type gemm_clamp_i32_i8_i8: function-pointer types and the ukernel struct that
+ * every variant of this type fills. Same names, member order and signatures as the
+ * reference's src/gemm/gemm_i8_i8/gemm_clamp_i32_i8_i8/tqt_gemm_clamp_i32_i8_i8_interface.h:20-50, so a caller that binds a variant through
+ * this struct can bind the gfx950 variant (tqt_*_gemm_clamp_i32_i8_i8_mfma_gfx950) unchanged.
+ */
+#ifndef TQT_GEMM_CLAMP_I32_I8_I8_INTERFACE_H
+#define TQT_GEMM_CLAMP_I32_I8_I8_INTERFACE_H
+
+#include "tqt_gfx950_common.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef size_t (*tqt_gemm_clamp_i32_i8_i8_get_m_step_func)(void);
+typedef size_t (*tqt_gemm_clamp_i32_i8_i8_get_n_step_func)(void);
+typedef size_t (*tqt_gemm_clamp_i32_i8_i8_get_a_offset_func)(size_t m_idx, size_t k_idx, size_t lda);
+typedef size_t (*tqt_gemm_clamp_i32_i8_i8_get_b_offset_func)(size_t n_idx, size_t k_idx, size_t ldb);
+typedef size_t (*tqt_gemm_clamp_i32_i8_i8_get_c_offset_func)(size_t m_idx, size_t n_idx, size_t ldc);
+typedef size_t (*tqt_gemm_clamp_i32_i8_i8_get_d_offset_func)(size_t m_idx, size_t n_idx, size_t ldd);
+typedef size_t (*tqt_gemm_clamp_i32_i8_i8_get_d_size_func)(size_t m, size_t n);
+typedef void (*tqt_gemm_clamp_i32_i8_i8_run_gemm_func)(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, int32_t clamp_min, int32_t clamp_max);
+
+struct tqt_gemm_clamp_i32_i8_i8_ukernel
+{
+    tqt_gemm_clamp_i32_i8_i8_get_m_step_func get_m_step;
+    tqt_gemm_clamp_i32_i8_i8_get_n_step_func get_n_step;
+    tqt_gemm_clamp_i32_i8_i8_get_a_offset_func get_a_offset;
+    tqt_gemm_clamp_i32_i8_i8_get_b_offset_func get_b_offset;
+    tqt_gemm_clamp_i32_i8_i8_get_c_offset_func get_c_offset;
+    tqt_gemm_clamp_i32_i8_i8_get_d_offset_func get_d_offset;
+    tqt_gemm_clamp_i32_i8_i8_get_d_size_func get_d_size;
+    tqt_gemm_clamp_i32_i8_i8_run_gemm_func run_gemm;
+};
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif

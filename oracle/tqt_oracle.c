@@ -1,0 +1,838 @@
+/*
+ * TEST INFRASTRUCTURE ONLY (see tqt_oracle.h). CPU restatement of the reference semantics of
+ * the five TORQ-Tile kernel types built for gfx950. Compiled with -ffp-contract=off so that
+ * every float operation written here rounds once, in the order written.
+ *
+ * The integer kernels keep the reference's output tiling (m_step = 4 rows by n_step = 16
+ * columns, i.e. VLENB = 16 as on a VLEN = 128 core, cpp:16-20 of each reference kernel) so
+ * the same code serves as the timed CPU baseline; the per-output arithmetic is independent
+ * of the tiling.
+ */
+#include "tqt_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define TQTO_MR 4
+#define TQTO_NR 16
+
+static int g_threads = 1;
+
+void tqto_set_threads(int n)
+{
+    g_threads = n < 1 ? 1 : n;
+}
+
+int tqto_get_threads(void)
+{
+    return g_threads;
+}
+
+/* ------------------------------------------------------------------------------------------
+ * binary16 helpers
+ * ---------------------------------------------------------------------------------------- */
+
+float tqto_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    uint32_t bits;
+    float f;
+    if (e == 0) {
+        /* zero or subnormal: m * 2^-24, exact in binary32 */
+        f = (float)m * 5.9604644775390625e-08f;
+        return sign ? -f : f;
+    }
+    if (e == 31) {
+        bits = sign | 0x7f800000u | (m << 13);
+    } else {
+        bits = sign | ((e - 15u + 127u) << 23) | (m << 13);
+    }
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* Round a value given as (sign, 64-bit significand `sig` with value sig * 2^exp2) to binary16,
+ * nearest-even. Used for both the f32 and the f64 narrowing. */
+static uint16_t round_to_f16(uint32_t sign16, uint64_t sig, int exp2)
+{
+    /* normalise sig so that bit 63 is set */
+    if (sig == 0) {
+        return (uint16_t)sign16;
+    }
+    while (!(sig >> 63)) {
+        sig <<= 1;
+        exp2 -= 1;
+    }
+    /* value = 1.xxx * 2^(exp2 + 63) */
+    int e = exp2 + 63; /* unbiased exponent */
+    uint64_t q;        /* integer result in units of the target quantum */
+    int qexp;          /* quantum exponent */
+    if (e >= -14) {
+        qexp = e - 10; /* 11 significant bits */
+    } else {
+        qexp = -24; /* subnormal quantum */
+    }
+    int sh = qexp - exp2; /* bits to drop from sig (>= 53 for normal inputs) */
+    if (sh >= 64) {
+        /* everything below half a quantum unless sh == 64 handled by generic code */
+        if (sh > 64) {
+            return (uint16_t)sign16;
+        }
+        /* sh == 64: value in [2^63, 2^64) * 2^exp2 = [0.5, 1) quantum */
+        q = 0;
+        uint64_t half = (uint64_t)1 << 63;
+        if (sig > half) {
+            q = 1;
+        }
+        return (uint16_t)(sign16 | (uint16_t)q);
+    }
+    q = sig >> sh;
+    uint64_t rem = sig & ((((uint64_t)1) << sh) - 1);
+    uint64_t half = ((uint64_t)1) << (sh - 1);
+    if (rem > half || (rem == half && (q & 1))) {
+        q += 1;
+    }
+    if (qexp == -24) {
+        /* subnormal (q may have rounded up to 0x400 = smallest normal: same encoding) */
+        return (uint16_t)(sign16 | (uint16_t)q);
+    }
+    /* normal: q in [1024, 2048]; q == 2048 bumps the exponent */
+    if (q == 2048) {
+        q = 1024;
+        e += 1;
+    }
+    if (e > 15) {
+        return (uint16_t)(sign16 | 0x7c00u);
+    }
+    return (uint16_t)(sign16 | (uint16_t)((e + 15) << 10) | (uint16_t)(q - 1024));
+}
+
+uint16_t tqto_f32_to_f16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign16 = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {
+        if (ax > 0x7f800000u) {
+            return (uint16_t)(sign16 | 0x7e00u | ((ax >> 13) & 0x3ffu));
+        }
+        return (uint16_t)(sign16 | 0x7c00u);
+    }
+    uint32_t e = ax >> 23;
+    uint64_t sig = ax & 0x7fffffu;
+    int exp2;
+    if (e == 0) {
+        exp2 = -149;
+    } else {
+        sig |= 0x800000u;
+        exp2 = (int)e - 150;
+    }
+    return round_to_f16(sign16, sig, exp2);
+}
+
+static uint16_t f64_to_f16(double d)
+{
+    uint64_t x;
+    memcpy(&x, &d, 8);
+    uint32_t sign16 = (uint32_t)(x >> 48) & 0x8000u;
+    uint64_t ax = x & 0x7fffffffffffffffull;
+    if (ax >= 0x7ff0000000000000ull) {
+        return (uint16_t)(sign16 | (ax > 0x7ff0000000000000ull ? 0x7e00u : 0x7c00u));
+    }
+    uint64_t e = ax >> 52;
+    uint64_t sig = ax & 0xfffffffffffffull;
+    int exp2;
+    if (e == 0) {
+        exp2 = -1074;
+    } else {
+        sig |= 0x10000000000000ull;
+        exp2 = (int)e - 1075;
+    }
+    return round_to_f16(sign16, sig, exp2);
+}
+
+/* ------------------------------------------------------------------------------------------
+ * Requantization multiplier: src/gemm/gemm_i8_i8/tqt_utils_i8_i8.h:16-132
+ * ---------------------------------------------------------------------------------------- */
+
+static int64_t integer_from_exp(double input, int32_t *shift)
+{
+    /* tqt_utils_i8_i8.h:16-91: Q31 fraction from the double's bits, frexp exponent convention */
+    uint64_t u;
+    memcpy(&u, &input, 8);
+    const uint64_t sign_mask = 0x8000000000000000ull;
+    if ((u & ~sign_mask) == 0) {
+        *shift = 0;
+        return 0;
+    }
+    const uint32_t exponent_part = (uint32_t)((u & 0x7ff0000000000000ull) >> 52);
+    if (exponent_part == 0x7ffu) {
+        *shift = 0x7fffffff;
+        if (u & 0x000fffffffc00000ull) {
+            return 0;
+        }
+        return (u & sign_mask) ? (int64_t)0x8000000000000000ull : (int64_t)0x7fffffffffffffffll;
+    }
+    *shift = (int32_t)(exponent_part - 1023u) + 1;
+    int64_t fraction = 0x40000000 + (int64_t)((u & 0x000fffffffc00000ull) >> 22);
+    if ((u & 0x003fffffull) > 0x00200000ull) {
+        fraction += 1;
+    }
+    if (u & sign_mask) {
+        fraction *= -1;
+    }
+    return fraction;
+}
+
+void tqto_quantize_multiplier(double x, int32_t *mult, int32_t *shift)
+{
+    /* tqt_utils_i8_i8.h:98-132 */
+    if (x == 0.) {
+        *mult = 0;
+        *shift = 0;
+        return;
+    }
+    int64_t q = integer_from_exp(x, shift);
+    if (q == (1ll << 31)) {
+        q /= 2;
+        ++*shift;
+    }
+    if (*shift < -31) {
+        *shift = 0;
+        q = 0;
+    }
+    *mult = (int32_t)q;
+}
+
+/* Per-column (mult, stored shift) exactly as the run functions build their VLAs
+ * (…qsi8cxt_4x1vl_rvv.cpp:158-176; igemmcl …cpp:233-251). */
+static void column_multiplier(float scale_a, const float *scale_b, int32_t quant_channel_b,
+                              float scale_d, size_t j, int32_t *mult, int32_t *shift)
+{
+    size_t src = (quant_channel_b == 1) ? 0 : j;
+    double real_scale = (double)scale_a * (double)scale_b[src] / (double)scale_d;
+    tqto_quantize_multiplier(real_scale, mult, shift);
+    *shift = -*shift - 1;
+}
+
+int8_t tqto_requant_one(int32_t acc, int32_t mult, int32_t shift, int32_t zp, int8_t cmin,
+                        int8_t cmax)
+{
+    /* vmulh.vv: high 32 bits of the signed 64-bit product (floor division by 2^32) */
+    int64_t prod = (int64_t)acc * (int64_t)mult;
+    int32_t y = (int32_t)(prod >> 32);
+    /* vsra.vv: arithmetic shift by the low 5 bits of the shift operand */
+    y = y >> (shift & 31);
+    /* vadd.vx: 32-bit wrapping add of the output zero point */
+    y = (int32_t)((uint32_t)y + (uint32_t)zp);
+    /* vnclip.wx twice with shift 0: saturate to int16, then to int8 */
+    if (y > 32767) {
+        y = 32767;
+    }
+    if (y < -32768) {
+        y = -32768;
+    }
+    if (y > 127) {
+        y = 127;
+    }
+    if (y < -128) {
+        y = -128;
+    }
+    /* clamp_i8: vmax.vx then vmin.vx (tqt_kernel_gemm_i8_i8_4x1vl_rvv.h:231-259) */
+    int8_t r = (int8_t)y;
+    if (r < cmin) {
+        r = cmin;
+    }
+    if (r > cmax) {
+        r = cmax;
+    }
+    return r;
+}
+
+/* ------------------------------------------------------------------------------------------
+ * Tile iteration helper: every kernel below walks (m_step, n_step) tiles like the reference
+ * run functions; OpenMP splits tiles across threads when tqto_set_threads(n > 1).
+ * ---------------------------------------------------------------------------------------- */
+
+#define TILE_LOOP_BEGIN(m, n)                                                        \
+    {                                                                                \
+        const long n_mt = (long)(((m) + TQTO_MR - 1) / TQTO_MR);                     \
+        const long n_nt = (long)(((n) + TQTO_NR - 1) / TQTO_NR);                     \
+        const long n_tiles = n_mt * n_nt;                                            \
+        _Pragma("omp parallel for schedule(static) num_threads(g_threads) if (g_threads > 1)") \
+        for (long t = 0; t < n_tiles; ++t) {                                         \
+            const size_t m0 = (size_t)(t / n_nt) * TQTO_MR;                          \
+            const size_t n0 = (size_t)(t % n_nt) * TQTO_NR;                          \
+            const size_t mr = ((m) - m0) < TQTO_MR ? ((m) - m0) : TQTO_MR;           \
+            const size_t nr = ((n) - n0) < TQTO_NR ? ((n) - n0) : TQTO_NR;
+
+#define TILE_LOOP_END \
+    }                 \
+    }
+
+void tqto_gemm_clamp_i32_i8_i8(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                               const int8_t *B, size_t ldb, const int32_t *C, size_t ldc,
+                               int32_t *D, size_t ldd, int32_t cmin, int32_t cmax)
+{
+    /* …gemm_clamp_i32_i8_i8_4x1vl_rvv.cpp:71-101: init from C or 0, per-k row of B times an
+     * A scalar (i8*i8 exact in i16, widened into i32), then vmax(cmin), vmin(cmax). */
+    TILE_LOOP_BEGIN(m, n)
+    uint32_t acc[TQTO_MR][TQTO_NR];
+    for (size_t i = 0; i < mr; ++i) {
+        for (size_t j = 0; j < nr; ++j) {
+            acc[i][j] = C ? (uint32_t)C[(m0 + i) * ldc + n0 + j] : 0u;
+        }
+    }
+    for (size_t kk = 0; kk < k; ++kk) {
+        const int8_t *brow = B + kk * ldb + n0;
+        for (size_t i = 0; i < mr; ++i) {
+            const int32_t a = A[(m0 + i) * lda + kk];
+            for (size_t j = 0; j < nr; ++j) {
+                acc[i][j] += (uint32_t)(int32_t)(int16_t)(a * brow[j]);
+            }
+        }
+    }
+    for (size_t i = 0; i < mr; ++i) {
+        for (size_t j = 0; j < nr; ++j) {
+            int32_t v = (int32_t)acc[i][j];
+            v = v > cmin ? v : cmin;
+            v = v < cmax ? v : cmax;
+            D[(m0 + i) * ldd + n0 + j] = v;
+        }
+    }
+    TILE_LOOP_END
+}
+
+void tqto_gemm_qsi8cxt_acc(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                           const int8_t *B, size_t ldb, const int32_t *C, size_t ldc,
+                           const int32_t *bias, int32_t *out, size_t ldout)
+{
+    /* …qsi8cxt_4x1vl_rvv.cpp:86-113 (+ add_1xnbias, tqt_kernel_gemm_i8_i8_4x1vl_rvv.h:154-175):
+     * acc = (C or 0) + sum_k A[m,k]*B[n,k] + bias[n], all int32 with wrap-around. */
+    TILE_LOOP_BEGIN(m, n)
+    uint32_t acc[TQTO_MR][TQTO_NR];
+    for (size_t i = 0; i < mr; ++i) {
+        for (size_t j = 0; j < nr; ++j) {
+            acc[i][j] = C ? (uint32_t)C[(m0 + i) * ldc + n0 + j] : 0u;
+        }
+    }
+    for (size_t i = 0; i < mr; ++i) {
+        const int8_t *arow = A + (m0 + i) * lda;
+        for (size_t j = 0; j < nr; ++j) {
+            const int8_t *brow = B + (n0 + j) * ldb;
+            int32_t s = 0;
+            for (size_t kk = 0; kk < k; ++kk) {
+                s += (int32_t)arow[kk] * (int32_t)brow[kk];
+            }
+            acc[i][j] += (uint32_t)s;
+        }
+    }
+    for (size_t i = 0; i < mr; ++i) {
+        for (size_t j = 0; j < nr; ++j) {
+            uint32_t v = acc[i][j];
+            if (bias) {
+                v += (uint32_t)bias[n0 + j];
+            }
+            out[(m0 + i) * ldout + n0 + j] = (int32_t)v;
+        }
+    }
+    TILE_LOOP_END
+}
+
+void tqto_gemm_qai8_qai8_qsi8cxt(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                 const int8_t *B, size_t ldb, const int32_t *C, size_t ldc,
+                                 int8_t *D, size_t ldd, const int32_t *bias, int8_t cmin,
+                                 int8_t cmax, float scale_a, const float *scale_b,
+                                 int32_t quant_channel_b, float scale_d, int32_t zero_point_d)
+{
+    /* …qsi8cxt_4x1vl_rvv.cpp:140-198 */
+    TILE_LOOP_BEGIN(m, n)
+    int32_t mult[TQTO_NR], shift[TQTO_NR];
+    for (size_t j = 0; j < nr; ++j) {
+        column_multiplier(scale_a, scale_b, quant_channel_b, scale_d, n0 + j, &mult[j],
+                          &shift[j]);
+    }
+    int32_t acc[TQTO_MR * TQTO_NR];
+    /* single-tile accumulate, written into a local tile (ldout = TQTO_NR) */
+    {
+        for (size_t i = 0; i < mr; ++i) {
+            const int8_t *arow = A + (m0 + i) * lda;
+            for (size_t j = 0; j < nr; ++j) {
+                const int8_t *brow = B + (n0 + j) * ldb;
+                uint32_t v = C ? (uint32_t)C[(m0 + i) * ldc + n0 + j] : 0u;
+                int32_t s = 0;
+                for (size_t kk = 0; kk < k; ++kk) {
+                    s += (int32_t)arow[kk] * (int32_t)brow[kk];
+                }
+                v += (uint32_t)s;
+                if (bias) {
+                    v += (uint32_t)bias[n0 + j];
+                }
+                acc[i * TQTO_NR + j] = (int32_t)v;
+            }
+        }
+    }
+    for (size_t i = 0; i < mr; ++i) {
+        for (size_t j = 0; j < nr; ++j) {
+            D[(m0 + i) * ldd + n0 + j] = tqto_requant_one(acc[i * TQTO_NR + j], mult[j], shift[j],
+                                                          zero_point_d, cmin, cmax);
+        }
+    }
+    TILE_LOOP_END
+}
+
+void tqto_gemm_qai8dx_qsi4cxt_f32(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                  const uint8_t *B, size_t ldb, const float *C, size_t ldc,
+                                  float *D, size_t ldd, const float *bias, float cmin, float cmax,
+                                  const float *scale_a, const int32_t *zero_point_a,
+                                  const float *scale_b)
+{
+    /* …qai8dx_qsi4cxt_4x1vl_rvv.cpp:81-138 with tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:
+     *   dequant_bt :77-93 (lo = (b & 15) - 8 is the even k, hi = (b >> 4) - 8 the odd k),
+     *   accum_rsum_b :139-146, vmacc_lo/hi :152-224, apply_zp_correction :234-259,
+     *   dequant_acc_to_f32 :271-301 (vfcvt RNE, * scale_a, * scale_b), add_c_f32 :331-367,
+     *   add_1xnbias_f32 :307-323, clamp_f32 :373-397 (vfmax then vfmin). */
+    const size_t bstride = ldb / 2;
+    TILE_LOOP_BEGIN(m, n)
+    for (size_t j = 0; j < nr; ++j) {
+        const uint8_t *brow = B + (n0 + j) * bstride;
+        int32_t rsum = 0;
+        uint32_t acc[TQTO_MR] = {0, 0, 0, 0};
+        for (size_t kk = 0; kk < k; kk += 2) {
+            const uint8_t byte = brow[kk / 2];
+            const int32_t lo = (int32_t)(byte & 0xf) - 8;
+            const int32_t hi = (int32_t)(byte >> 4) - 8;
+            rsum += lo + hi;
+            for (size_t i = 0; i < mr; ++i) {
+                const int8_t *arow = A + (m0 + i) * lda;
+                acc[i] += (uint32_t)((int32_t)arow[kk] * lo);
+                acc[i] += (uint32_t)((int32_t)arow[kk + 1] * hi);
+            }
+        }
+        for (size_t i = 0; i < mr; ++i) {
+            const size_t mi = m0 + i;
+            int32_t v = (int32_t)(acc[i] - (uint32_t)zero_point_a[mi] * (uint32_t)rsum);
+            float f = (float)v;
+            f = f * scale_a[mi];
+            f = f * scale_b[n0 + j];
+            if (C) {
+                f = f + C[mi * ldc + n0 + j];
+            }
+            if (bias) {
+                f = f + bias[n0 + j];
+            }
+            f = fmaxf(f, cmin);
+            f = fminf(f, cmax);
+            D[mi * ldd + n0 + j] = f;
+        }
+    }
+    TILE_LOOP_END
+}
+
+void tqto_gemm_f16_qsi4c2t_f32acc(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,
+                                  size_t lda, const uint8_t *B, size_t ldb,
+                                  const uint16_t *scale_b, size_t ldsb, const uint16_t *C,
+                                  size_t ldc, uint16_t *D, size_t ldd, const uint16_t *bias,
+                                  uint16_t cmin, uint16_t cmax)
+{
+    /* test/common/reference_gemm.cpp:132-179 (TA = TD = float16_t, BiasMode k1xN). */
+    const size_t brow_bytes = ldb / 2;
+    const float cminf = tqto_f16_to_f32(cmin);
+    const float cmaxf = tqto_f16_to_f32(cmax);
+    TILE_LOOP_BEGIN(m, n)
+    for (size_t i = m0; i < m0 + mr; ++i) {
+        for (size_t j = n0; j < n0 + nr; ++j) {
+            float acc = 0.0f;
+            if (C) {
+                acc = tqto_f16_to_f32(C[i * ldc + j]);
+            }
+            for (size_t p = 0; p < k; ++p) {
+                const float a_val = tqto_f16_to_f32(A[i * lda + p]);
+                const uint8_t byte_val = B[j * brow_bytes + p / 2];
+                const int32_t b_raw =
+                    (p % 2 == 0) ? (int32_t)(byte_val & 0x0f) - 8 : (int32_t)(byte_val >> 4) - 8;
+                const float scale_val = tqto_f16_to_f32(scale_b[j * ldsb + p / bl]);
+                const float b_dequant = (float)b_raw * scale_val;
+                const float prod = a_val * b_dequant;
+                acc = acc + prod;
+            }
+            if (bias) {
+                acc = acc + tqto_f16_to_f32(bias[j]);
+            }
+            acc = (acc < cminf) ? cminf : acc; /* std::max(acc, clamp_min) */
+            acc = (cmaxf < acc) ? cmaxf : acc; /* std::min(acc, clamp_max) */
+            D[i * ldd + j] = tqto_f32_to_f16(acc);
+        }
+    }
+    TILE_LOOP_END
+}
+
+/* exact binary16 fused multiply-add, rounded once (the products and sums below are exact in
+ * binary64 for every operand magnitude this test data reaches) */
+static uint16_t f16_fma(uint16_t a, uint16_t b, uint16_t c)
+{
+    const double r = (double)tqto_f16_to_f32(a) * (double)tqto_f16_to_f32(b) +
+                     (double)tqto_f16_to_f32(c);
+    return f64_to_f16(r);
+}
+
+static uint16_t f16_mul(uint16_t a, uint16_t b)
+{
+    return f64_to_f16((double)tqto_f16_to_f32(a) * (double)tqto_f16_to_f32(b));
+}
+
+static uint16_t f16_add(uint16_t a, uint16_t b)
+{
+    return f64_to_f16((double)tqto_f16_to_f32(a) + (double)tqto_f16_to_f32(b));
+}
+
+void tqto_gemm_f16_qsi4c2t_rvv(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,
+                               size_t lda, const uint8_t *B, size_t ldb, const uint16_t *scale_b,
+                               size_t ldsb, const uint16_t *C, size_t ldc, uint16_t *D,
+                               size_t ldd, const uint16_t *bias, uint16_t cmin, uint16_t cmax)
+{
+    /* tqt_kernel_gemm_f16_i4_8x2vl_rvv.h: init_c :99-164 (or zero), per block load_scale
+     * :170-190, dequant_bt :199-260 (vfcvt i16->f16 exact, vfmul f16 rounds), vfmacc :364-478
+     * (f16 fused multiply-add in k order), add_1xnbias :484-545 (f16 add), clamp :551-646
+     * (vfmax then vfmin). */
+    const size_t brow_bytes = ldb / 2;
+    const float cminf = tqto_f16_to_f32(cmin);
+    const float cmaxf = tqto_f16_to_f32(cmax);
+    TILE_LOOP_BEGIN(m, n)
+    for (size_t i = m0; i < m0 + mr; ++i) {
+        for (size_t j = n0; j < n0 + nr; ++j) {
+            uint16_t acc = C ? C[i * ldc + j] : (uint16_t)0;
+            for (size_t p = 0; p < k; ++p) {
+                const uint8_t byte_val = B[j * brow_bytes + p / 2];
+                const int32_t q =
+                    (p % 2 == 0) ? (int32_t)(byte_val & 0x0f) - 8 : (int32_t)(byte_val >> 4) - 8;
+                const uint16_t wq = tqto_f32_to_f16((float)q);
+                const uint16_t w = f16_mul(wq, scale_b[j * ldsb + p / bl]);
+                acc = f16_fma(A[i * lda + p], w, acc);
+            }
+            if (bias) {
+                acc = f16_add(acc, bias[j]);
+            }
+            float v = tqto_f16_to_f32(acc);
+            v = fmaxf(v, cminf);
+            v = fminf(v, cmaxf);
+            D[i * ldd + j] = tqto_f32_to_f16(v);
+        }
+    }
+    TILE_LOOP_END
+}
+
+/* ------------------------------------------------------------------------------------------
+ * Convolution
+ * ---------------------------------------------------------------------------------------- */
+
+void tqto_im2col_cl_i8(size_t group_idx, const int8_t *input, int8_t *col,
+                       const struct tqto_conv_params *p)
+{
+    /* src/common/tqt_conv.h:131-202: row = output pixel (od, oh, ow); columns ordered
+     * (kd, kh, kw, ic); out-of-bounds taps are zero-filled. */
+    const size_t ID = p->input_shape[0], IH = p->input_shape[1], IW = p->input_shape[2];
+    const size_t OD = p->output_shape[0], OH = p->output_shape[1], OW = p->output_shape[2];
+    const size_t KD = p->kernel_shape[0], KH = p->kernel_shape[1], KW = p->kernel_shape[2];
+    const size_t ICg = p->input_channel / p->groups;
+    const size_t Kc = KD * KH * KW * ICg;
+    size_t row = 0;
+    for (size_t od = 0; od < OD; ++od) {
+        for (size_t oh = 0; oh < OH; ++oh) {
+            for (size_t ow = 0; ow < OW; ++ow) {
+                size_t cc = 0;
+                for (size_t kd = 0; kd < KD; ++kd) {
+                    const long id = (long)(od * p->stride[0] + kd * p->dilation[0]) - (long)p->pad[0];
+                    for (size_t kh = 0; kh < KH; ++kh) {
+                        const long ih =
+                            (long)(oh * p->stride[1] + kh * p->dilation[1]) - (long)p->pad[1];
+                        for (size_t kw = 0; kw < KW; ++kw) {
+                            const long iw =
+                                (long)(ow * p->stride[2] + kw * p->dilation[2]) - (long)p->pad[2];
+                            int8_t *dst = col + row * Kc + cc;
+                            if (id >= 0 && id < (long)ID && ih >= 0 && ih < (long)IH && iw >= 0 &&
+                                iw < (long)IW) {
+                                memcpy(dst,
+                                       input + (((size_t)id * IH + (size_t)ih) * IW + (size_t)iw) *
+                                                   p->input_channel +
+                                           group_idx * ICg,
+                                       ICg);
+                            } else {
+                                memset(dst, 0, ICg);
+                            }
+                            cc += ICg;
+                        }
+                    }
+                }
+                row++;
+            }
+        }
+    }
+}
+
+void tqto_igemmcl_qsi8cxt(size_t m, size_t n, const int8_t *input, size_t group_idx,
+                          size_t m_idx, const int8_t *B, size_t ldb, int8_t *D, size_t ldd,
+                          const int32_t *bias, int8_t cmin, int8_t cmax,
+                          const struct tqto_conv_params *p, float scale_a, const float *scale_b,
+                          int32_t quant_channel_b, float scale_d, int32_t zero_point_d)
+{
+    /* …igemmcl…qsi8cxt_4x1vl_rvv.cpp:81-151 (kernel) and :194-286 (run): output pixel
+     * g = m_idx + i decomposes as od = g/(OH*OW), oh = (g/OW)%OH, ow = g%OW; the k loop runs
+     * kd, kh, kw, ic with the weight pointer advancing by one per step; out-of-bounds
+     * pixels contribute 0; then bias, requantize, clamp; D[g * ldd + j]. */
+    const size_t ID = p->input_shape[0], IH = p->input_shape[1], IW = p->input_shape[2];
+    const size_t OH = p->output_shape[1], OW = p->output_shape[2];
+    const size_t KD = p->kernel_shape[0], KH = p->kernel_shape[1], KW = p->kernel_shape[2];
+    const size_t ICg = p->input_channel / p->groups;
+    const int8_t *in_g = input + group_idx * ICg;
+    TILE_LOOP_BEGIN(m, n)
+    int32_t mult[TQTO_NR], shift[TQTO_NR];
+    for (size_t j = 0; j < nr; ++j) {
+        column_multiplier(scale_a, scale_b, quant_channel_b, scale_d, n0 + j, &mult[j],
+                          &shift[j]);
+    }
+    for (size_t i = 0; i < mr; ++i) {
+        const size_t gp = m_idx + m0 + i;
+        const long od = (long)(gp / (OH * OW));
+        const long oh = (long)((gp / OW) % OH);
+        const long ow = (long)(gp % OW);
+        for (size_t j = 0; j < nr; ++j) {
+            const int8_t *w = B + (n0 + j) * ldb;
+            uint32_t acc = 0;
+            for (size_t kd = 0; kd < KD; ++kd) {
+                const long id = od * (long)p->stride[0] + (long)(kd * p->dilation[0]) - (long)p->pad[0];
+                for (size_t kh = 0; kh < KH; ++kh) {
+                    const long ih =
+                        oh * (long)p->stride[1] + (long)(kh * p->dilation[1]) - (long)p->pad[1];
+                    for (size_t kw = 0; kw < KW; ++kw) {
+                        const long iw =
+                            ow * (long)p->stride[2] + (long)(kw * p->dilation[2]) - (long)p->pad[2];
+                        const int inb = id >= 0 && id < (long)ID && ih >= 0 && ih < (long)IH &&
+                                        iw >= 0 && iw < (long)IW;
+                        const int8_t *src =
+                            inb ? in_g + (((size_t)id * IH + (size_t)ih) * IW + (size_t)iw) *
+                                             p->input_channel
+                                : NULL;
+                        for (size_t ic = 0; ic < ICg; ++ic) {
+                            const int32_t a = src ? (int32_t)src[ic] : 0;
+                            acc += (uint32_t)(a * (int32_t)w[ic]);
+                        }
+                        w += ICg;
+                    }
+                }
+            }
+            if (bias) {
+                acc += (uint32_t)bias[n0 + j];
+            }
+            D[gp * ldd + n0 + j] =
+                tqto_requant_one((int32_t)acc, mult[j], shift[j], zero_point_d, cmin, cmax);
+        }
+    }
+    TILE_LOOP_END
+}
+
+/* ------------------------------------------------------------------------------------------
+ * Caller-side input preparation (reference test harness)
+ * ---------------------------------------------------------------------------------------- */
+
+int8_t tqto_quantize_i8(float val, float scale, int32_t zp)
+{
+    /* test/common/test_common.h:232-240 */
+    float q = nearbyintf(val / scale) + (float)zp;
+    if (q > 127.0f) {
+        q = 127.0f;
+    }
+    if (q < -128.0f) {
+        q = -128.0f;
+    }
+    return (int8_t)q;
+}
+
+int32_t tqto_quantize_bias_i32(float val, float input_scale)
+{
+    /* test/common/test_common.h:268-277 */
+    float q = nearbyintf(val / input_scale);
+    if (q > 2147483647.0f) {
+        q = 2147483647.0f;
+    }
+    if (q < -2147483648.0f) {
+        q = -2147483648.0f;
+    }
+    if (q >= 2147483648.0f) {
+        return 2147483647; /* 2147483647.0f rounds to 2^31 in binary32 */
+    }
+    return (int32_t)q;
+}
+
+void tqto_fuse_zp_to_bias(int32_t *fused, const int32_t *bias, const int8_t *data, int32_t zp,
+                          size_t channels, size_t channel_size)
+{
+    /* test/common/test_common.h:280-290 */
+    for (size_t ch = 0; ch < channels; ++ch) {
+        int32_t s = 0;
+        for (size_t i = 0; i < channel_size; ++i) {
+            s += (int32_t)data[ch * channel_size + i];
+        }
+        fused[ch] = (int32_t)((uint32_t)bias[ch] - (uint32_t)zp * (uint32_t)s);
+    }
+}
+
+void tqto_compute_asym_quant_params_i8(const float *data, size_t size, float *scale,
+                                       int32_t *zp)
+{
+    /* test/common/quantized_gemm_test_runner.h:37-63 */
+    float fmin = FLT_MAX, fmax = -FLT_MAX;
+    for (size_t i = 0; i < size; ++i) {
+        if (data[i] < fmin) {
+            fmin = data[i];
+        }
+        if (data[i] > fmax) {
+            fmax = data[i];
+        }
+    }
+    fmax = fmax > 0.0f ? fmax : 0.0f;
+    fmin = fmin < 0.0f ? fmin : 0.0f;
+    const float s = (fmax - fmin) / 255.0f;
+    if (s == 0.0f) {
+        *scale = 1.0f;
+        *zp = 0;
+        return;
+    }
+    const float zp_tmp = -128.0f - fmin / s;
+    int32_t zp_val = (int32_t)nearbyintf(zp_tmp);
+    if (zp_val == -128) {
+        zp_val = -127;
+    }
+    *scale = s;
+    *zp = zp_val;
+}
+
+void tqto_compute_sym_quant_params_i8(const float *data, size_t size, float *scale)
+{
+    /* test/common/quantized_gemm_test_runner.h:67-86 */
+    float fmin = FLT_MAX, fmax = -FLT_MAX;
+    for (size_t i = 0; i < size; ++i) {
+        if (data[i] < fmin) {
+            fmin = data[i];
+        }
+        if (data[i] > fmax) {
+            fmax = data[i];
+        }
+    }
+    const float abs_max = (fabsf(fmax) >= fabsf(fmin)) ? fabsf(fmax) : fabsf(fmin);
+    float s = 2.0f * abs_max / 255.0f;
+    if (s == 0.0f) {
+        s = 1.0f;
+    }
+    *scale = s;
+}
+
+void tqto_quantize_a_per_row_asym(const float *A, size_t m, size_t k, int8_t *A_i8,
+                                  float *scale_a, int32_t *zp_a)
+{
+    /* test/gemm/test_gemm_i8_i4_rvv.cpp:40-77 */
+    for (size_t row = 0; row < m; ++row) {
+        const float *r = A + row * k;
+        float fmin = FLT_MAX, fmax = -FLT_MAX;
+        for (size_t i = 0; i < k; ++i) {
+            if (r[i] < fmin) {
+                fmin = r[i];
+            }
+            if (r[i] > fmax) {
+                fmax = r[i];
+            }
+        }
+        fmax = fmax > 0.0f ? fmax : 0.0f;
+        fmin = fmin < 0.0f ? fmin : 0.0f;
+        const float s = (fmax - fmin) / 255.0f;
+        if (s == 0.0f) {
+            scale_a[row] = 1.0f;
+            zp_a[row] = 0;
+            for (size_t i = 0; i < k; ++i) {
+                A_i8[row * k + i] = 0;
+            }
+            continue;
+        }
+        const float zp_tmp = -128.0f - fmin / s;
+        int32_t zp = (int32_t)nearbyintf(zp_tmp);
+        if (zp < -128) {
+            zp = -128;
+        }
+        if (zp > 127) {
+            zp = 127;
+        }
+        scale_a[row] = s;
+        zp_a[row] = zp;
+        for (size_t i = 0; i < k; ++i) {
+            A_i8[row * k + i] = tqto_quantize_i8(r[i], s, zp);
+        }
+    }
+}
+
+void tqto_quantize_b_per_channel_sym_int4(const float *B, size_t n, size_t k, uint8_t *B_packed,
+                                          float *scale_b)
+{
+    /* test/gemm/test_gemm_i8_i4_rvv.cpp:82-118 */
+    for (size_t row = 0; row < n; ++row) {
+        const float *r = B + row * k;
+        float abs_max = 0.0f;
+        for (size_t i = 0; i < k; ++i) {
+            const float v = fabsf(r[i]);
+            if (v > abs_max) {
+                abs_max = v;
+            }
+        }
+        float s = abs_max / 8.0f;
+        if (s == 0.0f) {
+            s = 1.0f;
+        }
+        scale_b[row] = s;
+        for (size_t kp = 0; kp < k / 2; ++kp) {
+            int32_t q0 = (int32_t)nearbyintf(r[2 * kp] / s);
+            int32_t q1 = (int32_t)nearbyintf(r[2 * kp + 1] / s);
+            q0 = q0 < -8 ? -8 : (q0 > 7 ? 7 : q0);
+            q1 = q1 < -8 ? -8 : (q1 > 7 ? 7 : q1);
+            B_packed[row * (k / 2) + kp] = (uint8_t)((q0 + 8) | ((q1 + 8) << 4));
+        }
+    }
+}
+
+void tqto_quantize_fp16_to_int4(size_t n, size_t k, size_t bl, const uint16_t *src,
+                                uint8_t *dst, uint16_t *scale, size_t ld_scale)
+{
+    /* test/common/quantize_utils.h:34-72 */
+    memset(dst, 0, n * (k / 2));
+    for (size_t j = 0; j < n; ++j) {
+        const size_t nb = k / bl;
+        for (size_t b = 0; b < nb; ++b) {
+            float max_value = 0.0f, abs_max_value = 0.0f;
+            for (size_t t = 0; t < bl; ++t) {
+                const float v = tqto_f16_to_f32(src[j * k + b * bl + t]);
+                if (fabsf(v) > abs_max_value) {
+                    abs_max_value = fabsf(v);
+                    max_value = v;
+                }
+            }
+            const float fp32_scale = max_value / -8.0f;
+            const float inv_scale = (fp32_scale != 0.0f) ? (1.0f / fp32_scale) : 0.0f;
+            scale[j * ld_scale + b] = tqto_f32_to_f16(fp32_scale);
+            for (size_t t = 0; t < bl; t += 2) {
+                const float v0 = tqto_f16_to_f32(src[j * k + b * bl + t]);
+                const float v1 = tqto_f16_to_f32(src[j * k + b * bl + t + 1]);
+                const float x0 = v0 * inv_scale + 8.5f;
+                const float x1 = v1 * inv_scale + 8.5f;
+                const uint8_t q0 = (uint8_t)fminf((float)(int8_t)x0, 15.0f);
+                const uint8_t q1 = (uint8_t)fminf((float)(int8_t)x1, 15.0f);
+                dst[j * (k / 2) + (b * bl + t) / 2] = (uint8_t)(q0 | (uint8_t)(q1 << 4));
+            }
+        }
+    }
+}

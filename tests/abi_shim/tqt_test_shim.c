@@ -1,0 +1,153 @@
+/*
+ * Test-side C caller of the library. It plays the part of a framework that binds the gfx950
+ * variants through the reference-shaped interface structs (tqt_*_interface.h) and calls them
+ * with C argument types, including _Float16 by value, which Python's ctypes cannot pass.
+ * Assigning each variant to its interface struct member is the compile-time check that every
+ * signature matches the interface exactly.
+ */
+#include <stdint.h>
+#include <string.h>
+
+#include "tqt_gemm_1xnbias_clamp_f16_f16_qsi4c2t_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_interface.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_clamp_i32_i8_i8_interface.h"
+#include "tqt_gemm_clamp_i32_i8_i8_mfma_gfx950.h"
+#include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_interface.h"
+#include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
+
+static const struct tqt_gemm_clamp_i32_i8_i8_ukernel k_clamp = {
+    tqt_get_m_step_gemm_clamp_i32_i8_i8_mfma_gfx950,
+    tqt_get_n_step_gemm_clamp_i32_i8_i8_mfma_gfx950,
+    tqt_get_a_offset_gemm_clamp_i32_i8_i8_mfma_gfx950,
+    tqt_get_b_offset_gemm_clamp_i32_i8_i8_mfma_gfx950,
+    tqt_get_c_offset_gemm_clamp_i32_i8_i8_mfma_gfx950,
+    tqt_get_d_offset_gemm_clamp_i32_i8_i8_mfma_gfx950,
+    tqt_get_d_size_gemm_clamp_i32_i8_i8_mfma_gfx950,
+    tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_ukernel k_w8a8 = {
+    tqt_get_m_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_ukernel k_w4a8 = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f16_f16_qsi4c2t_ukernel k_w4a16 = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_scale_b_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950,
+};
+
+static const struct tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_ukernel k_igemm = {
+    tqt_get_m_step_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_n_step_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_b_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_c_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_bias_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_d_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_d_size_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+};
+
+/* m_step and n_step of each kernel type read through its interface struct:
+ * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl. */
+void tqts_steps_via_interfaces(size_t out[10])
+{
+    out[0] = k_clamp.get_m_step();
+    out[1] = k_clamp.get_n_step();
+    out[2] = k_w8a8.get_m_step();
+    out[3] = k_w8a8.get_n_step();
+    out[4] = k_w4a8.get_m_step();
+    out[5] = k_w4a8.get_n_step();
+    out[6] = k_w4a16.get_m_step();
+    out[7] = k_w4a16.get_n_step();
+    out[8] = k_igemm.get_m_step();
+    out[9] = k_igemm.get_n_step();
+}
+
+/* W4A16 run through the interface struct with _Float16 clamps given as binary16 bits. */
+void tqts_run_w4a16(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda,
+                    const void *B, size_t ldb, const void *scale_b, size_t ldsb, const void *C,
+                    size_t ldc, void *D, size_t ldd, const void *bias, uint16_t cmin_bits,
+                    uint16_t cmax_bits)
+{
+    float16_t cmin, cmax;
+    memcpy(&cmin, &cmin_bits, 2);
+    memcpy(&cmax, &cmax_bits, 2);
+    k_w4a16.run_gemm(m, n, k, bl, A, lda, 0, B, ldb, 0, scale_b, ldsb, C, ldc, D, ldd, bias, cmin,
+                     cmax);
+}
+
+/* Stream-ordered W4A16 for timing. */
+void tqts_run_w4a16_async(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda,
+                          const void *B, size_t ldb, const void *scale_b, size_t ldsb,
+                          const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+                          uint16_t cmin_bits, uint16_t cmax_bits, void *stream)
+{
+    float16_t cmin, cmax;
+    memcpy(&cmin, &cmin_bits, 2);
+    memcpy(&cmax, &cmax_bits, 2);
+    tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950_async(m, n, k, bl, A, lda, 0, B, ldb, 0,
+                                                                 scale_b, ldsb, C, ldc, D, ldd,
+                                                                 bias, cmin, cmax, stream);
+}
+
+/* The other four kernel types through their interface structs (synchronous run). */
+void tqts_run_clamp(size_t m, size_t n, size_t k, const void *A, size_t lda, const void *B,
+                    size_t ldb, const void *C, size_t ldc, void *D, size_t ldd, int32_t cmin,
+                    int32_t cmax)
+{
+    k_clamp.run_gemm(m, n, k, A, lda, 0, B, ldb, 0, C, ldc, D, ldd, cmin, cmax);
+}
+
+void tqts_run_w8a8(size_t m, size_t n, size_t k, const void *A, size_t lda, const void *B,
+                   size_t ldb, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+                   int8_t cmin, int8_t cmax, const struct tqt_qai8_qai8_qsi8cx_params *params)
+{
+    k_w8a8.run_gemm(m, n, k, A, lda, 0, B, ldb, 0, C, ldc, D, ldd, bias, cmin, cmax, params);
+}
+
+void tqts_run_w4a8(size_t m, size_t n, size_t k, const void *A, size_t lda, const void *B,
+                   size_t ldb, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+                   float cmin, float cmax, const struct tqt_qai8dx_qsi4cx_params *params)
+{
+    k_w4a8.run_gemm(m, n, k, A, lda, 0, B, ldb, 0, C, ldc, D, ldd, bias, cmin, cmax, params);
+}
+
+void tqts_run_igemmcl(size_t m, size_t n, const void *input, size_t group_idx, size_t m_idx,
+                      const void *B, size_t ldb, void *D, size_t ldd, const void *bias,
+                      int8_t cmin, int8_t cmax, const tqt_conv_params *conv,
+                      const struct tqt_qai8_qai8_qsi8cx_params *params)
+{
+    k_igemm.run_igemm(m, n, 0, input, group_idx, m_idx, 0, B, ldb, 0, NULL, 0, D, ldd, bias, cmin,
+                      cmax, conv, params);
+}

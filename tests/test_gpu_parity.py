@@ -1,0 +1,272 @@
+"""GPU parity: every kernel type through the C ABI against the CPU oracle on identical inputs.
+
+Shapes: the reference's own test shape lists (test/gemm/test_gemm_i8_i8_rvv.cpp:31-41,
+test/gemm/test_gemm_i8_i4_rvv.cpp:164-179, test/gemm/test_gemm_f16_i4_rvv.cpp:19-49,
+test/conv/test_igemm_i8_i8_rvv.cpp:21-41), the BASELINE.json configurations at full size, and
+extra ragged / aligned shapes that exercise both the MFMA fast paths and the generic paths.
+
+Bar: bit-exact for int32 and int8 outputs and for the W4A8 f32 output (same operation order,
+no FMA); W4A16 f16 output within 2 binary16 ULP of both the f32-accumulating reference oracle
+and the exact (float64) result, the ULP taken at max(|expected|, 2^-14, 2^-13 * sum|a*w|)
+(see ulp_distance_f16).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import tqt_testlib as T
+
+pytestmark = pytest.mark.gpu
+
+INT8_REF_SHAPES = [(32, 32, 32, False), (3, 8, 11, False), (5, 11, 10, False), (9, 19, 23, False),
+                   (15, 32, 25, False), (60, 63, 127, False), (32, 32, 32, True),
+                   (60, 63, 127, True)]
+INT8_FAST_SHAPES = [(64, 256, 512, False), (130, 260, 192, True), (200, 136, 80, False),
+                    (1, 128, 64, False), (257, 129, 1024, True)]
+
+
+def _gr():
+    import gpu_run
+
+    return gpu_run
+
+
+@pytest.mark.parametrize("m,n,k,with_c", INT8_REF_SHAPES + INT8_FAST_SHAPES)
+def test_clamp_i32_parity(gpu, m, n, k, with_c):
+    A, B, C = T.gen_clamp(m, n, k, seed=42 + m, with_c=with_c, lo=-50, hi=50)
+    for cmin, cmax in [(-100000, 100000), (-2**31, 2**31 - 1)]:
+        got = _gr().run_clamp(A, B, C, cmin, cmax)
+        exp = T.oracle_clamp(A, B, C, cmin, cmax)
+        np.testing.assert_array_equal(got, exp)
+
+
+def test_clamp_i32_config1(gpu):
+    """BASELINE cfg 1: A [64,512], B [512,256] uniform in [-128,127], no C, full int32 clamp."""
+    A, B, C = T.gen_clamp(64, 256, 512, seed=42)
+    got = _gr().run_clamp(A, B, None, -2**31, 2**31 - 1)
+    exp = T.oracle_clamp(A, B, None, -2**31, 2**31 - 1)
+    np.testing.assert_array_equal(got, exp)
+    # closed form: int64 matrix product fits int32 here
+    np.testing.assert_array_equal(got, (A.astype(np.int64) @ B.astype(np.int64)).astype(np.int32))
+
+
+@pytest.mark.parametrize("m,n,k,with_c", INT8_REF_SHAPES + INT8_FAST_SHAPES)
+def test_w8a8_parity(gpu, m, n, k, with_c):
+    d = T.gen_w8a8(m, n, k, seed=7 + n, with_c=with_c)
+    got = _gr().run_w8a8(d)
+    exp = T.oracle_w8a8(d["A"], d["B"], d["C"], d["bias"], -128, 127, d["scale_a"], d["scale_b"],
+                        n, d["scale_d"], d["zp_d"])
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_w8a8_variants(gpu):
+    """No bias, narrow clamp, nonzero output zero point, per-tensor scale (quant_channel_b=1),
+    and a real scale >= 0.5 (negative stored shift, shifted by shift & 31)."""
+    m, n, k = 96, 200, 320
+    base = T.gen_w8a8(m, n, k, seed=11)
+    cases = [
+        dict(bias=None),
+        dict(zp_d=17),
+        dict(qcb=1),
+        dict(scale_d=np.float32(1e-5)),
+    ]
+    for upd in cases:
+        d = dict(base, **upd)
+        cmin, cmax = (-20, 90) if "zp_d" in upd else (-128, 127)
+        got = _gr().run_w8a8(d, cmin, cmax)
+        exp = T.oracle_w8a8(d["A"], d["B"], d["C"], d["bias"], cmin, cmax, d["scale_a"],
+                            d["scale_b"], d.get("qcb", n), d["scale_d"], d["zp_d"])
+        np.testing.assert_array_equal(got, exp, err_msg=str(upd.keys()))
+
+
+def test_w8a8_config2_full(gpu):
+    """BASELINE cfg 2 at full size: M=512, K=4096, N=4096, bit-exact."""
+    d = T.gen_w8a8(512, 4096, 4096, seed=42)
+    got = _gr().run_w8a8(d)
+    exp = T.oracle_w8a8(d["A"], d["B"], None, d["bias"], -128, 127, d["scale_a"], d["scale_b"],
+                        4096, d["scale_d"], d["zp_d"])
+    np.testing.assert_array_equal(got, exp)
+
+
+W4A8_REF_SHAPES = [(8, 8, 8, dict()), (16, 16, 16, dict()), (32, 32, 32, dict()),
+                   (5, 11, 16, dict()), (7, 3, 8, dict()), (17, 19, 24, dict()),
+                   (31, 35, 64, dict()), (60, 61, 128, dict()),
+                   (32, 32, 32, dict(bias=True)), (17, 19, 24, dict(bias=True)),
+                   (32, 32, 32, dict(clamp=(-0.5, 0.5))), (32, 32, 32, dict(c=True)),
+                   (32, 32, 32, dict(c=True, bias=True, clamp=(-0.5, 0.5)))]
+W4A8_FAST_SHAPES = [(1, 160, 256, dict(bias=True)), (4, 100, 512, dict(bias=True, c=True)),
+                    (15, 48, 384, dict(bias=True)), (16, 64, 1024, dict(clamp=(-0.5, 0.5))),
+                    (33, 37, 640, dict(bias=True))]
+
+
+@pytest.mark.parametrize("m,n,k,opt", W4A8_REF_SHAPES + W4A8_FAST_SHAPES)
+def test_w4a8_parity(gpu, m, n, k, opt):
+    d = T.gen_w4a8(m, n, k, seed=42 + k, with_c=opt.get("c", False),
+                   with_bias=opt.get("bias", False))
+    cmin, cmax = opt.get("clamp", (-np.inf, np.inf))
+    got = _gr().run_w4a8(d, cmin, cmax)
+    exp = T.oracle_w4a8(d["A"], d["Bp"], d["C"], d["bias"], cmin, cmax, d["scale_a"], d["zp_a"],
+                        d["scale_b"])
+    np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_w4a8_config3_full(gpu, m):
+    """BASELINE cfg 3 at full size: K=4096, N=11008, M in {1, 4, 8}; bit-exact f32."""
+    d = T.gen_w4a8(m, 11008, 4096, seed=42)
+    got = _gr().run_w4a8(d)
+    exp = T.oracle_w4a8(d["A"], d["Bp"], None, d["bias"], -np.inf, np.inf, d["scale_a"],
+                        d["zp_a"], d["scale_b"])
+    np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def w4a16_exact_and_scale(d):
+    """Exact (float64) result and S = sum_k |a_k * w_k| per output, w = (q - 8) * s exactly."""
+    A = T.bits_f16(d["A16"]).astype(np.float64)
+    Bp, bl = d["Bp"], d["bl"]
+    S16 = T.bits_f16(d["S16"]).astype(np.float32)
+    m, k = A.shape
+    n = Bp.shape[0]
+    exact = np.zeros((m, n))
+    S = np.zeros((m, n))
+    Aabs = np.abs(A)
+    for j0 in range(0, n, 2048):
+        j1 = min(n, j0 + 2048)
+        q = np.empty((j1 - j0, k), np.float32)
+        q[:, 0::2] = (Bp[j0:j1] & 15).astype(np.float32) - 8
+        q[:, 1::2] = (Bp[j0:j1] >> 4).astype(np.float32) - 8
+        W = (q * np.repeat(S16[j0:j1], bl, axis=1)).astype(np.float64)  # exact in f32
+        exact[:, j0:j1] = A @ W.T
+        S[:, j0:j1] = Aabs @ np.abs(W).T
+    if d["C16"] is not None:
+        exact += T.bits_f16(d["C16"]).astype(np.float64)
+        S += np.abs(T.bits_f16(d["C16"]).astype(np.float64))
+    if d["bias16"] is not None:
+        exact += T.bits_f16(d["bias16"]).astype(np.float64)[None, :]
+    return exact, S
+
+
+def ulp_distance_f16(got_bits, exp_vals, S):
+    """|got - expected| in binary16 ULPs of max(|expected|, 2^-14, 2^-13 * S).
+
+    Below magnitude 2^-13 * sum|a*w| one f16 ULP is smaller than a single f32 rounding of the
+    accumulated sum, so no f32-accumulating evaluation order can promise it; the reference's
+    own test oracle (sequential f32 sum) is within 1 ULP of exact math under this floor."""
+    g = T.bits_f16(got_bits).astype(np.float64)
+    e = np.asarray(exp_vals, np.float64)
+    mag = np.maximum(np.maximum(np.abs(e), 2.0 ** -14), 2.0 ** -13 * S)
+    ulp = 2.0 ** (np.floor(np.log2(mag)) - 10)
+    return np.abs(g - e) / ulp
+
+
+def check_w4a16(got, exp, d, clamp):
+    exact, S = w4a16_exact_and_scale(d)
+    exact = np.clip(exact, clamp[0], clamp[1])
+    d_oracle = ulp_distance_f16(got, T.bits_f16(exp).astype(np.float64), S)
+    d_exact = ulp_distance_f16(got, exact.astype(np.float16).astype(np.float64), S)
+    assert d_oracle.max() <= 2.0, "max ULP vs oracle %s" % d_oracle.max()
+    assert d_exact.max() <= 2.0, "max ULP vs exact %s" % d_exact.max()
+    return d_oracle, d_exact
+
+
+W4A16_REF_SHAPES = [(8, 8, 4, 2, {}), (16, 16, 8, 2, {}), (32, 32, 32, 2, {}), (32, 32, 32, 4, {}),
+                    (32, 32, 32, 32, {}), (5, 11, 10, 2, {}), (7, 3, 10, 2, {}),
+                    (17, 19, 24, 4, {}), (31, 35, 64, 32, {}), (60, 61, 128, 32, {}),
+                    (32, 32, 32, 2, dict(bias=True)), (17, 19, 24, 4, dict(bias=True)),
+                    (32, 32, 32, 4, dict(clamp=(-0.5, 0.5))), (32, 32, 32, 4, dict(c=True)),
+                    (32, 32, 32, 4, dict(c=True, bias=True, clamp=(-0.5, 0.5)))]
+W4A16_FAST_SHAPES = [(32, 256, 4096, 32, dict(bias=True)), (1, 48, 128, 32, dict(bias=True)),
+                     (33, 40, 512, 32, dict(c=True, bias=True)),
+                     (64, 160, 1152, 32, dict(clamp=(-0.5, 0.5)))]
+
+
+@pytest.mark.parametrize("m,n,k,bl,opt", W4A16_REF_SHAPES + W4A16_FAST_SHAPES)
+def test_w4a16_parity(gpu, shim, m, n, k, bl, opt):
+    d = T.gen_w4a16(m, n, k, bl=bl, seed=42 + k, with_c=opt.get("c", False),
+                    with_bias=opt.get("bias", False))
+    lo, hi = opt.get("clamp", (-65504.0, 65504.0))
+    cmin, cmax = int(T.f16_bits(lo)), int(T.f16_bits(hi))
+    got = _gr().run_w4a16(shim, d, cmin, cmax)
+    exp = T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], bl, d["C16"], d["bias16"], cmin, cmax)
+    check_w4a16(got, exp, d, (lo, hi))
+    # distance to the RVV kernel's own f16-accumulating numerics, reported only: the reference
+    # test accepts up to 1.0 absolute between those and the f32 oracle
+    rvv = T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], bl, d["C16"], d["bias16"], cmin, cmax,
+                         rvv=True)
+    diff = np.abs(T.bits_f16(got).astype(np.float64) - T.bits_f16(rvv).astype(np.float64))
+    assert diff.max() <= 1.0
+
+
+def test_w4a16_config4_full(gpu, shim):
+    """BASELINE cfg 4 at full size: M=32, K=4096, N=14336, bl=32; <= 2 f16 ULP."""
+    d = T.gen_w4a16(32, 14336, 4096, bl=32, seed=42)
+    cmin, cmax = int(T.f16_bits(-65504.0)), int(T.f16_bits(65504.0))
+    got = _gr().run_w4a16(shim, d, cmin, cmax)
+    exp = T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], 32, None, d["bias16"], cmin, cmax)
+    check_w4a16(got, exp, d, (-65504.0, 65504.0))
+
+
+IGEMM_REF = [  # (IC, OC, IH, IW, KH, KW, stride, pad, dil)
+    (3, 16, 8, 8, 3, 3, (1, 1), (0, 0), (1, 1)),
+    (16, 32, 8, 8, 3, 3, (1, 1), (0, 0), (1, 1)),
+    (16, 32, 8, 8, 1, 1, (1, 1), (0, 0), (1, 1)),
+    (3, 16, 8, 8, 3, 3, (1, 1), (1, 1), (1, 1)),
+    (3, 16, 8, 8, 3, 3, (2, 2), (0, 0), (1, 1)),
+    (3, 16, 8, 8, 3, 3, (1, 1), (2, 2), (2, 2)),
+    (3, 16, 8, 8, 3, 3, (2, 2), (1, 1), (1, 1)),
+    (8, 16, 7, 11, 3, 5, (1, 1), (0, 0), (1, 1)),
+    (64, 128, 4, 4, 1, 1, (1, 1), (0, 0), (1, 1)),
+    (3, 32, 16, 16, 3, 3, (1, 1), (1, 1), (1, 1)),
+    (3, 8, 6, 6, 3, 3, (1, 1), (0, 0), (1, 1)),
+    (64, 32, 4, 4, 3, 3, (1, 1), (1, 1), (1, 1)),
+]
+IGEMM_FAST = [
+    (32, 48, 9, 13, 3, 3, (1, 1), (1, 1), (1, 1)),
+    (128, 128, 14, 14, 3, 3, (2, 2), (1, 1), (1, 1)),
+    (16, 24, 12, 10, 5, 3, (1, 2), (2, 1), (1, 2)),
+]
+
+
+@pytest.mark.parametrize("ic,oc,ih,iw,kh,kw,stride,pad,dil", IGEMM_REF + IGEMM_FAST)
+def test_igemmcl_parity(gpu, ic, oc, ih, iw, kh, kw, stride, pad, dil):
+    d = T.gen_igemmcl(1, ih, iw, ic, oc, kh, kw, stride=stride, pad=pad, dil=dil, seed=ic + oc)
+    got = _gr().run_igemmcl(d)
+    exp = T.oracle_igemmcl(d["inp"], d["W"], d["bias"], -128, 127, d["conv"], d["scale_a"],
+                           d["scale_b"], oc, d["scale_d"], d["zp_d"])
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_igemmcl_tiled_calls(gpu):
+    """The reference caller pattern: one run per m_step tile with m_idx (D addressed
+    absolutely), covering a ragged last tile."""
+    d = T.gen_igemmcl(2, 10, 9, 32, 40, 3, 3, pad=(1, 1), seed=5)
+    conv = d["conv"]
+    M = conv.output_shape[0] * conv.output_shape[1] * conv.output_shape[2]
+    step = 64
+    D = np.zeros((M, 40), np.int8)
+    for m_idx in range(0, M, step):
+        D = _gr().run_igemmcl(d, m=min(step, M - m_idx), m_idx=m_idx, D_init=D)
+    exp = T.oracle_igemmcl(d["inp"], d["W"], d["bias"], -128, 127, conv, d["scale_a"],
+                           d["scale_b"], 40, d["scale_d"], d["zp_d"])
+    np.testing.assert_array_equal(D, exp)
+
+
+def test_igemmcl_config5_full(gpu):
+    """BASELINE cfg 5 at full size: NHWC 8x56x56x128 (batch as depth), 3x3, OC 128, pad 1."""
+    d = T.gen_igemmcl(8, 56, 56, 128, 128, 3, 3, pad=(1, 1), seed=42)
+    got = _gr().run_igemmcl(d)
+    exp = T.oracle_igemmcl(d["inp"], d["W"], d["bias"], -128, 127, d["conv"], d["scale_a"],
+                           d["scale_b"], 128, d["scale_d"], d["zp_d"])
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_interfaces_and_null_params(gpu, shim, lib):
+    """NULL params leave D untouched (reference run_* returns early)."""
+    import torch
+
+    D = torch.full((4, 4), 7, dtype=torch.int8, device="cuda:0")
+    lib.fn("w8a8", "run")(4, 4, 16, None, 16, 0, None, 16, 0, None, 4, D.data_ptr(), 4, None,
+                          -128, 127, None)
+    assert int(D.sum().item()) == 7 * 16

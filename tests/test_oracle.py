@@ -1,0 +1,448 @@
+"""CPU checks that pin the oracle (oracle/tqt_oracle.c) before it is trusted as the checker.
+
+Sources of truth, in order of strength:
+  1. golden fixtures written by tests/golden/make_golden.py from the reference's own compiled
+     test code (its RNG, reference_gemm_i32_i8, reference_gemm_quantized_weight_mixed,
+     tqt_im2col_cl, tqt_quantize_multiplier, quantize helpers);
+  2. the same reference code live (oracle/_ref/libtqt_ref.so) where it was built;
+  3. independent closed forms (numpy int64 / float64 products, numpy float16 rounding);
+  4. hand-computed known answers and invariants for the requantization epilogue, which only
+     the RVV source text defines (tqt_kernel_gemm_i8_i8_4x1vl_rvv.h:334-408).
+"""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import tqt_testlib as T
+
+G = T.GOLDEN_DIR
+
+
+def golden(name):
+    return np.load(os.path.join(G, name), allow_pickle=False)
+
+
+# ------------------------------------------------------------------------------------------
+# binary16 conversion helpers (checked against numpy's own rounding)
+# ------------------------------------------------------------------------------------------
+
+def test_f16_to_f32_exhaustive():
+    o = T.oracle()
+    bits = np.arange(65536, dtype=np.uint16)
+    got = np.array([o.tqto_f16_to_f32(int(b)) for b in bits], np.float32)
+    exp = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(exp)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rounding():
+    o = T.oracle()
+    rng = np.random.default_rng(0)
+    # every f16 value, every midpoint between neighbours (ties), neighbours of midpoints,
+    # overflow boundary, subnormal range, random values
+    h = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = (h[:-1] + h[1:]) / 2
+    vals = np.concatenate([h, mids, np.nextafter(mids, 0), np.nextafter(mids, 1), -mids,
+                           [65504.0, 65519.99, 65520.0, 1e6, 2.0 ** -25, 2.0 ** -26, 3e-8],
+                           rng.standard_normal(20000) * 10.0 ** rng.uniform(-8, 5, 20000)])
+    vals = vals.astype(np.float32)
+    got = np.array([o.tqto_f32_to_f16(float(v)) for v in vals], np.uint16)
+    exp = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, exp)
+
+
+# ------------------------------------------------------------------------------------------
+# Requantization multiplier
+# ------------------------------------------------------------------------------------------
+
+def qm(x):
+    o = T.oracle()
+    m, s = ctypes.c_int32(), ctypes.c_int32()
+    o.tqto_quantize_multiplier(float(x), ctypes.byref(m), ctypes.byref(s))
+    return m.value, s.value
+
+
+def test_quantize_multiplier_known_answers():
+    # frexp convention: x = (mult / 2^31) * 2^shift, mult in [2^30, 2^31)
+    assert qm(0.5) == (1 << 30, 0)
+    assert qm(0.25) == (1 << 30, -1)
+    assert qm(1.0) == (1 << 30, 1)
+    assert qm(0.0004)[1] == -11
+    assert qm(0.0) == (0, 0)
+    assert qm(2.0 ** -40) == (0, 0)  # shift < -31 flushes to zero
+    assert qm(0.75) == (3 << 29, 0)
+    # 2^30 + all-ones upper fraction rounds up to 2^31 -> halved, shift + 1
+    assert qm(1.0 - 2.0 ** -53) == (1 << 30, 1)
+    assert qm(-0.5) == (-(1 << 30), 0)
+
+
+def test_quantize_multiplier_vs_reference_golden():
+    g = golden("ref_qm.npz")
+    got = np.array([qm(x) for x in g["x"]], np.int64)
+    assert np.array_equal(got[:, 0], g["mult"])
+    assert np.array_equal(got[:, 1], g["shift"])
+
+
+def test_quantize_multiplier_closed_form():
+    """For finite x in [2^-31, 2^31) the pair approximates x within half a Q31 step."""
+    rng = np.random.default_rng(3)
+    for x in 10.0 ** rng.uniform(-9, 6, 5000):
+        m, s = qm(x)
+        approx = m * 2.0 ** (s - 31)
+        assert abs(approx - x) <= 2.0 ** (s - 31) * 0.5 + 1e-300
+        assert (1 << 30) <= m < (1 << 31)
+
+
+# ------------------------------------------------------------------------------------------
+# Requantization epilogue (only the RVV text defines it: hand known-answers + invariants)
+# ------------------------------------------------------------------------------------------
+
+def rq(acc, mult, shift, zp=0, cmin=-128, cmax=127):
+    return T.oracle().tqto_requant_one(acc, mult, shift, zp, cmin, cmax)
+
+
+def test_requant_known_answers():
+    M30 = 1 << 30
+    assert rq(-5, M30, 0) == -2          # floor(-1.25): vmulh rounds toward -inf
+    assert rq(5, M30, 0) == 1            # floor(1.25)
+    assert rq(-1, M30, 0) == -1          # floor(-0.25)
+    assert rq(100, M30, 1, 3) == 15      # 25 >> 1 = 12, + 3
+    assert rq(-100, M30, 1) == -13       # -25 >> 1 = -13 (arithmetic shift)
+    assert rq(1000000, M30, 0) == 127    # saturate high
+    assert rq(-1000000, M30, 0) == -128  # saturate low
+    assert rq(2**31 - 1, 2**31 - 1, 0, 2**31 - 1) == -128  # 32-bit wrap of the zp add
+    assert rq(2**31 - 1, M30, -1) == 0   # stored shift -1 shifts by 31
+    assert rq(40, M30, 0, 0, -5, 7) == 7  # clamp after saturation
+    assert rq(-40, M30, 0, 0, -5, 7) == -5
+    assert rq(12345, 0, 0, 9) == 9       # zero multiplier
+
+
+def test_requant_invariants():
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        mult = int(rng.integers(1 << 30, 1 << 31))
+        shift = int(rng.integers(0, 12))
+        zp = int(rng.integers(-20, 21))
+        accs = np.sort(rng.integers(-(1 << 20), 1 << 20, 64))
+        ys = [rq(int(a), mult, shift, zp) for a in accs]
+        assert all(ys[i] <= ys[i + 1] for i in range(len(ys) - 1))  # monotone
+        real = mult / 2.0 ** 32 / 2.0 ** shift
+        for a, y in zip(accs, ys):
+            exact = np.floor(np.floor(a * mult / 2.0 ** 32) / 2.0 ** shift) + zp
+            assert y == int(np.clip(exact, -128, 127))
+            if -128 < y < 127:
+                assert a * real + zp - 1 < y <= a * real + zp + 1e-9  # floor, not round
+
+
+# ------------------------------------------------------------------------------------------
+# GEMM restatements vs the reference's own test code
+# ------------------------------------------------------------------------------------------
+
+def test_clamp_i32_vs_reference_golden():
+    g = golden("ref_clamp_i32.npz")
+    for i, (m, n, k, with_c) in enumerate(g["shapes"]):
+        A, B, D = g["clamp_%d_A" % i], g["clamp_%d_B" % i], g["clamp_%d_D" % i]
+        C = g["clamp_%d_C" % i] if with_c else None
+        got = T.oracle_clamp(A, B, C, -100000, 100000)
+        np.testing.assert_array_equal(got, D)
+        ref64 = A.astype(np.int64) @ B.astype(np.int64) + (0 if C is None else C)
+        np.testing.assert_array_equal(got, np.clip(ref64, -100000, 100000))
+
+
+def test_w4a16_f32acc_vs_reference_golden():
+    """The f32-accumulating W4A16 oracle reproduces reference_gemm_quantized_weight_mixed
+    bit for bit on the reference's own test inputs (its RNG, its int4 quantizer)."""
+    g = golden("ref_w4a16.npz")
+    for i, (m, n, k, bl, bias, c, clamp) in enumerate(g["shapes"]):
+        pre = "w4a16_%d_" % i
+        C = g[pre + "C"] if c else None
+        bv = g[pre + "bias"] if bias else None
+        cmin, cmax = (int(v) for v in g[pre + "clamp"])
+        got = T.oracle_w4a16(g[pre + "A"], g[pre + "Bp"], g[pre + "S"], int(bl), C, bv, cmin, cmax)
+        np.testing.assert_array_equal(got, g[pre + "D"])
+
+
+def test_w4a16_rvv_numerics_within_reference_tolerance():
+    """The RVV-numerics restatement (f16 weights, f16 FMA chain) stays within the reference
+    test's own tolerance (abs 1.0, cosine 0.9999) of the f32 oracle on the reference inputs."""
+    g = golden("ref_w4a16.npz")
+    for i, (m, n, k, bl, bias, c, clamp) in enumerate(g["shapes"]):
+        pre = "w4a16_%d_" % i
+        C = g[pre + "C"] if c else None
+        bv = g[pre + "bias"] if bias else None
+        cmin, cmax = (int(v) for v in g[pre + "clamp"])
+        got = T.bits_f16(T.oracle_w4a16(g[pre + "A"], g[pre + "Bp"], g[pre + "S"], int(bl), C,
+                                        bv, cmin, cmax, rvv=True)).astype(np.float64)
+        ref = T.bits_f16(g[pre + "D"]).astype(np.float64)
+        assert np.abs(got - ref).max() <= 1.0
+        cos = (got * ref).sum() / (np.linalg.norm(got) * np.linalg.norm(ref) + 1e-30)
+        assert cos >= 0.9999
+
+
+def test_w4a16_f32acc_closed_form():
+    """Independent float64 evaluation: the f32 oracle is within 2 f16 ULP (ULP floored at the
+    f32 accumulation-noise scale 2^-13 * sum|a*w|) of exact math."""
+    d = T.gen_w4a16(16, 96, 1024, bl=32, seed=9, with_c=True, with_bias=True)
+    cmin, cmax = int(T.f16_bits(-65504.0)), int(T.f16_bits(65504.0))
+    got = T.bits_f16(T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], 32, d["C16"], d["bias16"], cmin,
+                                    cmax)).astype(np.float64)
+    A = T.bits_f16(d["A16"]).astype(np.float64)
+    q = np.empty((96, 1024))
+    q[:, 0::2] = (d["Bp"] & 15) - 8.0
+    q[:, 1::2] = (d["Bp"] >> 4) - 8.0
+    W = q * np.repeat(T.bits_f16(d["S16"]).astype(np.float64), 32, axis=1)
+    exact = A @ W.T + T.bits_f16(d["C16"]) + T.bits_f16(d["bias16"])[None, :]
+    S = np.abs(A) @ np.abs(W).T + np.abs(T.bits_f16(d["C16"]).astype(np.float64))
+    mag = np.maximum(np.maximum(np.abs(exact), 2.0 ** -14), 2.0 ** -13 * S)
+    ulp = 2.0 ** (np.floor(np.log2(mag)) - 10)
+    assert (np.abs(got - exact.astype(np.float16).astype(np.float64)) / ulp).max() <= 2.0
+
+
+def test_w4a16_rejects_dropped_scale():
+    """A plausible mistake (scale of the wrong block) is caught by the closed-form check."""
+    d = T.gen_w4a16(4, 16, 128, bl=32, seed=2, with_bias=False)
+    cmin, cmax = int(T.f16_bits(-65504.0)), int(T.f16_bits(65504.0))
+    ok = T.bits_f16(T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], 32, None, None, cmin, cmax))
+    bad_s = d["S16"].copy()
+    bad_s[:, [0, 1]] = bad_s[:, [1, 0]]
+    bad = T.bits_f16(T.oracle_w4a16(d["A16"], d["Bp"], bad_s, 32, None, None, cmin, cmax))
+    assert np.abs(ok.astype(np.float64) - bad.astype(np.float64)).max() > 1e-2
+
+
+def test_w8a8_accumulator_closed_form():
+    d = T.gen_w8a8(37, 45, 96, seed=4, with_c=True)
+    acc = T.oracle_w8a8_acc(d["A"], d["B"], d["C"], d["bias"])
+    exp = (d["A"].astype(np.int64) @ d["B"].astype(np.int64).T + d["C"] + d["bias"][None, :])
+    np.testing.assert_array_equal(acc, exp.astype(np.int32))
+
+
+def test_w8a8_is_acc_then_requant():
+    """The W8A8 oracle equals (closed-form int32 accumulator) -> per-column reference
+    multiplier (golden-pinned) -> pinned requantization, element by element."""
+    d = T.gen_w8a8(24, 40, 64, seed=8)
+    d["scale_d"] = np.float32(0.2)  # keep most outputs unsaturated
+    D = T.oracle_w8a8(d["A"], d["B"], None, d["bias"], -128, 127, d["scale_a"], d["scale_b"], 40,
+                      d["scale_d"], 0)
+    acc = d["A"].astype(np.int64) @ d["B"].astype(np.int64).T + d["bias"][None, :]
+    r = T.ref()
+    for j in range(40):
+        real = float(np.float64(d["scale_a"]) * np.float64(d["scale_b"][j]) /
+                     np.float64(d["scale_d"]))
+        m, s = qm(real)
+        if r is not None:
+            mm, ss = ctypes.c_int32(), ctypes.c_int32()
+            r.tqtr_quantize_multiplier(real, ctypes.byref(mm), ctypes.byref(ss))
+            assert (mm.value, ss.value) == (m, s)
+        for i in range(24):
+            assert D[i, j] == rq(int(acc[i, j]), m, -s - 1)
+    assert 0.2 < np.mean((D > -128) & (D < 127))
+
+
+def test_w8a8_float_sanity_like_reference_test():
+    """The reference test's own acceptance (test/common/quantized_gemm_test_runner.h:190-306):
+    dequantized int8 output within 1.0 absolute and cosine 0.999 of the fp32 reference GEMM."""
+    o = T.oracle()
+    m, n, k = 32, 48, 64
+    rng = np.random.default_rng(42)
+    Af = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    Bf = rng.uniform(-1, 1, (n, k)).astype(np.float32)
+    bf = rng.uniform(-10, 10, n).astype(np.float32)
+    sa, za = ctypes.c_float(), ctypes.c_int32()
+    o.tqto_compute_asym_quant_params_i8(T.ptr(Af), m * k, ctypes.byref(sa), ctypes.byref(za))
+    sb = np.zeros(n, np.float32)
+    for ch in range(n):
+        s = ctypes.c_float()
+        o.tqto_compute_sym_quant_params_i8(T.ptr(Bf[ch]), k, ctypes.byref(s))
+        sb[ch] = s.value
+    A = np.array([[o.tqto_quantize_i8(float(v), sa.value, za.value) for v in row] for row in Af],
+                 np.int8)
+    B = np.array([[o.tqto_quantize_i8(float(v), float(sb[ch]), 0) for v in Bf[ch]]
+                  for ch in range(n)], np.int8)
+    bias = np.array([o.tqto_quantize_bias_i32(float(bf[ch]), sa.value * float(sb[ch]))
+                     for ch in range(n)], np.int32)
+    fused = np.zeros(n, np.int32)
+    o.tqto_fuse_zp_to_bias(T.ptr(fused), T.ptr(bias), T.ptr(B), za.value, n, k)
+    ref = Af.astype(np.float64) @ Bf.astype(np.float64).T + bf[None, :]
+    sd, zd = ctypes.c_float(), ctypes.c_int32()
+    ref32 = ref.astype(np.float32)
+    o.tqto_compute_asym_quant_params_i8(T.ptr(ref32), m * n, ctypes.byref(sd), ctypes.byref(zd))
+    D = T.oracle_w8a8(A, B, None, fused, -128, 127, sa.value, sb, n, sd.value, zd.value)
+    deq = (D.astype(np.float64) - zd.value) * sd.value
+    assert np.abs(deq - ref).max() <= 1.0
+    cos = (deq * ref).sum() / (np.linalg.norm(deq) * np.linalg.norm(ref))
+    assert cos >= 0.999
+
+
+def test_w4a8_closed_form():
+    """Integer part by numpy int64 products; f32 epilogue by numpy float32 single ops in the
+    reference's order; and within 1e-5 relative of a float64 evaluation."""
+    d = T.gen_w4a8(9, 70, 256, seed=6, with_c=True, with_bias=True)
+    D = T.oracle_w4a8(d["A"], d["Bp"], d["C"], d["bias"], -np.inf, np.inf, d["scale_a"],
+                      d["zp_a"], d["scale_b"])
+    q = np.empty((70, 256), np.int64)
+    q[:, 0::2] = (d["Bp"] & 15).astype(np.int64) - 8
+    q[:, 1::2] = (d["Bp"] >> 4).astype(np.int64) - 8
+    a = d["A"].astype(np.int64)
+    acc = (a - d["zp_a"][:, None]) @ q.T  # sum (a - zp) * b == sum a*b - zp * sum b
+    f = acc.astype(np.float32)
+    f = (f * d["scale_a"][:, None]).astype(np.float32)
+    f = (f * d["scale_b"][None, :]).astype(np.float32)
+    f = (f + d["C"]).astype(np.float32)
+    f = (f + d["bias"][None, :]).astype(np.float32)
+    np.testing.assert_array_equal(D.view(np.uint32), f.view(np.uint32))
+    exact = (acc.astype(np.float64) * d["scale_a"][:, None] * d["scale_b"][None, :] + d["C"] +
+             d["bias"][None, :])
+    assert np.allclose(D, exact, rtol=1e-5, atol=1e-6)
+
+
+def test_w4a8_nibble_order_matters():
+    """Swapping the nibble order (odd k in the low nibble) changes the result: the even-k-low
+    convention of the reference (tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:77-93) is what is pinned."""
+    d = T.gen_w4a8(3, 20, 64, seed=1, with_bias=False)
+    D = T.oracle_w4a8(d["A"], d["Bp"], None, None, -np.inf, np.inf, d["scale_a"], d["zp_a"],
+                      d["scale_b"])
+    swapped = ((d["Bp"] >> 4) | (d["Bp"] << 4)).astype(np.uint8)
+    D2 = T.oracle_w4a8(d["A"], swapped, None, None, -np.inf, np.inf, d["scale_a"], d["zp_a"],
+                       d["scale_b"])
+    assert not np.array_equal(D, D2)
+
+
+# ------------------------------------------------------------------------------------------
+# Convolution restatement
+# ------------------------------------------------------------------------------------------
+
+def test_im2col_vs_reference_golden():
+    g = golden("ref_im2col.npz")
+    o = T.oracle()
+    for i, (ic, oc, ih, iw, kh, kw, sh, sw, ph, pw, dh, dw) in enumerate(g["shapes"]):
+        conv = T.make_conv((1, ih, iw), (1, kh, kw), (1, sh, sw), (1, dh, dw), (0, ph, pw), ic, oc)
+        inp = g["im2col_%d_in" % i]
+        col = np.zeros_like(g["im2col_%d_col" % i])
+        o.tqto_im2col_cl_i8(0, T.ptr(inp), T.ptr(col), ctypes.byref(conv))
+        np.testing.assert_array_equal(col, g["im2col_%d_col" % i])
+
+
+def test_igemmcl_equals_im2col_then_gemm():
+    """igemmcl == convcl: explicit im2col (reference tqt_im2col_cl, golden) followed by the
+    W8A8 GEMM (src/conv/conv_i8_i8/convcl…qsi8cxt…cpp:76-91)."""
+    g = golden("ref_im2col.npz")
+    for i, (ic, oc, ih, iw, kh, kw, sh, sw, ph, pw, dh, dw) in enumerate(g["shapes"]):
+        d = T.gen_igemmcl(1, ih, iw, ic, oc, kh, kw, stride=(sh, sw), pad=(ph, pw),
+                          dil=(dh, dw), seed=i)
+        inp = g["im2col_%d_in" % i].reshape(1, ih, iw, ic)
+        col = g["im2col_%d_col" % i]
+        D = T.oracle_igemmcl(inp, d["W"], d["bias"], -128, 127, d["conv"], d["scale_a"],
+                             d["scale_b"], oc, d["scale_d"], d["zp_d"])
+        G = T.oracle_w8a8(col, d["W"], None, d["bias"], -128, 127, d["scale_a"], d["scale_b"], oc,
+                          d["scale_d"], d["zp_d"])
+        np.testing.assert_array_equal(D, G)
+
+
+def test_igemmcl_tiles_and_batch_depth():
+    """Per-tile calls with m_idx reproduce one full call; a batch folded into depth equals
+    separate per-image convolutions."""
+    d = T.gen_igemmcl(3, 7, 9, 16, 24, 3, 3, pad=(1, 1), seed=12)
+    full = T.oracle_igemmcl(d["inp"], d["W"], d["bias"], -128, 127, d["conv"], d["scale_a"],
+                            d["scale_b"], 24, d["scale_d"], d["zp_d"])
+    M = full.shape[0]
+    D = np.zeros_like(full)
+    for m_idx in range(0, M, 4):
+        T.oracle_igemmcl(d["inp"], d["W"], d["bias"], -128, 127, d["conv"], d["scale_a"],
+                         d["scale_b"], 24, d["scale_d"], d["zp_d"], m=min(4, M - m_idx),
+                         m_idx=m_idx, D=D)
+    np.testing.assert_array_equal(D, full)
+    per = 7 * 9
+    for img in range(3):
+        single = T.make_conv((1, 7, 9), (1, 3, 3), (1, 1, 1), (1, 1, 1), (0, 1, 1), 16, 24)
+        one = T.oracle_igemmcl(np.ascontiguousarray(d["inp"][img:img + 1]), d["W"], d["bias"],
+                               -128, 127, single, d["scale_a"], d["scale_b"], 24, d["scale_d"],
+                               d["zp_d"])
+        np.testing.assert_array_equal(one, full[img * per:(img + 1) * per])
+
+
+def test_igemmcl_float_sanity_like_reference_test():
+    """Reference conv test acceptance (test/common/quantized_igemm_test_runner.h:359-469):
+    dequantized output within 1.0 absolute / cosine 0.999 of reference_conv<float>."""
+    r = T.ref()
+    if r is None:
+        pytest.skip("reference test code not built here")
+    o = T.oracle()
+    ic, oc, ih, iw = 16, 32, 8, 8
+    conv = T.make_conv((1, ih, iw), (1, 3, 3), (1, 1, 1), (1, 1, 1), (0, 1, 1), ic, oc)
+    K = 9 * ic
+    act = np.zeros((ih * iw, ic), np.float32)
+    r.tqtr_fill_uniform_f32(-1.0, 1.0, 42, T.ptr(act), ih * iw, ic)
+    w = np.zeros((oc, K), np.float32)
+    r.tqtr_fill_uniform_f32(-1.0, 1.0, 43, T.ptr(w), oc, K)
+    bf = np.zeros(oc, np.float32)
+    r.tqtr_fill_uniform_f32(-10.0, 10.0, 123, T.ptr(bf), 1, oc)
+    M = conv.output_shape[1] * conv.output_shape[2]
+    ref = np.zeros((M, oc), np.float32)
+    r.tqtr_reference_conv_cl_f32(0, T.ptr(act), T.ptr(w), T.ptr(bf), T.ptr(ref),
+                                 ctypes.byref(conv), -3.4e38, 3.4e38)
+    sa, za = ctypes.c_float(), ctypes.c_int32()
+    o.tqto_compute_asym_quant_params_i8(T.ptr(act), act.size, ctypes.byref(sa), ctypes.byref(za))
+    sb = np.zeros(oc, np.float32)
+    for ch in range(oc):
+        s = ctypes.c_float()
+        o.tqto_compute_sym_quant_params_i8(T.ptr(w[ch]), K, ctypes.byref(s))
+        sb[ch] = s.value
+    A = np.array([[o.tqto_quantize_i8(float(v), sa.value, za.value) for v in row] for row in act],
+                 np.int8).reshape(1, ih, iw, ic)
+    W = np.array([[o.tqto_quantize_i8(float(v), float(sb[ch]), 0) for v in w[ch]]
+                  for ch in range(oc)], np.int8)
+    bias = np.array([o.tqto_quantize_bias_i32(float(bf[ch]), sa.value * float(sb[ch]))
+                     for ch in range(oc)], np.int32)
+    fused = np.zeros(oc, np.int32)
+    o.tqto_fuse_zp_to_bias(T.ptr(fused), T.ptr(bias), T.ptr(W), za.value, oc, K)
+    sd, zd = ctypes.c_float(), ctypes.c_int32()
+    o.tqto_compute_asym_quant_params_i8(T.ptr(ref), ref.size, ctypes.byref(sd), ctypes.byref(zd))
+    D = T.oracle_igemmcl(A, W, fused, -128, 127, conv, sa.value, sb, oc, sd.value, zd.value)
+    deq = (D.astype(np.float64) - zd.value) * sd.value
+    # the reference pads with int8 0, not zero_point_a, while the bias fusion covers all of K:
+    # border pixels carry a bias the fp32 reference does not have, as in the reference test
+    assert np.abs(deq - ref).max() <= 1.0 + 2 * abs(za.value) * sa.value * float(sb.max()) * K
+    cos = (deq * ref).sum() / (np.linalg.norm(deq) * np.linalg.norm(ref))
+    assert cos >= 0.99
+
+
+# ------------------------------------------------------------------------------------------
+# Harness quantization helpers vs the reference's own code
+# ------------------------------------------------------------------------------------------
+
+def test_quant_helpers_vs_reference_golden():
+    g = golden("ref_quant.npz")
+    o = T.oracle()
+    q8 = np.array([o.tqto_quantize_i8(float(v), float(s), int(z))
+                   for v, s, z in zip(g["vals"], g["scales"], g["zps"])], np.int8)
+    np.testing.assert_array_equal(q8, g["q8"])
+    qb = np.array([o.tqto_quantize_bias_i32(float(v) * 100, float(s) * 1e-3)
+                   for v, s in zip(g["vals"], g["scales"])], np.int32)
+    np.testing.assert_array_equal(qb, g["qb"])
+    fused = np.zeros(37, np.int32)
+    o.tqto_fuse_zp_to_bias(T.ptr(fused), T.ptr(g["bias"]), T.ptr(g["Bf"]), -7, 37, 53)
+    np.testing.assert_array_equal(fused, g["fused"])
+    i4 = np.zeros((9, 32), np.uint8)
+    i4s = np.zeros((9, 4), np.uint16)
+    o.tqto_quantize_fp16_to_int4(9, 64, 16, T.ptr(g["src"]), T.ptr(i4), T.ptr(i4s), 4)
+    np.testing.assert_array_equal(i4, g["i4"])
+    np.testing.assert_array_equal(i4s, g["i4s"])
+
+
+def test_live_reference_matches_golden():
+    """Where the reference test code is built (the build container), recompute one golden
+    vector live, so the fixtures cannot drift from the code that wrote them."""
+    r = T.ref()
+    if r is None:
+        pytest.skip("reference test code not built here")
+    g = golden("ref_clamp_i32.npz")
+    m, n, k, _ = g["shapes"][5]
+    A, B = g["clamp_5_A"], g["clamp_5_B"]
+    D = np.zeros((m, n), np.int32)
+    r.tqtr_reference_gemm_i32_i8(int(m), int(n), int(k), T.ptr(A), int(k), T.ptr(B), int(n), 0,
+                                 None, int(n), T.ptr(D), int(n), -100000, 100000)
+    np.testing.assert_array_equal(D, g["clamp_5_D"])

@@ -1,0 +1,398 @@
+// gemm_1xnbias_clamp_f16_f16_qsi4c2t (W4A16, block-quantized int4 weights) on gfx950.
+//
+// Fast path (bl == 32, k % 128 == 0, k <= 4096): a workgroup of 8 wave64s owns a strip of
+// 16-channel weight tiles for one group of 32 activation rows. Wave w owns a fixed slice of k
+// (a run of 32-wide scale blocks) and keeps its slice of A (32 rows, f16) in registers for the
+// whole strip, so A is read from memory once per workgroup. For each 16-channel tile:
+//   * each lane loads 16 contiguous weight bytes (one whole 32-k block of one channel) per
+//     128-bit load; a 4x4 lane-group transpose with v_permlane32_swap/v_permlane16_swap gives
+//     each lane group its 8-k slice of four consecutive blocks, the MFMA B-operand layout;
+//   * nibbles become f16 (q - 8) exactly: (nib | 0x6400) is the f16 value 1024 + q, and a
+//     packed f16 subtract of 1032 leaves q - 8;
+//   * v_mfma_f32_16x16x32_f16 contracts one scale block (all products exact in f32), and the
+//     block's f32 partial is scaled by the f32 value of its f16 scale and accumulated;
+//   * the eight waves' f32 partials are summed through LDS; C, bias and the clamp are applied
+//     in f32 and the result is rounded once to f16.
+// A generic one-thread-per-output kernel covers every other shape with the reference test
+// oracle's exact operation order (reference test/common/reference_gemm.cpp:132-179).
+#include "tqt_hip_common.hpp"
+#include "tqt_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950.h"
+
+namespace tqt {
+namespace {
+
+constexpr int kWaves = 8;
+constexpr int kMaxGroupsPerWave = 4;  // 4-block groups (128 k each) per wave -> k <= 4096
+constexpr int kMRows = 32;            // activation rows per workgroup (two 16-row MFMA tiles)
+constexpr int kNTile = 16;
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+struct W4A16Args
+{
+    int M, N, K;
+    int ntiles;  // 16-channel tiles
+    const _Float16 *A;
+    long long lda;
+    const uint8_t *B;
+    long long bstride;  // bytes between weight rows
+    const _Float16 *scale_b;
+    long long ldsb;
+    const _Float16 *C;
+    long long ldc;
+    _Float16 *D;
+    long long ldd;
+    const _Float16 *bias;
+    float cmin, cmax;
+    int bl;
+};
+
+// 4x4 transpose of 32-bit values across the four 16-lane groups: on entry p[j] of lane group
+// g holds element (g, j); on exit p[j] of lane group g holds element (j, g).
+__device__ __forceinline__ void transpose_lane_groups(uint32_t p[4])
+{
+    auto s02 = __builtin_amdgcn_permlane32_swap(p[0], p[2], false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(p[1], p[3], false, false);
+    // p0 = [x00 x10 x02 x12], p2 = [x20 x30 x22 x32], p1 = [x01 x11 x03 x13], p3 = [x21 x31 x23 x33]
+    auto t01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    auto t23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    p[0] = t01[0];
+    p[1] = t01[1];
+    p[2] = t23[0];
+    p[3] = t23[1];
+}
+
+// 8 nibbles (k = 0..7 of this lane's slice, nibble i at bits 4i) -> 8 exact f16 values q - 8,
+// in slot order k = 0, 4, 1, 5, 2, 6, 3, 7.
+__device__ __forceinline__ f16x8 unpack_q8(uint32_t x)
+{
+    const f16x2 bias = f16x2{static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    uint32_t d[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        d[j] = ((x >> (4 * j)) & 0x000f000fu) | 0x64006400u;
+    }
+    f16x8 out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f16x2 h = __builtin_bit_cast(f16x2, d[j]) + bias;
+        out[2 * j] = h[0];
+        out[2 * j + 1] = h[1];
+    }
+    return out;
+}
+
+// 8 consecutive f16 activations k = 0..7 -> slot order k = 0, 4, 1, 5, 2, 6, 3, 7.
+__device__ __forceinline__ f16x8 permute_a(u32x4 v)
+{
+    u32x4 o;
+    o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+    return __builtin_bit_cast(f16x8, o);
+}
+
+__global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
+{
+    __shared__ float s_part[2][kWaves][kMRows][kNTile];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int fr = lane & 15;
+    const int fg = lane >> 4;
+    const int mg0 = blockIdx.y * kMRows;
+
+    // Strip of 16-channel tiles for this workgroup.
+    const int t_begin = static_cast<int>((static_cast<long long>(blockIdx.x) * a.ntiles) / gridDim.x);
+    const int t_end = static_cast<int>((static_cast<long long>(blockIdx.x + 1) * a.ntiles) / gridDim.x);
+
+    // k slice of this wave, in 4-block groups of 128 k.
+    const int ngroups = a.K / 128;
+    const int gpw = (ngroups + kWaves - 1) / kWaves;
+    const int g_begin = min(ngroups, wave * gpw);
+    const int g_cnt = min(ngroups, g_begin + gpw) - g_begin;
+
+    // A operand for every block of the slice and both 16-row tiles.
+    f16x8 fa[kMaxGroupsPerWave * 4][2];
+#pragma unroll
+    for (int j = 0; j < kMaxGroupsPerWave * 4; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int row = mg0 + mt * 16 + fr;
+            if (j < g_cnt * 4 && row < a.M) {
+                const int k = (g_begin * 4 + j) * 32 + fg * 8;
+                fa[j][mt] = permute_a(*reinterpret_cast<const u32x4 *>(
+                    a.A + static_cast<long long>(row) * a.lda + k));
+            } else {
+                fa[j][mt] = f16x8{};
+            }
+        }
+    }
+
+    u32x4 wcur[kMaxGroupsPerWave], wnext[kMaxGroupsPerWave];
+    uint64_t scur[kMaxGroupsPerWave], snext[kMaxGroupsPerWave];
+
+    auto load_tile = [&](int t, u32x4 (&w)[kMaxGroupsPerWave], uint64_t (&s)[kMaxGroupsPerWave]) {
+        const int n = t * kNTile + fr;
+        const bool ok = (t < t_end) && (n < a.N);
+        const uint8_t *wrow = a.B + static_cast<long long>(ok ? n : 0) * a.bstride;
+        const _Float16 *srow = a.scale_b + static_cast<long long>(ok ? n : 0) * a.ldsb;
+#pragma unroll
+        for (int q = 0; q < kMaxGroupsPerWave; ++q) {
+            if (ok && q < g_cnt) {
+                const int grp = g_begin + q;
+                w[q] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4 *>(wrow + grp * 64 + fg * 16));
+                s[q] = *reinterpret_cast<const uint64_t *>(srow + grp * 4);
+            } else {
+                w[q] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
+                s[q] = 0;
+            }
+        }
+    };
+
+    load_tile(t_begin, wcur, scur);
+    int buf = 0;
+    for (int t = t_begin; t < t_end; ++t) {
+        load_tile(t + 1, wnext, snext);
+
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int q = 0; q < kMaxGroupsPerWave; ++q) {
+            if (q < g_cnt) {
+                uint32_t p[4] = {wcur[q][0], wcur[q][1], wcur[q][2], wcur[q][3]};
+                transpose_lane_groups(p);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f16x8 wb = unpack_q8(p[j]);
+                    const uint16_t sbits = static_cast<uint16_t>(scur[q] >> (16 * j));
+                    const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sbits));
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) {
+                        const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            fa[q * 4 + j][mt], wb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            acc[mt][r] = __builtin_fmaf(part[r], sf, acc[mt][r]);
+                        }
+                    }
+                }
+            }
+        }
+        // partial of this wave: rows 16*mt + 4*fg + r, column fr
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s_part[buf][wave][mt * 16 + 4 * fg + r][fr] = acc[mt][r];
+            }
+        }
+        __syncthreads();
+        {
+            const int orow = tid >> 4;  // 0..31
+            const int ocol = tid & 15;
+            const int gm = mg0 + orow;
+            const int gn = t * kNTile + ocol;
+            if (gm < a.M && gn < a.N) {
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    v += s_part[buf][w][orow][ocol];
+                }
+                if (a.C) {
+                    v += static_cast<float>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+                }
+                if (a.bias) {
+                    v += static_cast<float>(a.bias[gn]);
+                }
+                v = fmaxf(v, a.cmin);
+                v = fminf(v, a.cmax);
+                a.D[static_cast<long long>(gm) * a.ldd + gn] = static_cast<_Float16>(v);
+            }
+        }
+        buf ^= 1;
+#pragma unroll
+        for (int q = 0; q < kMaxGroupsPerWave; ++q) {
+            wcur[q] = wnext[q];
+            scur[q] = snext[q];
+        }
+    }
+}
+
+// Generic path: the reference test oracle's operation order, one thread per output
+// (acc = C; acc += a * (f32(q - 8) * f32(s)) in k order without FMA; acc += bias; clamp).
+__global__ __launch_bounds__(256) void w4a16_generic_kernel(W4A16Args a)
+{
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= static_cast<long long>(a.M) * a.N) {
+        return;
+    }
+    const int gm = static_cast<int>(idx / a.N);
+    const int gn = static_cast<int>(idx - static_cast<long long>(gm) * a.N);
+    float acc = 0.f;
+    if (a.C) {
+        acc = static_cast<float>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+    }
+    const _Float16 *arow = a.A + static_cast<long long>(gm) * a.lda;
+    const uint8_t *brow = a.B + static_cast<long long>(gn) * a.bstride;
+    const _Float16 *srow = a.scale_b + static_cast<long long>(gn) * a.ldsb;
+    for (int p = 0; p < a.K; ++p) {
+        const uint8_t byte = brow[p >> 1];
+        const int q = (p & 1) ? (byte >> 4) - 8 : (byte & 0xf) - 8;
+        const float s = static_cast<float>(srow[p / a.bl]);
+        const float bd = __fmul_rn(static_cast<float>(q), s);
+        acc = __fadd_rn(acc, __fmul_rn(static_cast<float>(arow[p]), bd));
+    }
+    if (a.bias) {
+        acc = __fadd_rn(acc, static_cast<float>(a.bias[gn]));
+    }
+    acc = (acc < a.cmin) ? a.cmin : acc;
+    acc = (a.cmax < acc) ? a.cmax : acc;
+    a.D[static_cast<long long>(gm) * a.ldd + gn] = static_cast<_Float16>(acc);
+}
+
+int device_cu_count()
+{
+    int dev = 0;
+    TQT_HIP_CHECK(hipGetDevice(&dev));
+    int cus = 0;
+    TQT_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    return cus > 0 ? cus : 1;
+}
+
+}  // namespace
+}  // namespace tqt
+
+using namespace tqt;
+
+extern "C" {
+
+static const size_t kW4A16MStep = 32;
+static const size_t kW4A16NStep = 16;
+
+size_t tqt_get_m_step_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(void)
+{
+    return kW4A16MStep;
+}
+size_t tqt_get_n_step_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(void)
+{
+    return kW4A16NStep;
+}
+size_t tqt_get_a_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(size_t m_idx, size_t k_idx,
+                                                                       size_t lda, size_t bl)
+{
+    TQT_REQUIRE(m_idx % kW4A16MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(bl >= 2 && bl % 2 == 0, "bl >= 2 && bl % 2 == 0");
+    TQT_REQUIRE(k_idx % bl == 0, "k_idx % bl == 0");
+    return (m_idx * lda + k_idx) * sizeof(float16_t);
+}
+size_t tqt_get_b_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(size_t n_idx, size_t k_idx,
+                                                                       size_t ldb, size_t bl)
+{
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    TQT_REQUIRE(bl >= 2 && bl % 2 == 0, "bl >= 2 && bl % 2 == 0");
+    TQT_REQUIRE(k_idx % bl == 0, "k_idx % bl == 0");
+    return n_idx * (ldb / 2) + k_idx / 2;
+}
+size_t tqt_get_scale_b_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(size_t n_idx,
+                                                                             size_t b_idx,
+                                                                             size_t ldsb)
+{
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    return (n_idx * ldsb + b_idx) * sizeof(float16_t);
+}
+size_t tqt_get_c_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(size_t m_idx, size_t n_idx,
+                                                                       size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kW4A16MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(float16_t);
+}
+size_t tqt_get_bias_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(size_t n_idx)
+{
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    return n_idx * sizeof(float16_t);
+}
+size_t tqt_get_d_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(size_t m_idx, size_t n_idx,
+                                                                       size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kW4A16MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(float16_t);
+}
+size_t tqt_get_d_size_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(float16_t);
+}
+
+void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda, size_t k_idx_a,
+    const void *B, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb, const void *C,
+    size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min, float16_t clamp_max,
+    void *stream)
+{
+    (void)k_idx_a;
+    (void)k_idx_b;
+    if (m == 0 || n == 0) {
+        return;
+    }
+    // reference …qsi4c2t_8x2vl_rvv.h:59 / .cpp:38-40: bl even and >= 2, k % bl == 0
+    TQT_REQUIRE(bl >= 2 && bl % 2 == 0, "bl >= 2 && bl % 2 == 0");
+    TQT_REQUIRE(k % bl == 0, "k % bl == 0");
+    TQT_REQUIRE(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "dimension exceeds 2^31-1");
+    TQT_REQUIRE((A && B && scale_b) || k == 0, "A/B/scale_b == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    W4A16Args a = {};
+    a.M = static_cast<int>(m);
+    a.N = static_cast<int>(n);
+    a.K = static_cast<int>(k);
+    a.ntiles = static_cast<int>((n + kNTile - 1) / kNTile);
+    a.A = static_cast<const _Float16 *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const uint8_t *>(B);
+    a.bstride = static_cast<long long>(ldb / 2);
+    a.scale_b = static_cast<const _Float16 *>(scale_b);
+    a.ldsb = static_cast<long long>(ldsb);
+    a.C = static_cast<const _Float16 *>(C);
+    a.ldc = static_cast<long long>(ldc);
+    a.D = static_cast<_Float16 *>(D);
+    a.ldd = static_cast<long long>(ldd);
+    a.bias = static_cast<const _Float16 *>(bias);
+    a.cmin = static_cast<float>(clamp_min);
+    a.cmax = static_cast<float>(clamp_max);
+    a.bl = static_cast<int>(bl);
+    hipStream_t s = as_stream(stream);
+    const bool fast = bl == 32 && k % 128 == 0 && k <= 128u * kWaves * kMaxGroupsPerWave &&
+                      lda % 8 == 0 && (ldb / 2) % 16 == 0 && ldsb % 4 == 0 && aligned16(A) &&
+                      aligned16(B) && (reinterpret_cast<uintptr_t>(scale_b) & 7u) == 0;
+    if (fast) {
+        static int cus = device_cu_count();
+        const int gx = a.ntiles < cus ? a.ntiles : cus;
+        const unsigned long long gy = (m + kMRows - 1) / kMRows;
+        TQT_REQUIRE(gy < 65536, "m too large");
+        hipLaunchKernelGGL(w4a16_mfma_kernel, dim3(gx, static_cast<unsigned>(gy)), dim3(512), 0, s,
+                           a);
+    } else {
+        const long long total = static_cast<long long>(m) * static_cast<long long>(n);
+        const long long blocks = (total + 255) / 256;
+        TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
+        hipLaunchKernelGGL(w4a16_generic_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                           s, a);
+    }
+    check_launch("tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(
+    size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda, size_t k_idx_a,
+    const void *B, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb, const void *C,
+    size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min, float16_t clamp_max)
+{
+    tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950_async(
+        m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd, bias,
+        clamp_min, clamp_max, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950");
+}
+
+}  // extern "C"

@@ -1,0 +1,769 @@
+// int8 x int8 -> int32 contraction on gfx950 int8 MFMA, shared by three kernel types:
+//   gemm_clamp_i32_i8_i8                                (B is [k, n] row-major, int32 out)
+//   gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt     (B is [n, k], requantized int8 out)
+//   igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt  (A gathered from an NDHWC image)
+//
+// Fast path: a workgroup of 256 threads (4 wave64s in a 2x2 grid) computes a BM x 128 output
+// tile. K advances 64 bytes at a time through double-buffered LDS tiles; each wave issues
+// v_mfma_i32_16x16x64_i8 on 16x16 sub-tiles. The int32 epilogue (C, bias, requantization,
+// saturation, clamp) is fused into the store. A generic one-thread-per-output kernel covers
+// shapes the fast path does not accept (unaligned pointers or strides, K not a multiple of 16,
+// channel counts not a multiple of 16).
+#include "tqt_hip_common.hpp"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_clamp_i32_i8_i8_mfma_gfx950.h"
+#include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
+
+namespace tqt {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBN = 128;
+constexpr int kBK = 64;
+
+enum AMode { A_MATRIX = 0, A_CONV_CL = 1 };
+enum BMode { B_NK = 0, B_KN = 1 };
+enum EpiMode { EPI_CLAMP_I32 = 0, EPI_REQUANT_I8 = 1 };
+
+struct ConvGeom
+{
+    int ID, IH, IW;
+    int OH, OW;
+    int KH, KW;
+    int SD, SH, SW;
+    int DD, DH, DW;
+    int PD, PH, PW;
+    int IC;   // channel stride of the NDHWC input
+    int ICg;  // channels per group (K = KD*KH*KW*ICg)
+};
+
+struct Int8Args
+{
+    int M, N, K;
+    const int8_t *A;  // matrix A, or the group's channel base of the NDHWC input
+    long long lda;
+    const int8_t *B;
+    long long ldb;
+    const int32_t *C;
+    long long ldc;
+    void *D;
+    long long ldd;
+    long long d_row0;  // igemmcl: D row of local pixel 0 (= m_idx); 0 otherwise
+    long long p0;      // igemmcl: global pixel index of local pixel 0 (= m_idx)
+    const int32_t *bias;
+    int32_t cmin, cmax;
+    float scale_a;
+    const float *scale_b;
+    int32_t quant_channel_b;
+    float scale_d;
+    int32_t zp_d;
+    ConvGeom cv;
+};
+
+// LDS tile of R rows x 64 bytes. The 16-byte column chunk of row r is XOR-swizzled with
+// (r >> 2) & 3 so that the 16 rows read by one 16-lane group of ds_read_b128 hit distinct
+// banks.
+__device__ __forceinline__ int lds_off(int row, int chunk)
+{
+    return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 4);
+}
+
+// A-side gather for the implicit convolution: 16 input bytes for local pixel `row` and
+// reduction index k (k % 16 == 0, a 16-byte run never crosses a tap because ICg % 16 == 0).
+__device__ __forceinline__ i32x4 conv_chunk(const Int8Args &a, int od, int oh, int ow, int k)
+{
+    const ConvGeom &g = a.cv;
+    const int tap = k / g.ICg;
+    const int ic = k - tap * g.ICg;
+    const int kw = tap % g.KW;
+    const int t2 = tap / g.KW;
+    const int kh = t2 % g.KH;
+    const int kd = t2 / g.KH;
+    const int id = od * g.SD + kd * g.DD - g.PD;
+    const int ih = oh * g.SH + kh * g.DH - g.PH;
+    const int iw = ow * g.SW + kw * g.DW - g.PW;
+    if (id < 0 || id >= g.ID || ih < 0 || ih >= g.IH || iw < 0 || iw >= g.IW) {
+        return i32x4{0, 0, 0, 0};
+    }
+    const long long pix = (static_cast<long long>(id) * g.IH + ih) * g.IW + iw;
+    return *reinterpret_cast<const i32x4 *>(a.A + pix * g.IC + ic);
+}
+
+template <int BM, int AM, int BMd, int EPI>
+__global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
+{
+    constexpr int WM = BM / 2;        // rows per wave
+    constexpr int MT = WM / 16;       // 16-row sub-tiles per wave
+    constexpr int NT = 4;             // 16-col sub-tiles per wave (64 columns)
+    constexpr int A_CHUNKS = BM * 4 / kThreads;  // 16-byte chunks per thread per A tile
+    constexpr int B_CHUNKS = kBN * 4 / kThreads;
+
+    __shared__ __attribute__((aligned(16))) int8_t lds_a[2][BM * kBK];
+    __shared__ __attribute__((aligned(16))) int8_t lds_b[2][kBN * kBK];
+    __shared__ int32_t s_mult[kBN];
+    __shared__ int32_t s_shift[kBN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+
+    const int tiles_n = (a.N + kBN - 1) / kBN;
+    const int tile_m = blockIdx.x / tiles_n;
+    const int tile_n = blockIdx.x - tile_m * tiles_n;
+    const int m0 = tile_m * BM;
+    const int n0 = tile_n * kBN;
+
+    if constexpr (EPI == EPI_REQUANT_I8) {
+        if (tid < kBN && n0 + tid < a.N) {
+            column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, n0 + tid,
+                                  s_mult[tid], s_shift[tid]);
+        }
+    }
+
+    // Per-thread load assignment (fixed across the K loop).
+    int a_row[A_CHUNKS], a_chk[A_CHUNKS];
+    bool a_ok[A_CHUNKS];
+    int a_od[A_CHUNKS], a_oh[A_CHUNKS], a_ow[A_CHUNKS];
+    const int8_t *a_ptr[A_CHUNKS];
+#pragma unroll
+    for (int j = 0; j < A_CHUNKS; ++j) {
+        const int c = tid + j * kThreads;
+        a_row[j] = c >> 2;
+        a_chk[j] = c & 3;
+        const int gm = m0 + a_row[j];
+        a_ok[j] = gm < a.M;
+        if constexpr (AM == A_MATRIX) {
+            a_ptr[j] = a.A + static_cast<long long>(a_ok[j] ? gm : 0) * a.lda + a_chk[j] * 16;
+            a_od[j] = a_oh[j] = a_ow[j] = 0;
+        } else {
+            const long long p = a.p0 + (a_ok[j] ? gm : 0);
+            const long long ohw = static_cast<long long>(a.cv.OH) * a.cv.OW;
+            a_od[j] = static_cast<int>(p / ohw);
+            a_oh[j] = static_cast<int>((p / a.cv.OW) % a.cv.OH);
+            a_ow[j] = static_cast<int>(p % a.cv.OW);
+            a_ptr[j] = nullptr;
+        }
+    }
+    int b_row[B_CHUNKS], b_chk[B_CHUNKS];
+    bool b_ok[B_CHUNKS];
+    const int8_t *b_ptr[B_CHUNKS];
+#pragma unroll
+    for (int j = 0; j < B_CHUNKS; ++j) {
+        const int c = tid + j * kThreads;
+        if constexpr (BMd == B_NK) {
+            b_row[j] = c >> 2;  // n within the tile
+            b_chk[j] = c & 3;   // 16-byte k chunk
+            const int gn = n0 + b_row[j];
+            b_ok[j] = gn < a.N;
+            b_ptr[j] = a.B + static_cast<long long>(b_ok[j] ? gn : 0) * a.ldb + b_chk[j] * 16;
+        } else {
+            b_row[j] = c >> 3;  // k within the tile
+            b_chk[j] = c & 7;   // 16-column chunk
+            const int gn = n0 + b_chk[j] * 16;
+            b_ok[j] = gn < a.N;
+            b_ptr[j] = a.B + (b_ok[j] ? gn : 0);
+        }
+    }
+
+    i32x4 ra[A_CHUNKS], rb[B_CHUNKS];
+
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < A_CHUNKS; ++j) {
+            const int k = k0 + a_chk[j] * 16;
+            if (a_ok[j] && k < a.K) {
+                if constexpr (AM == A_MATRIX) {
+                    ra[j] = *reinterpret_cast<const i32x4 *>(a_ptr[j] + k0);
+                } else {
+                    ra[j] = conv_chunk(a, a_od[j], a_oh[j], a_ow[j], k);
+                }
+            } else {
+                ra[j] = i32x4{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < B_CHUNKS; ++j) {
+            if constexpr (BMd == B_NK) {
+                const int k = k0 + b_chk[j] * 16;
+                rb[j] = (b_ok[j] && k < a.K) ? *reinterpret_cast<const i32x4 *>(b_ptr[j] + k0)
+                                             : i32x4{0, 0, 0, 0};
+            } else {
+                const int k = k0 + b_row[j];
+                const int gn = n0 + b_chk[j] * 16;
+                if (b_ok[j] && k < a.K) {
+                    const int8_t *src = b_ptr[j] + static_cast<long long>(k) * a.ldb;
+                    if (gn + 16 <= a.N) {
+                        rb[j] = *reinterpret_cast<const i32x4 *>(src);
+                    } else {
+                        i32x4 tmp = i32x4{0, 0, 0, 0};
+                        int8_t *tb = reinterpret_cast<int8_t *>(&tmp);
+                        for (int i = 0; i < 16 && gn + i < a.N; ++i) {
+                            tb[i] = src[i];
+                        }
+                        rb[j] = tmp;
+                    }
+                } else {
+                    rb[j] = i32x4{0, 0, 0, 0};
+                }
+            }
+        }
+    };
+
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < A_CHUNKS; ++j) {
+            *reinterpret_cast<i32x4 *>(&lds_a[buf][lds_off(a_row[j], a_chk[j])]) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < B_CHUNKS; ++j) {
+            if constexpr (BMd == B_NK) {
+                *reinterpret_cast<i32x4 *>(&lds_b[buf][lds_off(b_row[j], b_chk[j])]) = rb[j];
+            } else {
+                // Transpose 16 consecutive n of one k into the [n][k] tile.
+                const int k = b_row[j];
+                const int8_t *bytes = reinterpret_cast<const int8_t *>(&rb[j]);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int n = b_chk[j] * 16 + i;
+                    lds_b[buf][lds_off(n, k >> 4) + (k & 15)] = bytes[i];
+                }
+            }
+        }
+    };
+
+    i32x4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            acc[i][j] = i32x4{0, 0, 0, 0};
+        }
+    }
+
+    const int nk = (a.K + kBK - 1) / kBK;
+    const int frag_row = lane & 15;
+    const int frag_chk = lane >> 4;
+
+    if (nk > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) {
+            load_tile((kt + 1) * kBK);
+        }
+        i32x4 fa[MT], fb[NT];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const int r = wm * WM + i * 16 + frag_row;
+            fa[i] = *reinterpret_cast<const i32x4 *>(&lds_a[buf][lds_off(r, frag_chk)]);
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int r = wn * 64 + j * 16 + frag_row;
+            fb[j] = *reinterpret_cast<const i32x4 *>(&lds_b[buf][lds_off(r, frag_chk)]);
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (kt + 1 < nk) {
+            store_tile(buf ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue: lane holds D[4 * (lane / 16) + r][lane % 16] of every 16x16 sub-tile.
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int lc = wn * 64 + j * 16 + (lane & 15);
+            const int gn = n0 + lc;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
+                if (gm >= a.M || gn >= a.N) {
+                    continue;
+                }
+                uint32_t v = static_cast<uint32_t>(acc[i][j][r]);
+                if (a.C) {
+                    v += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+                }
+                if (a.bias) {
+                    v += static_cast<uint32_t>(a.bias[gn]);
+                }
+                const long long drow = a.d_row0 + gm;
+                if constexpr (EPI == EPI_CLAMP_I32) {
+                    int32_t x = static_cast<int32_t>(v);
+                    x = x < a.cmin ? a.cmin : x;
+                    x = x > a.cmax ? a.cmax : x;
+                    static_cast<int32_t *>(a.D)[drow * a.ldd + gn] = x;
+                } else {
+                    static_cast<int8_t *>(a.D)[drow * a.ldd + gn] = requant_dev(
+                        static_cast<int32_t>(v), s_mult[lc], s_shift[lc], a.zp_d, a.cmin, a.cmax);
+                }
+            }
+        }
+    }
+}
+
+// Generic path: one thread per output, any strides and any K.
+template <int AM, int BMd, int EPI>
+__global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
+{
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const long long total = static_cast<long long>(a.M) * a.N;
+    if (idx >= total) {
+        return;
+    }
+    const int gm = static_cast<int>(idx / a.N);
+    const int gn = static_cast<int>(idx - static_cast<long long>(gm) * a.N);
+    uint32_t acc = 0;
+    if constexpr (AM == A_MATRIX) {
+        const int8_t *arow = a.A + static_cast<long long>(gm) * a.lda;
+        for (int k = 0; k < a.K; ++k) {
+            const int32_t bv = (BMd == B_NK) ? a.B[static_cast<long long>(gn) * a.ldb + k]
+                                             : a.B[static_cast<long long>(k) * a.ldb + gn];
+            acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * bv);
+        }
+    } else {
+        const ConvGeom &g = a.cv;
+        const long long p = a.p0 + gm;
+        const long long ohw = static_cast<long long>(g.OH) * g.OW;
+        const int od = static_cast<int>(p / ohw);
+        const int oh = static_cast<int>((p / g.OW) % g.OH);
+        const int ow = static_cast<int>(p % g.OW);
+        const int8_t *w = a.B + static_cast<long long>(gn) * a.ldb;
+        const int taps = a.K / g.ICg;
+        for (int tap = 0; tap < taps; ++tap) {
+            const int kw = tap % g.KW;
+            const int kh = (tap / g.KW) % g.KH;
+            const int kd = tap / (g.KW * g.KH);
+            const int id = od * g.SD + kd * g.DD - g.PD;
+            const int ih = oh * g.SH + kh * g.DH - g.PH;
+            const int iw = ow * g.SW + kw * g.DW - g.PW;
+            const bool inb = id >= 0 && id < g.ID && ih >= 0 && ih < g.IH && iw >= 0 && iw < g.IW;
+            const int8_t *src =
+                inb ? a.A + ((static_cast<long long>(id) * g.IH + ih) * g.IW + iw) * g.IC : nullptr;
+            for (int ic = 0; ic < g.ICg; ++ic) {
+                const int32_t av = src ? static_cast<int32_t>(src[ic]) : 0;
+                acc += static_cast<uint32_t>(av * static_cast<int32_t>(w[ic]));
+            }
+            w += g.ICg;
+        }
+    }
+    if (a.C) {
+        acc += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+    }
+    if (a.bias) {
+        acc += static_cast<uint32_t>(a.bias[gn]);
+    }
+    const long long drow = a.d_row0 + gm;
+    if constexpr (EPI == EPI_CLAMP_I32) {
+        int32_t x = static_cast<int32_t>(acc);
+        x = x < a.cmin ? a.cmin : x;
+        x = x > a.cmax ? a.cmax : x;
+        static_cast<int32_t *>(a.D)[drow * a.ldd + gn] = x;
+    } else {
+        int32_t mult, shift;
+        column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, gn, mult, shift);
+        static_cast<int8_t *>(a.D)[drow * a.ldd + gn] =
+            requant_dev(static_cast<int32_t>(acc), mult, shift, a.zp_d, a.cmin, a.cmax);
+    }
+}
+
+template <int AM, int BMd, int EPI>
+void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *where)
+{
+    if (a.M <= 0 || a.N <= 0) {
+        return;
+    }
+    if (fast) {
+        const int tiles_n = (a.N + kBN - 1) / kBN;
+        const long long tiles_m128 = (a.M + 127) / 128;
+        // Use 64-row tiles when 128-row tiles would leave most of the 256 CUs idle.
+        if (tiles_m128 * tiles_n >= 256) {
+            const long long blocks = tiles_m128 * tiles_n;
+            TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
+            hipLaunchKernelGGL((int8_mfma_kernel<128, AM, BMd, EPI>), dim3(blocks), dim3(kThreads),
+                               0, stream, a);
+        } else {
+            const long long blocks = ((a.M + 63) / 64) * static_cast<long long>(tiles_n);
+            TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
+            hipLaunchKernelGGL((int8_mfma_kernel<64, AM, BMd, EPI>), dim3(blocks), dim3(kThreads),
+                               0, stream, a);
+        }
+    } else {
+        const long long total = static_cast<long long>(a.M) * a.N;
+        const long long blocks = (total + 255) / 256;
+        TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
+        hipLaunchKernelGGL((int8_generic_kernel<AM, BMd, EPI>), dim3(blocks), dim3(256), 0, stream,
+                           a);
+    }
+    check_launch(where);
+}
+
+Int8Args base_args(size_t m, size_t n, size_t k)
+{
+    TQT_REQUIRE(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "dimension exceeds 2^31-1");
+    Int8Args a = {};
+    a.M = static_cast<int>(m);
+    a.N = static_cast<int>(n);
+    a.K = static_cast<int>(k);
+    return a;
+}
+
+}  // namespace
+}  // namespace tqt
+
+using namespace tqt;
+
+// =============================================================================================
+// gemm_clamp_i32_i8_i8 (reference …/gemm_clamp_i32_i8_i8_4x1vl_rvv.cpp:25-146)
+// =============================================================================================
+extern "C" {
+
+static const size_t kClampMStep = 128;
+static const size_t kClampNStep = 128;
+
+size_t tqt_get_m_step_gemm_clamp_i32_i8_i8_mfma_gfx950(void)
+{
+    return kClampMStep;
+}
+size_t tqt_get_n_step_gemm_clamp_i32_i8_i8_mfma_gfx950(void)
+{
+    return kClampNStep;
+}
+size_t tqt_get_a_offset_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda)
+{
+    TQT_REQUIRE(m_idx % kClampMStep == 0, "m_idx % m_step == 0");
+    return (m_idx * lda + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_b_offset_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb)
+{
+    TQT_REQUIRE(n_idx % kClampNStep == 0, "n_idx % n_step == 0");
+    return (k_idx * ldb + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_c_offset_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kClampMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kClampNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_d_offset_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kClampMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kClampNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_d_size_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(int32_t);
+}
+
+void tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950_async(size_t m, size_t n, size_t k, const void *A,
+                                                    size_t lda, size_t k_idx_a, const void *B,
+                                                    size_t ldb, size_t k_idx_b, const void *C,
+                                                    size_t ldc, void *D, size_t ldd,
+                                                    int32_t clamp_min, int32_t clamp_max,
+                                                    void *stream)
+{
+    (void)k_idx_a;
+    (void)k_idx_b;
+    if (m == 0 || n == 0) {
+        return;
+    }
+    TQT_REQUIRE(A != nullptr || k == 0, "A == NULL");
+    TQT_REQUIRE(B != nullptr || k == 0, "B == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    Int8Args a = base_args(m, n, k);
+    a.A = static_cast<const int8_t *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const int8_t *>(B);
+    a.ldb = static_cast<long long>(ldb);
+    a.C = static_cast<const int32_t *>(C);
+    a.ldc = static_cast<long long>(ldc);
+    a.D = D;
+    a.ldd = static_cast<long long>(ldd);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    const bool fast = (k % 16 == 0) && (lda % 16 == 0) && (ldb % 16 == 0) && aligned16(A) &&
+                      aligned16(B);
+    launch_int8<A_MATRIX, B_KN, EPI_CLAMP_I32>(a, fast, as_stream(stream),
+                                                "tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950");
+}
+
+void tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t m, size_t n, size_t k, const void *A,
+                                              size_t lda, size_t k_idx_a, const void *B,
+                                              size_t ldb, size_t k_idx_b, const void *C,
+                                              size_t ldc, void *D, size_t ldd, int32_t clamp_min,
+                                              int32_t clamp_max)
+{
+    tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950_async(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C,
+                                                   ldc, D, ldd, clamp_min, clamp_max, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950");
+}
+
+// =============================================================================================
+// gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt (reference …qsi8cxt_4x1vl_rvv.cpp:26-198)
+// =============================================================================================
+
+static const size_t kReqMStep = 128;
+static const size_t kReqNStep = 128;
+
+size_t tqt_get_m_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(void)
+{
+    return kReqMStep;
+}
+size_t tqt_get_n_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(void)
+{
+    return kReqNStep;
+}
+size_t tqt_get_a_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(size_t m_idx,
+                                                                                    size_t k_idx,
+                                                                                    size_t lda)
+{
+    TQT_REQUIRE(m_idx % kReqMStep == 0, "m_idx % m_step == 0");
+    return (m_idx * lda + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_b_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(size_t n_idx,
+                                                                                    size_t k_idx,
+                                                                                    size_t ldb)
+{
+    TQT_REQUIRE(n_idx % kReqNStep == 0, "n_idx % n_step == 0");
+    return (n_idx * ldb + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_c_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(size_t m_idx,
+                                                                                    size_t n_idx,
+                                                                                    size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kReqMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kReqNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_bias_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
+    size_t n_idx)
+{
+    TQT_REQUIRE(n_idx % kReqNStep == 0, "n_idx % n_step == 0");
+    return n_idx * sizeof(int32_t);
+}
+size_t tqt_get_d_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(size_t m_idx,
+                                                                                    size_t n_idx,
+                                                                                    size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kReqMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kReqNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_d_size_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(size_t m,
+                                                                                  size_t n)
+{
+    return m * n * sizeof(int8_t);
+}
+
+void tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qai8_qsi8cx_params *params,
+    void *stream)
+{
+    (void)k_idx_a;
+    (void)k_idx_b;
+    if (!params) {
+        return;  // reference …qsi8cxt_4x1vl_rvv.cpp:148-150
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    TQT_REQUIRE(params->scale_b != nullptr, "params->scale_b == NULL");
+    TQT_REQUIRE(A != nullptr || k == 0, "A == NULL");
+    TQT_REQUIRE(B != nullptr || k == 0, "B == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    Int8Args a = base_args(m, n, k);
+    a.A = static_cast<const int8_t *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const int8_t *>(B);
+    a.ldb = static_cast<long long>(ldb);
+    a.C = static_cast<const int32_t *>(C);
+    a.ldc = static_cast<long long>(ldc);
+    a.D = D;
+    a.ldd = static_cast<long long>(ldd);
+    a.bias = static_cast<const int32_t *>(bias);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    a.scale_a = params->scale_a;
+    a.scale_b = params->scale_b;
+    a.quant_channel_b = params->quant_channel_b;
+    a.scale_d = params->scale_d;
+    a.zp_d = params->zero_point_d;
+    const bool fast = (k % 16 == 0) && (lda % 16 == 0) && (ldb % 16 == 0) && aligned16(A) &&
+                      aligned16(B);
+    launch_int8<A_MATRIX, B_NK, EPI_REQUANT_I8>(
+        a, fast, as_stream(stream),
+        "tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qai8_qsi8cx_params *params)
+{
+    if (!params) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950_async(
+        m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min, clamp_max,
+        params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
+}
+
+// =============================================================================================
+// igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt (reference …igemmcl…_4x1vl_rvv.cpp:26-286)
+// =============================================================================================
+
+static const size_t kConvMStep = 128;
+static const size_t kConvNStep = 128;
+
+size_t tqt_get_m_step_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(void)
+{
+    return kConvMStep;
+}
+size_t tqt_get_n_step_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(void)
+{
+    return kConvNStep;
+}
+size_t tqt_get_b_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
+    size_t n_idx, size_t k_idx, size_t ldb)
+{
+    TQT_REQUIRE(n_idx % kConvNStep == 0, "n_idx % n_step == 0");
+    return (n_idx * ldb + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_c_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
+    size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(n_idx % kConvNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_bias_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
+    size_t n_idx)
+{
+    TQT_REQUIRE(n_idx % kConvNStep == 0, "n_idx % n_step == 0");
+    return n_idx * sizeof(int32_t);
+}
+size_t tqt_get_d_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
+    size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(n_idx % kConvNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_d_size_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(size_t m,
+                                                                                    size_t n)
+{
+    return m * n * sizeof(int8_t);
+}
+
+void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t m_idx,
+    size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qai8_qsi8cx_params *quant_params,
+    void *stream)
+{
+    (void)k;
+    (void)k_idx_a;
+    (void)k_idx_b;
+    (void)C;
+    (void)ldc;
+    if (!conv_params || !quant_params) {
+        return;  // reference …igemmcl…cpp:206-208
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    const tqt_conv_params &p = *conv_params;
+    TQT_REQUIRE(p.groups >= 1 && p.input_channel % p.groups == 0, "input_channel % groups != 0");
+    TQT_REQUIRE(quant_params->scale_b != nullptr, "quant_params->scale_b == NULL");
+    TQT_REQUIRE(input != nullptr && B != nullptr && D != nullptr, "NULL tensor pointer");
+    const size_t icg = p.input_channel / p.groups;
+    const size_t kfull = p.kernel_shape[0] * p.kernel_shape[1] * p.kernel_shape[2] * icg;
+    for (int i = 0; i < 3; ++i) {
+        TQT_REQUIRE(p.input_shape[i] < (1u << 30) && p.output_shape[i] < (1u << 30) &&
+                        p.kernel_shape[i] < (1u << 15) && p.stride[i] < (1u << 15) &&
+                        p.dilation[i] < (1u << 15) && p.pad[i] < (1u << 15),
+                    "conv geometry out of range");
+    }
+    TQT_REQUIRE(p.input_channel < (1u << 30), "input_channel out of range");
+    Int8Args a = base_args(m, n, kfull);
+    a.A = static_cast<const int8_t *>(input) + group_idx * icg;
+    a.B = static_cast<const int8_t *>(B);
+    a.ldb = static_cast<long long>(ldb);
+    a.D = D;
+    a.ldd = static_cast<long long>(ldd);
+    a.d_row0 = static_cast<long long>(m_idx);
+    a.p0 = static_cast<long long>(m_idx);
+    a.bias = static_cast<const int32_t *>(bias);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    a.scale_a = quant_params->scale_a;
+    a.scale_b = quant_params->scale_b;
+    a.quant_channel_b = quant_params->quant_channel_b;
+    a.scale_d = quant_params->scale_d;
+    a.zp_d = quant_params->zero_point_d;
+    ConvGeom &g = a.cv;
+    g.ID = static_cast<int>(p.input_shape[0]);
+    g.IH = static_cast<int>(p.input_shape[1]);
+    g.IW = static_cast<int>(p.input_shape[2]);
+    g.OH = static_cast<int>(p.output_shape[1]);
+    g.OW = static_cast<int>(p.output_shape[2]);
+    g.KH = static_cast<int>(p.kernel_shape[1]);
+    g.KW = static_cast<int>(p.kernel_shape[2]);
+    g.SD = static_cast<int>(p.stride[0]);
+    g.SH = static_cast<int>(p.stride[1]);
+    g.SW = static_cast<int>(p.stride[2]);
+    g.DD = static_cast<int>(p.dilation[0]);
+    g.DH = static_cast<int>(p.dilation[1]);
+    g.DW = static_cast<int>(p.dilation[2]);
+    g.PD = static_cast<int>(p.pad[0]);
+    g.PH = static_cast<int>(p.pad[1]);
+    g.PW = static_cast<int>(p.pad[2]);
+    g.IC = static_cast<int>(p.input_channel);
+    g.ICg = static_cast<int>(icg);
+    TQT_REQUIRE(g.OH > 0 && g.OW > 0 && icg > 0, "empty conv geometry");
+    const bool fast = (icg % 16 == 0) && (p.input_channel % 16 == 0) && (ldb % 16 == 0) &&
+                      aligned16(a.A) && aligned16(B);
+    launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8>(
+        a, fast, as_stream(stream),
+        "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
+}
+
+void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t m_idx,
+    size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qai8_qsi8cx_params *quant_params)
+{
+    if (!conv_params || !quant_params) {
+        return;
+    }
+    tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950_async(
+        m, n, k, input, group_idx, m_idx, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias,
+        clamp_min, clamp_max, conv_params, quant_params, nullptr);
+    finish_sync(nullptr,
+                "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
+}
+
+const char *tqt_gfx950_target(void)
+{
+    return "gfx950";
+}
+
+}  // extern "C"

@@ -1,0 +1,209 @@
+"""ctypes binding of the gfx950 TORQ-Tile C ABI (libtorq_tile_gfx950.so).
+
+This is the Python-side stub a framework maintainer would add to call the library: it declares
+every exported symbol with its exact C signature (include/*.h) and mirrors the parameter
+structs field for field. Buffers are passed as raw device addresses (int); torch tensors on a
+ROCm device provide them via ``tensor.data_ptr()``.
+
+Loading fails loudly: there is no CPU fallback. ``load()`` raises if the shared library has not
+been built (``make -C torq-tile_amd``).
+"""
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libtorq_tile_gfx950.so")
+
+c_size = ctypes.c_size_t
+c_vp = ctypes.c_void_p
+
+VARIANT = "mfma_gfx950"
+KERNELS = {
+    "clamp": "gemm_clamp_i32_i8_i8",
+    "w8a8": "gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt",
+    "w4a8": "gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt",
+    "w4a16": "gemm_1xnbias_clamp_f16_f16_qsi4c2t",
+    "igemmcl": "igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt",
+}
+
+
+class QAI8QSI8CXParams(ctypes.Structure):
+    """struct tqt_qai8_qai8_qsi8cx_params (reference tqt_params_i8_i8.h:16-24)."""
+
+    _fields_ = [
+        ("scale_a", ctypes.c_float),
+        ("zero_point_a", ctypes.c_int32),
+        ("scale_b", c_vp),
+        ("quant_channel_b", ctypes.c_int32),
+        ("scale_d", ctypes.c_float),
+        ("zero_point_d", ctypes.c_int32),
+    ]
+
+
+class QAI8DXQSI4CXParams(ctypes.Structure):
+    """struct tqt_qai8dx_qsi4cx_params (reference tqt_params_i8_i4.h:23-28)."""
+
+    _fields_ = [("scale_a", c_vp), ("zero_point_a", c_vp), ("scale_b", c_vp)]
+
+
+class ConvParams(ctypes.Structure):
+    """struct tqt_conv_params (reference src/common/tqt_conv.h:20-31)."""
+
+    _fields_ = [
+        ("input_shape", c_size * 3),
+        ("output_shape", c_size * 3),
+        ("kernel_shape", c_size * 3),
+        ("stride", c_size * 3),
+        ("dilation", c_size * 3),
+        ("pad", c_size * 3),
+        ("input_channel", c_size),
+        ("output_channel", c_size),
+        ("groups", c_size),
+    ]
+
+
+def conv_params(input_shape, kernel_shape, stride, dilation, pad, ic, oc, groups=1):
+    """Build ConvParams with the output shape the reference test harness computes
+    (test/common/conv_test_runner.h: (in + 2 pad - dil (k - 1) - 1) / stride + 1)."""
+    p = ConvParams()
+    out = [
+        (input_shape[i] + 2 * pad[i] - dilation[i] * (kernel_shape[i] - 1) - 1) // stride[i] + 1
+        for i in range(3)
+    ]
+    for i in range(3):
+        p.input_shape[i] = input_shape[i]
+        p.output_shape[i] = out[i]
+        p.kernel_shape[i] = kernel_shape[i]
+        p.stride[i] = stride[i]
+        p.dilation[i] = dilation[i]
+        p.pad[i] = pad[i]
+    p.input_channel = ic
+    p.output_channel = oc
+    p.groups = groups
+    return p
+
+
+def _sym(kind, action):
+    name = KERNELS[kind]
+    if action == "run":
+        verb = "run_igemm" if kind == "igemmcl" else "run"
+        return "tqt_%s_%s_%s" % (verb, name, VARIANT)
+    return "tqt_%s_%s_%s" % (action, name, VARIANT)
+
+
+# (action, restype, argtypes) per kernel type; float16 clamps are not callable from ctypes and
+# are reached through the test shim instead.
+_GEMM_I8_ARGS = [c_size, c_size, c_size, c_vp, c_size, c_size, c_vp, c_size, c_size, c_vp,
+                 c_size, c_vp, c_size]
+_SIGS = {
+    "clamp": {
+        "get_m_step": (c_size, []),
+        "get_n_step": (c_size, []),
+        "get_a_offset": (c_size, [c_size] * 3),
+        "get_b_offset": (c_size, [c_size] * 3),
+        "get_c_offset": (c_size, [c_size] * 3),
+        "get_d_offset": (c_size, [c_size] * 3),
+        "get_d_size": (c_size, [c_size] * 2),
+        "run": (None, _GEMM_I8_ARGS + [ctypes.c_int32, ctypes.c_int32]),
+        "run_async": (None, _GEMM_I8_ARGS + [ctypes.c_int32, ctypes.c_int32, c_vp]),
+    },
+    "w8a8": {
+        "get_m_step": (c_size, []),
+        "get_n_step": (c_size, []),
+        "get_a_offset": (c_size, [c_size] * 3),
+        "get_b_offset": (c_size, [c_size] * 3),
+        "get_c_offset": (c_size, [c_size] * 3),
+        "get_bias_offset": (c_size, [c_size]),
+        "get_d_offset": (c_size, [c_size] * 3),
+        "get_d_size": (c_size, [c_size] * 2),
+        "run": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_int8, ctypes.c_int8,
+                                       ctypes.POINTER(QAI8QSI8CXParams)]),
+        "run_async": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_int8, ctypes.c_int8,
+                                             ctypes.POINTER(QAI8QSI8CXParams), c_vp]),
+    },
+    "w4a8": {
+        "get_m_step": (c_size, []),
+        "get_n_step": (c_size, []),
+        "get_a_offset": (c_size, [c_size] * 3),
+        "get_b_offset": (c_size, [c_size] * 3),
+        "get_c_offset": (c_size, [c_size] * 3),
+        "get_bias_offset": (c_size, [c_size]),
+        "get_d_offset": (c_size, [c_size] * 3),
+        "get_d_size": (c_size, [c_size] * 2),
+        "run": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float,
+                                       ctypes.POINTER(QAI8DXQSI4CXParams)]),
+        "run_async": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float,
+                                             ctypes.POINTER(QAI8DXQSI4CXParams), c_vp]),
+    },
+    "w4a16": {
+        "get_m_step": (c_size, []),
+        "get_n_step": (c_size, []),
+        "get_a_offset": (c_size, [c_size] * 4),
+        "get_b_offset": (c_size, [c_size] * 4),
+        "get_scale_b_offset": (c_size, [c_size] * 3),
+        "get_c_offset": (c_size, [c_size] * 3),
+        "get_bias_offset": (c_size, [c_size]),
+        "get_d_offset": (c_size, [c_size] * 3),
+        "get_d_size": (c_size, [c_size] * 2),
+    },
+    "igemmcl": {
+        "get_m_step": (c_size, []),
+        "get_n_step": (c_size, []),
+        "get_b_offset": (c_size, [c_size] * 3),
+        "get_c_offset": (c_size, [c_size] * 3),
+        "get_bias_offset": (c_size, [c_size]),
+        "get_d_offset": (c_size, [c_size] * 3),
+        "get_d_size": (c_size, [c_size] * 2),
+        "run": (None, [c_size, c_size, c_size, c_vp, c_size, c_size, c_size, c_vp, c_size, c_size,
+                       c_vp, c_size, c_vp, c_size, c_vp, ctypes.c_int8, ctypes.c_int8,
+                       ctypes.POINTER(ConvParams), ctypes.POINTER(QAI8QSI8CXParams)]),
+        "run_async": (None, [c_size, c_size, c_size, c_vp, c_size, c_size, c_size, c_vp, c_size,
+                             c_size, c_vp, c_size, c_vp, c_size, c_vp, ctypes.c_int8,
+                             ctypes.c_int8, ctypes.POINTER(ConvParams),
+                             ctypes.POINTER(QAI8QSI8CXParams), c_vp]),
+    },
+}
+
+
+class Lib:
+    """Typed access to every exported function: ``lib.fn(kind, action)``."""
+
+    def __init__(self, path=LIB_PATH):
+        if not os.path.exists(path):
+            raise RuntimeError(
+                "gfx950 library not built: %s missing (run make -C torq-tile_amd)" % path)
+        self.path = path
+        self.dll = ctypes.CDLL(path)
+        self._fns = {}
+        for kind, actions in _SIGS.items():
+            for action, (res, args) in actions.items():
+                if action == "run_async":
+                    name = _sym(kind, "run") + "_async"
+                else:
+                    name = _sym(kind, action)
+                f = getattr(self.dll, name)
+                f.restype = res
+                f.argtypes = args
+                self._fns[(kind, action)] = f
+        self.dll.tqt_gfx950_target.restype = ctypes.c_char_p
+        self.dll.tqt_gfx950_target.argtypes = []
+
+    def fn(self, kind, action):
+        return self._fns[(kind, action)]
+
+    def symbol_names(self):
+        names = [_sym(k, a) if a != "run_async" else _sym(k, "run") + "_async"
+                 for (k, a) in self._fns]
+        names += [_sym("w4a16", "run"), _sym("w4a16", "run") + "_async", "tqt_gfx950_target"]
+        return sorted(set(names))
+
+
+_LIB = None
+
+
+def load():
+    global _LIB
+    if _LIB is None:
+        _LIB = Lib()
+    return _LIB
