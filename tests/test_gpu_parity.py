@@ -96,9 +96,16 @@ W4A8_REF_SHAPES = [(8, 8, 8, dict()), (16, 16, 16, dict()), (32, 32, 32, dict())
                    (32, 32, 32, dict(bias=True)), (17, 19, 24, dict(bias=True)),
                    (32, 32, 32, dict(clamp=(-0.5, 0.5))), (32, 32, 32, dict(c=True)),
                    (32, 32, 32, dict(c=True, bias=True, clamp=(-0.5, 0.5)))]
+# Decode path (k % 256 == 0): k in pairs of 256 split over 8 waves, including empty waves
+# (k = 256, 768), a tail pair per wave (k = 2304, 4352), activations staged in LDS
+# (rows * k <= 8192) or read per step, several 15-row chunks with a short last one, and n tails.
 W4A8_FAST_SHAPES = [(1, 160, 256, dict(bias=True)), (4, 100, 512, dict(bias=True, c=True)),
-                    (15, 48, 384, dict(bias=True)), (16, 64, 1024, dict(clamp=(-0.5, 0.5))),
-                    (33, 37, 640, dict(bias=True))]
+                    (15, 48, 768, dict(bias=True)), (16, 64, 1024, dict(clamp=(-0.5, 0.5))),
+                    (33, 37, 2304, dict(bias=True)), (3, 45, 4352, dict(c=True)),
+                    (2, 17, 2048, dict(bias=True)), (31, 33, 512, dict(bias=True, c=True)),
+                    (2, 24, 65536, dict()),
+                    # k % 256 != 0 goes to the per-output path
+                    (15, 48, 384, dict(bias=True)), (33, 37, 640, dict(bias=True))]
 
 
 @pytest.mark.parametrize("m,n,k,opt", W4A8_REF_SHAPES + W4A8_FAST_SHAPES)
@@ -109,6 +116,20 @@ def test_w4a8_parity(gpu, m, n, k, opt):
     got = _gr().run_w4a8(d, cmin, cmax)
     exp = T.oracle_w4a8(d["A"], d["Bp"], d["C"], d["bias"], cmin, cmax, d["scale_a"], d["zp_a"],
                         d["scale_b"])
+    np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def test_w4a8_extreme_values(gpu):
+    """Largest accumulator the decode path admits: k = 65536, a = -128, q = 0 (w = -8)."""
+    m, n, k = 3, 32, 65536
+    d = T.gen_w4a8(m, n, k, seed=7, with_bias=True)
+    d["A"][:] = -128
+    d["A"][1, ::2] = 127
+    d["Bp"][:] = 0x00
+    d["Bp"][5:9] = 0xff
+    got = _gr().run_w4a8(d)
+    exp = T.oracle_w4a8(d["A"], d["Bp"], None, d["bias"], -np.inf, np.inf, d["scale_a"],
+                        d["zp_a"], d["scale_b"])
     np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
 
 

@@ -22,7 +22,10 @@ G = T.GOLDEN_DIR
 
 
 def golden(name):
-    return np.load(os.path.join(G, name), allow_pickle=False)
+    """All arrays of a fixture, loaded eagerly: an NpzFile re-reads each key on access, so a
+    pointer taken from g[key] would outlive the temporary array it points into."""
+    with np.load(os.path.join(G, name), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
 
 
 # ------------------------------------------------------------------------------------------

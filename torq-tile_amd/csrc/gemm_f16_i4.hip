@@ -389,6 +389,9 @@ void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(
     const void *B, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb, const void *C,
     size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min, float16_t clamp_max)
 {
+    if (m == 0 || n == 0) {
+        return;
+    }
     tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950_async(
         m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd, bias,
         clamp_min, clamp_max, nullptr);

@@ -1,28 +1,34 @@
 // gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt (W4A8) on gfx950.
 //
-// Fast path (decode-shaped, any m in chunks of 15 rows): one workgroup of 4 wave64s owns a
-// 16-channel weight tile (16 rows of B, contiguous [16, k/2] bytes) for one chunk of up to 15
-// activation rows. Each wave streams a quarter of k: one 128-bit load per lane covers 32
-// nibbles (k values) of one channel. Nibbles are split with two bit operations into unsigned
-// bytes q in [0, 15] and fed to v_mfma_i32_16x16x64_i8 as the B operand; the activation rows
-// are the A operand, byte-permuted into the same (even k, odd k) order. Two terms fold the
-// -8 zero point of the weights and the per-channel weight sum into the same MFMAs:
-//   * an extra MFMA per step with a constant B operand of -8 adds -8 * sum_k a to every
-//     column, so the accumulator holds sum_k a * (q - 8) exactly;
-//   * activation row `rows` (the first unused row of the 16-row A operand) is all ones, so
-//     that accumulator row holds sum_k (q - 8), the rsum_b of the reference.
-// The four waves' int32 partials are summed through LDS and the reference's f32 epilogue
-// (zero-point correction, two scale multiplies, C, bias, clamp; no FMA) runs per output.
+// Fast path (decode-shaped, any m in chunks of 15 rows, k % 256 == 0): one workgroup of 8
+// wave64s owns a 16-channel weight tile (16 rows of B) for one chunk of up to 15 activation
+// rows; wave w owns one eighth of k.
+//   * Weights stream in 128-bit loads shaped 8 rows x 128 bytes per wave instruction (whole
+//     cache lines), are staged through wave-private LDS (16-byte chunks XOR-swizzled by row)
+//     and read back in the MFMA B-operand layout. Each 128-byte-per-row "pair" of k (two MFMA
+//     steps) is consumed as soon as its two loads land, so compute overlaps the stream.
+//   * Nibbles become signed bytes in two bit operations each: ((w << 4) & 0xf0f0f0f0) ^
+//     0x80808080 is the byte 16 * (lo - 8) and (w & 0xf0f0f0f0) ^ 0x80808080 is 16 * (hi - 8).
+//     v_mfma_i32_16x16x64_i8 then accumulates exactly 16 * sum_k a * (q - 8); the workgroup
+//     sum is shifted right by 4 (exact: |16 * sum| < 2^31 for k <= 65536).
+//   * Activation row `rows` of the 16-row A operand is all ones, so that accumulator row is
+//     16 * sum_k (q - 8), the rsum_b of the reference; rows past it are zero.
+//   * Activations are permuted to the (even k, odd k) byte order of the decoded weights; they
+//     are staged in LDS once per workgroup when rows * k fits, else loaded per step.
+// The eight waves' partial sums meet in LDS and the reference's f32 epilogue (zero-point
+// correction, two scale multiplies, C, bias, clamp; no FMA) runs per output.
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
 
-constexpr int kRowsPerChunk = 15;  // activation rows per workgroup (row 15 is the ones row)
+constexpr int kRowsPerChunk = 15;  // activation rows per workgroup (one more row holds ones)
 constexpr int kNTile = 16;         // weight channels per workgroup
-constexpr int kStepK = 128;        // k values per wave step (4 lane groups x 32 nibbles)
-constexpr int kBatch = 8;          // steps whose loads are issued together
+constexpr int kWaves = 8;          // k is split eight ways inside the workgroup
+constexpr int kPairK = 256;        // k values per pair (128 bytes per weight row, 2 MFMA steps)
+constexpr int kPairsPerBatch = 2;  // pairs whose loads are in flight together per wave
+constexpr int kALdsBytes = 8192;   // activation bytes staged in LDS when rows * k fits
 
 struct W4A8Args
 {
@@ -42,142 +48,208 @@ struct W4A8Args
     const float *scale_b;
 };
 
-__device__ __forceinline__ float epilogue_f32(const W4A8Args &a, int gm, int gn, int32_t acc,
-                                              int32_t rsum)
+// reference tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:234-419: zp correction (int32), RNE convert, two
+// separate multiplies, C then bias (separate adds), vfmax then vfmin.
+__device__ __forceinline__ float epilogue_f32(int32_t acc, int32_t rsum, int32_t zp, float sa,
+                                              float sb, const float *c, const float *bias,
+                                              float cmin, float cmax)
 {
-    // tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:234-419: zp correction (int32), RNE convert, two
-    // separate multiplies, C then bias (separate adds), vfmax then vfmin.
+    // Rounds after every operation: the library is built with -ffp-contract=off, since hipcc
+    // would otherwise fuse a * b + c (__fmul_rn / __fadd_rn do not prevent it).
     const int32_t v = static_cast<int32_t>(static_cast<uint32_t>(acc) -
-                                           static_cast<uint32_t>(a.zp_a[gm]) *
-                                               static_cast<uint32_t>(rsum));
+                                           static_cast<uint32_t>(zp) * static_cast<uint32_t>(rsum));
     float f = __int2float_rn(v);
-    f = __fmul_rn(f, a.scale_a[gm]);
-    f = __fmul_rn(f, a.scale_b[gn]);
-    if (a.C) {
-        f = __fadd_rn(f, a.C[static_cast<long long>(gm) * a.ldc + gn]);
+    f = __fmul_rn(f, sa);
+    f = __fmul_rn(f, sb);
+    if (c) {
+        f = __fadd_rn(f, *c);
     }
-    if (a.bias) {
-        f = __fadd_rn(f, a.bias[gn]);
+    if (bias) {
+        f = __fadd_rn(f, *bias);
     }
-    f = fmaxf(f, a.cmin);
-    f = fminf(f, a.cmax);
+    f = fmaxf(f, cmin);
+    f = fminf(f, cmax);
     return f;
 }
 
-__global__ __launch_bounds__(256) void w4a8_mfma_kernel(W4A8Args a)
+// 32 activation bytes (k = 0..31 of this lane's slice) -> two MFMA operands in the byte order
+// of the decoded weights: (even k of bytes 0-7, odd k of bytes 0-7, even k 8-15, odd k 8-15).
+__device__ __forceinline__ void permute_act(const i32x4 v0, const i32x4 v1, i32x4 &x0, i32x4 &x1)
 {
-    __shared__ int32_t s_part[4][16][16];
+    const uint32_t b0 = v0[0], b1 = v0[1], b2 = v0[2], b3 = v0[3];
+    const uint32_t b4 = v1[0], b5 = v1[1], b6 = v1[2], b7 = v1[3];
+    x0[0] = static_cast<int32_t>(__builtin_amdgcn_perm(b1, b0, 0x06040200u));
+    x0[1] = static_cast<int32_t>(__builtin_amdgcn_perm(b1, b0, 0x07050301u));
+    x0[2] = static_cast<int32_t>(__builtin_amdgcn_perm(b3, b2, 0x06040200u));
+    x0[3] = static_cast<int32_t>(__builtin_amdgcn_perm(b3, b2, 0x07050301u));
+    x1[0] = static_cast<int32_t>(__builtin_amdgcn_perm(b5, b4, 0x06040200u));
+    x1[1] = static_cast<int32_t>(__builtin_amdgcn_perm(b5, b4, 0x07050301u));
+    x1[2] = static_cast<int32_t>(__builtin_amdgcn_perm(b7, b6, 0x06040200u));
+    x1[3] = static_cast<int32_t>(__builtin_amdgcn_perm(b7, b6, 0x07050301u));
+}
+
+// 16 weight bytes (32 nibbles, low nibble = even k) -> signed bytes 16 * (q - 8), as two MFMA
+// operands (lo nibbles then hi nibbles of bytes 0-7, then of bytes 8-15).
+__device__ __forceinline__ void decode_w16(const u32x4 w, i32x4 &q0, i32x4 &q1)
+{
+    q0[0] = static_cast<int32_t>(((w[0] << 4) & 0xf0f0f0f0u) ^ 0x80808080u);
+    q0[1] = static_cast<int32_t>((w[0] & 0xf0f0f0f0u) ^ 0x80808080u);
+    q0[2] = static_cast<int32_t>(((w[1] << 4) & 0xf0f0f0f0u) ^ 0x80808080u);
+    q0[3] = static_cast<int32_t>((w[1] & 0xf0f0f0f0u) ^ 0x80808080u);
+    q1[0] = static_cast<int32_t>(((w[2] << 4) & 0xf0f0f0f0u) ^ 0x80808080u);
+    q1[1] = static_cast<int32_t>((w[2] & 0xf0f0f0f0u) ^ 0x80808080u);
+    q1[2] = static_cast<int32_t>(((w[3] << 4) & 0xf0f0f0f0u) ^ 0x80808080u);
+    q1[3] = static_cast<int32_t>((w[3] & 0xf0f0f0f0u) ^ 0x80808080u);
+}
+
+template <bool kActInLds>
+__global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][2 * kPairsPerBatch][1024];
+    __shared__ __attribute__((aligned(16))) int8_t s_a[kActInLds ? kALdsBytes : 16];
+    __shared__ int32_t s_part[kWaves][16][16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int fr = lane & 15;  // A-operand row (activation) / B-operand column (channel)
+    const int fg = lane >> 4;  // 16-k slot group of the MFMA step
+    const int r8 = lane >> 3;  // row within an 8-row load
+    const int c8 = lane & 7;   // 16-byte chunk within a 128-byte row segment
     const int n0 = blockIdx.x * kNTile;
     const int m0 = blockIdx.y * kRowsPerChunk;
     const int rows = min(kRowsPerChunk, a.M - m0);
 
-    const int fr = lane & 15;  // A-operand row (activation) / B-operand column (channel)
-    const int fg = lane >> 4;  // k group within the 64-k MFMA step
-
-    // This lane's weight row and activation row.
-    const bool w_ok = (n0 + fr) < a.N;
-    const uint8_t *wrow = a.B + static_cast<long long>(w_ok ? n0 + fr : 0) * a.bstride + fg * 16;
-    const bool a_real = fr < rows;
-    const bool a_ones = fr == rows;
-    const int8_t *arow = a.A + static_cast<long long>(a_real ? m0 + fr : 0) * a.lda + fg * 32;
-
-    const int nsteps = a.K / kStepK;
-    const int per_wave = (nsteps + 3) / 4;
-    const int s_begin = wave * per_wave;
-    const int s_end = min(nsteps, s_begin + per_wave);
-
-    const i32x4 neg8 = i32x4{static_cast<int32_t>(0xf8f8f8f8u), static_cast<int32_t>(0xf8f8f8f8u),
-                             static_cast<int32_t>(0xf8f8f8f8u), static_cast<int32_t>(0xf8f8f8f8u)};
-    const i32x4 ones = i32x4{0x01010101, 0x01010101, 0x01010101, 0x01010101};
-    i32x4 acc = i32x4{0, 0, 0, 0};
-
-    for (int sb = s_begin; sb < s_end; sb += kBatch) {
-        u32x4 wv[kBatch];
-        i32x4 av0[kBatch], av1[kBatch];
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            const int s = sb + i;
-            if (s < s_end && w_ok) {
-                wv[i] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4 *>(wrow + static_cast<long long>(s) * (kStepK / 2)));
-            } else {
-                wv[i] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            const int s = sb + i;
-            if (s < s_end && a_real) {
-                const int8_t *p = arow + static_cast<long long>(s) * kStepK;
-                av0[i] = *reinterpret_cast<const i32x4 *>(p);
-                av1[i] = *reinterpret_cast<const i32x4 *>(p + 16);
-            } else if (a_ones) {
-                av0[i] = ones;
-                av1[i] = ones;
-            } else {
-                av0[i] = i32x4{0, 0, 0, 0};
-                av1[i] = i32x4{0, 0, 0, 0};
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kBatch; ++i) {
-            if (sb + i >= s_end) {
-                break;
-            }
-            // Weight nibbles -> unsigned bytes: lo = even k, hi = odd k of each byte.
-            i32x4 q0, q1;
-            q0[0] = static_cast<int32_t>(wv[i][0] & 0x0f0f0f0fu);
-            q0[1] = static_cast<int32_t>((wv[i][0] >> 4) & 0x0f0f0f0fu);
-            q0[2] = static_cast<int32_t>(wv[i][1] & 0x0f0f0f0fu);
-            q0[3] = static_cast<int32_t>((wv[i][1] >> 4) & 0x0f0f0f0fu);
-            q1[0] = static_cast<int32_t>(wv[i][2] & 0x0f0f0f0fu);
-            q1[1] = static_cast<int32_t>((wv[i][2] >> 4) & 0x0f0f0f0fu);
-            q1[2] = static_cast<int32_t>(wv[i][3] & 0x0f0f0f0fu);
-            q1[3] = static_cast<int32_t>((wv[i][3] >> 4) & 0x0f0f0f0fu);
-            // Activations in the same order: (even bytes, odd bytes) of each 8-byte run.
-            i32x4 x0, x1;
-            const uint32_t a0 = static_cast<uint32_t>(av0[i][0]), a1 = static_cast<uint32_t>(av0[i][1]);
-            const uint32_t a2 = static_cast<uint32_t>(av0[i][2]), a3 = static_cast<uint32_t>(av0[i][3]);
-            const uint32_t a4 = static_cast<uint32_t>(av1[i][0]), a5 = static_cast<uint32_t>(av1[i][1]);
-            const uint32_t a6 = static_cast<uint32_t>(av1[i][2]), a7 = static_cast<uint32_t>(av1[i][3]);
-            x0[0] = static_cast<int32_t>(__builtin_amdgcn_perm(a1, a0, 0x06040200u));
-            x0[1] = static_cast<int32_t>(__builtin_amdgcn_perm(a1, a0, 0x07050301u));
-            x0[2] = static_cast<int32_t>(__builtin_amdgcn_perm(a3, a2, 0x06040200u));
-            x0[3] = static_cast<int32_t>(__builtin_amdgcn_perm(a3, a2, 0x07050301u));
-            x1[0] = static_cast<int32_t>(__builtin_amdgcn_perm(a5, a4, 0x06040200u));
-            x1[1] = static_cast<int32_t>(__builtin_amdgcn_perm(a5, a4, 0x07050301u));
-            x1[2] = static_cast<int32_t>(__builtin_amdgcn_perm(a7, a6, 0x06040200u));
-            x1[3] = static_cast<int32_t>(__builtin_amdgcn_perm(a7, a6, 0x07050301u));
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, q0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, neg8, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, q1, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, neg8, acc, 0, 0, 0);
-        }
-    }
-
-    // lane holds rows 4*fg + r, column fr of the 16x16 partial
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        s_part[wave][4 * fg + r][fr] = acc[r];
-    }
-    __syncthreads();
+    // Epilogue operands of output (orow, ocol), fetched first so they are in flight with the
+    // weight stream.
     const int orow = tid >> 4;
     const int ocol = tid & 15;
-    const int32_t total = static_cast<int32_t>(
-        static_cast<uint32_t>(s_part[0][orow][ocol]) + static_cast<uint32_t>(s_part[1][orow][ocol]) +
-        static_cast<uint32_t>(s_part[2][orow][ocol]) + static_cast<uint32_t>(s_part[3][orow][ocol]));
+    const bool out_ok = tid < 256 && orow < rows && n0 + ocol < a.N;
+    float p_sb = 0.f, p_sa = 0.f, p_bias = 0.f, p_c = 0.f;
+    int32_t p_za = 0;
+    if (out_ok) {
+        const int gm = m0 + orow, gn = n0 + ocol;
+        p_sb = a.scale_b[gn];
+        p_sa = a.scale_a[gm];
+        p_za = a.zp_a[gm];
+        if (a.bias) {
+            p_bias = a.bias[gn];
+        }
+        if (a.C) {
+            p_c = a.C[static_cast<long long>(gm) * a.ldc + gn];
+        }
+    }
+
+    const int npairs = a.K / kPairK;
+    const int ppw = (npairs + kWaves - 1) / kWaves;
+    const int p_begin = min(npairs, wave * ppw);
+    const int p_end = min(npairs, p_begin + ppw);
+
+    const i32x4 ones = i32x4{0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    const i32x4 zero = i32x4{0, 0, 0, 0};
+    const bool a_real = fr < rows;
+    const bool a_ones = fr == rows;
+
+    if constexpr (kActInLds) {
+        // Activations [rows, K] -> LDS (row stride K), loaded before the weights are issued.
+        const int cpr = a.K / 16;
+        for (int c = tid; c < rows * cpr; c += kWaves * 64) {
+            const int r = c / cpr;
+            const int off = (c - r * cpr) * 16;
+            *reinterpret_cast<i32x4 *>(&s_a[r * a.K + off]) =
+                *reinterpret_cast<const i32x4 *>(a.A + static_cast<long long>(m0 + r) * a.lda + off);
+        }
+        __syncthreads();
+    }
+
+    i32x4 acc0 = zero, acc1 = zero;
+    for (int pb = p_begin; pb < p_end; pb += kPairsPerBatch) {
+        // activations of this batch (register path): 32 bytes per lane per step
+        i32x4 av[2 * kPairsPerBatch][2];
+        if constexpr (!kActInLds) {
+#pragma unroll
+            for (int s = 0; s < 2 * kPairsPerBatch; ++s) {
+                const int pair = pb + (s >> 1);
+                if (a_real && pair < p_end) {
+                    const int8_t *p = a.A + static_cast<long long>(m0 + fr) * a.lda +
+                                      pair * kPairK + (s & 1) * 128 + fg * 32;
+                    av[s][0] = *reinterpret_cast<const i32x4 *>(p);
+                    av[s][1] = *reinterpret_cast<const i32x4 *>(p + 16);
+                } else {
+                    av[s][0] = a_ones ? ones : zero;
+                    av[s][1] = a_ones ? ones : zero;
+                }
+            }
+        }
+        // weights of this batch: load j covers rows 8 * (j & 1) .. +8, pair pb + j / 2
+        u32x4 wr[2 * kPairsPerBatch];
+#pragma unroll
+        for (int j = 0; j < 2 * kPairsPerBatch; ++j) {
+            const int pair = pb + (j >> 1);
+            const int row = 8 * (j & 1) + r8;
+            const int grow = n0 + row < a.N ? n0 + row : n0;
+            if (pair < p_end) {
+                wr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+                    a.B + static_cast<long long>(grow) * a.bstride + pair * (kPairK / 2) + c8 * 16));
+            } else {
+                wr[j] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // q = 8
+            }
+        }
+#pragma unroll
+        for (int pp = 0; pp < kPairsPerBatch; ++pp) {
+            // stage this pair: (row, chunk) at row * 128 + ((chunk ^ (row & 7)) << 4)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = 2 * pp + h;
+                *reinterpret_cast<u32x4 *>(&s_w[wave][j][r8 * 128 + ((c8 ^ r8) << 4)]) = wr[j];
+            }
+            const int pair = pb + pp;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                i32x4 v0, v1;
+                if constexpr (kActInLds) {
+                    if (a_real && pair < p_end) {
+                        const int8_t *p = &s_a[fr * a.K + pair * kPairK + h * 128 + fg * 32];
+                        v0 = *reinterpret_cast<const i32x4 *>(p);
+                        v1 = *reinterpret_cast<const i32x4 *>(p + 16);
+                    } else {
+                        v0 = a_ones ? ones : zero;
+                        v1 = v0;
+                    }
+                } else {
+                    v0 = av[2 * pp + h][0];
+                    v1 = av[2 * pp + h][1];
+                }
+                i32x4 x0, x1, q0, q1;
+                permute_act(v0, v1, x0, x1);
+                const int jj = 2 * pp + (fr >> 3);
+                const int rr = fr & 7;
+                const int c = 4 * h + fg;
+                decode_w16(*reinterpret_cast<const u32x4 *>(&s_w[wave][jj][rr * 128 + ((c ^ rr) << 4)]),
+                           q0, q1);
+                acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, q0, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, q1, acc1, 0, 0, 0);
+            }
+        }
+    }
+
+    // lane holds rows 4 * fg + r, column fr of this wave's 16x16 partial
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        s_part[wave][4 * fg + r][fr] = acc0[r] + acc1[r];
+    }
     __syncthreads();
-    s_part[0][orow][ocol] = total;
-    __syncthreads();
-    const int gm = m0 + orow;
-    const int gn = n0 + ocol;
-    if (orow < rows && gn < a.N) {
-        const int32_t rsum = s_part[0][rows][ocol];
-        a.D[static_cast<long long>(gm) * a.ldd + gn] = epilogue_f32(a, gm, gn, total, rsum);
+    if (out_ok) {
+        uint32_t tot = 0, rs = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            tot += static_cast<uint32_t>(s_part[w][orow][ocol]);
+            rs += static_cast<uint32_t>(s_part[w][rows][ocol]);
+        }
+        const int gm = m0 + orow, gn = n0 + ocol;
+        a.D[static_cast<long long>(gm) * a.ldd + gn] = epilogue_f32(
+            static_cast<int32_t>(tot) >> 4, static_cast<int32_t>(rs) >> 4, p_za, p_sa, p_sb,
+            a.C ? &p_c : nullptr, a.bias ? &p_bias : nullptr, a.cmin, a.cmax);
     }
 }
 
@@ -201,8 +273,10 @@ __global__ __launch_bounds__(256) void w4a8_generic_kernel(W4A8Args a)
         acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * lo);
         acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k + 1]) * hi);
     }
-    a.D[static_cast<long long>(gm) * a.ldd + gn] =
-        epilogue_f32(a, gm, gn, static_cast<int32_t>(acc), static_cast<int32_t>(rsum));
+    a.D[static_cast<long long>(gm) * a.ldd + gn] = epilogue_f32(
+        static_cast<int32_t>(acc), static_cast<int32_t>(rsum), a.zp_a[gm], a.scale_a[gm],
+        a.scale_b[gn], a.C ? &a.C[static_cast<long long>(gm) * a.ldc + gn] : nullptr,
+        a.bias ? &a.bias[gn] : nullptr, a.cmin, a.cmax);
 }
 
 }  // namespace
@@ -298,14 +372,20 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950_async(
     a.zp_a = params->zero_point_a;
     a.scale_b = params->scale_b;
     hipStream_t s = as_stream(stream);
-    const bool fast = (k % kStepK == 0) && (lda % 16 == 0) && ((ldb / 2) % 16 == 0) &&
-                      aligned16(A) && aligned16(B);
+    const bool fast = (k % kPairK == 0) && k <= 65536 && (lda % 16 == 0) &&
+                      ((ldb / 2) % 16 == 0) && aligned16(A) && aligned16(B) &&
+                      (m + kRowsPerChunk - 1) / kRowsPerChunk < 65536;
     if (fast) {
         const unsigned gx = static_cast<unsigned>((n + kNTile - 1) / kNTile);
         const unsigned long long gy = (m + kRowsPerChunk - 1) / kRowsPerChunk;
-        TQT_REQUIRE(gy < 65536, "m too large for the decode path");
-        hipLaunchKernelGGL(w4a8_mfma_kernel, dim3(gx, static_cast<unsigned>(gy)), dim3(256), 0, s,
-                           a);
+        const size_t rows_max = m < static_cast<size_t>(kRowsPerChunk) ? m : kRowsPerChunk;
+        if (rows_max * k <= static_cast<size_t>(kALdsBytes)) {
+            hipLaunchKernelGGL(w4a8_mfma_kernel<true>, dim3(gx, static_cast<unsigned>(gy)),
+                               dim3(kWaves * 64), 0, s, a);
+        } else {
+            hipLaunchKernelGGL(w4a8_mfma_kernel<false>, dim3(gx, static_cast<unsigned>(gy)),
+                               dim3(kWaves * 64), 0, s, a);
+        }
     } else {
         const long long total = static_cast<long long>(m) * static_cast<long long>(n);
         const long long blocks = (total + 255) / 256;
@@ -322,6 +402,9 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950(
     float clamp_min, float clamp_max, const struct tqt_qai8dx_qsi4cx_params *params)
 {
     if (!params) {
+        return;
+    }
+    if (m == 0 || n == 0) {
         return;
     }
     tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950_async(

@@ -508,6 +508,9 @@ void tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t m, size_t n, size_t k, cons
                                               size_t ldc, void *D, size_t ldd, int32_t clamp_min,
                                               int32_t clamp_max)
 {
+    if (m == 0 || n == 0) {
+        return;
+    }
     tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950_async(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C,
                                                    ldc, D, ldd, clamp_min, clamp_max, nullptr);
     finish_sync(nullptr, "tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950");
@@ -618,6 +621,9 @@ void tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
     int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qai8_qsi8cx_params *params)
 {
     if (!params) {
+        return;
+    }
+    if (m == 0 || n == 0) {
         return;
     }
     tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950_async(
@@ -752,6 +758,9 @@ void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx95
     const tqt_conv_params *conv_params, const struct tqt_qai8_qai8_qsi8cx_params *quant_params)
 {
     if (!conv_params || !quant_params) {
+        return;
+    }
+    if (m == 0 || n == 0) {
         return;
     }
     tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950_async(
