@@ -261,6 +261,89 @@ def bench_clamp(torch, mod, lib, timer, warmup, steps, rng):
                 ops=ops, copies=1)
 
 
+def bench_copy(torch, timer, warmup, steps):
+    """Plain streaming kernel of known traffic (bitwise_not over 256 MB of int32): reads and
+    writes exactly `nbytes` each per launch; calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    nbytes = 256 << 20
+    src = torch.zeros(nbytes // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+
+    def launch(i):
+        torch.bitwise_not(src, out=dst)
+
+    ms = timer.run(launch, 1, warmup, steps)
+    return dict(ms=ms, bytes=2 * nbytes, read=nbytes, write=nbytes, copies=1)
+
+
+# ------------------------------------------------------------------------------------------
+# HBM traffic per launch from rocprofv3 counters (FETCH_SIZE, then WRITE_SIZE)
+# ------------------------------------------------------------------------------------------
+
+PMC_LEGS = "w8a8,w4a8,copy"
+KERNEL_KEYS = {"w8a8": "int8_mfma_kernel", "w4a8": "w4a8_mfma_kernel", "copy": "bitwise_not"}
+
+
+def pmc_pass(counter, timeout_s=120):
+    """One rocprofv3 --pmc run of this script's PMC_LEGS in a child process; returns
+    {leg: mean counter value per dispatch (KiB)} or None."""
+    import csv
+    import glob
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None
+    out = tempfile.mkdtemp(prefix="tqt_pmc_", dir="/tmp")
+    cmd = [prof, "--pmc", counter, "-d", out, "-o", "pmc", "--output-format", "csv", "--",
+           sys.executable, os.path.abspath(__file__), "--only", PMC_LEGS, "--steps", "6",
+           "--warmup", "2"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
+                            stderr=subprocess.DEVNULL, start_new_session=True)
+    try:
+        proc.wait(timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.wait()
+        shutil.rmtree(out, ignore_errors=True)
+        return None
+    vals = {leg: [] for leg in KERNEL_KEYS}
+    for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
+        with open(path, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row.get("Kernel_Name", "")
+                for leg, key in KERNEL_KEYS.items():
+                    if key in name:
+                        vals[leg].append(float(row["Counter_Value"]))
+    shutil.rmtree(out, ignore_errors=True)
+    if not all(vals.values()):
+        return None
+    return {leg: sum(v) / len(v) for leg, v in vals.items()}
+
+
+def hbm_traffic():
+    """HBM bytes per launch of the W8A8 and W4A8 kernels: FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by bytes / counter of the copy kernel, whose traffic is known."""
+    fetch = pmc_pass("FETCH_SIZE")
+    write = pmc_pass("WRITE_SIZE") if fetch else None
+    if not fetch or not write:
+        return None
+    nbytes = 256 << 20
+    f_scale = nbytes / fetch["copy"]
+    w_scale = nbytes / write["copy"]
+    res = {"fetch_scale_bytes_per_KiB": round(f_scale, 2),
+           "write_scale_bytes_per_KiB": round(w_scale, 2)}
+    for leg in ("w8a8", "w4a8"):
+        res[leg] = {"read": fetch[leg] * f_scale, "write": write[leg] * w_scale,
+                    "total": fetch[leg] * f_scale + write[leg] * w_scale}
+    return res
+
+
 # ------------------------------------------------------------------------------------------
 # CPU baseline (oracle restatement of the reference kernel; bounded sample)
 # ------------------------------------------------------------------------------------------
@@ -295,6 +378,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes that measure HBM traffic")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,conv,clamp,copy): "
+                         "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: these kernels run on a single MI355X and this "
@@ -312,6 +400,24 @@ def main():
     rng = np.random.default_rng(42)
     K, W = args.steps, args.warmup
 
+    if args.only:
+        legs = {
+            "w8a8": lambda: bench_w8a8(torch, mod, lib, timer, W, K, rng),
+            "w4a8": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1),
+            "w4a8m4": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 4),
+            "w4a8m8": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 8),
+            "w4a16": lambda: bench_w4a16(torch, mod, lib, timer, W, K, rng),
+            "conv": lambda: bench_conv(torch, mod, lib, timer, W, K, rng),
+            "clamp": lambda: bench_clamp(torch, mod, lib, timer, W, K, rng),
+            "copy": lambda: bench_copy(torch, timer, W, K),
+        }
+        with torch.cuda.stream(stream):
+            for leg in args.only.split(","):
+                r = legs[leg]()
+                print(json.dumps({"leg": leg, "us_per_launch": round(r["ms"] * 1e3, 3),
+                                  "bytes": r["bytes"], "copies": r["copies"]}), flush=True)
+        return
+
     with torch.cuda.stream(stream):
         w8 = bench_w8a8(torch, mod, lib, timer, W, K, rng)
         w4 = {mm: bench_w4a8(torch, mod, lib, timer, W, K, rng, mm) for mm in (1, 4, 8)}
@@ -320,6 +426,9 @@ def main():
         cl = bench_clamp(torch, mod, lib, timer, W, K, rng)
 
     w41 = w4[1]
+    traffic = None if args.no_traffic else hbm_traffic()
+    t_w8 = round(traffic["w8a8"]["total"]) if traffic else None
+    t_w4 = round(traffic["w4a8"]["total"]) if traffic else None
     out = {
         "metric": "W4A8 GEMV HBM GB/s (M=1) + W8A8 GEMM int8 TOPS (M=512), % roofline",
         "value": round(w8["tops"], 3),
@@ -339,13 +448,13 @@ def main():
                    "M": 512, "K": 4096, "N": 4096},
         "roofline": {"bound": "mfma", "achieved": round(w8["tops"], 3), "peak": INT8_PEAK_TOPS,
                      "unit": "TOPS", "frac": round(w8["tops"] / INT8_PEAK_TOPS, 4),
-                     "traffic": None},
+                     "traffic": t_w8, "algorithmic_bytes": w8["bytes"]},
         "w4a8": {
             "workload": "gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt M=1 K=4096 N=11008 (W4A8 decode)",
             "value": round(w41["gbs"], 2), "unit": "GB/s", "us_per_launch": round(w41["ms"] * 1e3, 3),
             "roofline": {"bound": "hbm", "achieved": round(w41["gbs"], 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(w41["gbs"] / HBM_PEAK_GBS, 4),
-                         "traffic": None},
+                         "traffic": t_w4, "algorithmic_bytes": w41["bytes"]},
             "M4": {"GB/s": round(w4[4]["gbs"], 2), "us": round(w4[4]["ms"] * 1e3, 3),
                    "frac": round(w4[4]["gbs"] / HBM_PEAK_GBS, 4)},
             "M8": {"GB/s": round(w4[8]["gbs"], 2), "us": round(w4[8]["ms"] * 1e3, 3),
@@ -364,6 +473,15 @@ def main():
                                               "mfma_frac": round(cv["tops"] / INT8_PEAK_TOPS, 4)},
         },
     }
+    if traffic:
+        out["traffic_detail"] = {
+            "source": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE (KiB per dispatch), scaled "
+                      "by the counters of a 256 MB bitwise_not copy kernel",
+            "fetch_scale_bytes_per_KiB": traffic["fetch_scale_bytes_per_KiB"],
+            "write_scale_bytes_per_KiB": traffic["write_scale_bytes_per_KiB"],
+            "w8a8": {k: round(v) for k, v in traffic["w8a8"].items()},
+            "w4a8": {k: round(v) for k, v in traffic["w4a8"].items()},
+        }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(w8)
     print(json.dumps(out), flush=True)
