@@ -3,12 +3,17 @@
 //   gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt     (B is [n, k], requantized int8 out)
 //   igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt  (A gathered from an NDHWC image)
 //
-// Fast path: a workgroup of 256 threads (4 wave64s in a 2x2 grid) computes a BM x 128 output
-// tile. K advances 64 bytes at a time through double-buffered LDS tiles; each wave issues
-// v_mfma_i32_16x16x64_i8 on 16x16 sub-tiles. The int32 epilogue (C, bias, requantization,
-// saturation, clamp) is fused into the store. A generic one-thread-per-output kernel covers
-// shapes the fast path does not accept (unaligned pointers or strides, K not a multiple of 16,
-// channel counts not a multiple of 16).
+// Three kernels, chosen per call:
+//   * int8_stream_kernel (plain A, B = [n, k], k % 128 == 0: W8A8 at its config): a 4-deep
+//     ring of LDS stages filled by direct global->LDS loads, v_mfma_i32_32x32x32_i8, XCD-aware
+//     tile order (described at the kernel);
+//   * int8_mfma_kernel (igemmcl, the other 16-byte-aligned shapes, clamp_i32's [k, n] B): 256 threads
+//     (4 wave64s in a 2x2 grid) on a BM x 128 tile, k in steps of 64 bytes through double-buffered
+//     LDS tiles, v_mfma_i32_16x16x64_i8;
+//   * int8_generic_kernel: one thread per output for unaligned pointers or strides, k not a
+//     multiple of 16, or channel counts not a multiple of 16.
+// All three accumulate exactly in int32 and fuse the epilogue (C, bias, requantization,
+// saturation, clamp) into the store.
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
 #include "tqt_gemm_clamp_i32_i8_i8_mfma_gfx950.h"
@@ -316,6 +321,279 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Streaming kernel for B = [n, k] (W8A8 and igemmcl), k % 128 == 0.
+//
+// A workgroup of 4 wave64s (2 x 2) owns a BM x 128 output tile (BM = 64 or 128) and walks k in
+// stages of 128 bytes through a 4-deep ring of LDS stages filled by direct global->LDS loads
+// (global_load_lds_dwordx4: lane i of an instruction writes 16 bytes at LDS base + 16 * i, so
+// no VGPRs carry the tiles). Each LDS row holds 128 k-bytes of one A row or one B row; its eight
+// 16-byte chunks are stored XOR-swizzled with (row >> 1) & 7, which makes both the loads (8 rows
+// x 128 B per instruction, whole cache lines) and the MFMA operand reads (ds_read_b128 of 32
+// rows) conflict-free. Waves wait for their own loads with an explicit vmcnt and meet at a plain
+// s_barrier: __syncthreads() would also drain every load still in flight for later stages.
+// v_mfma_i32_32x32x32_i8 accumulates exactly in int32; the epilogue is fused into the store.
+// Workgroups are ordered for the 8 XCDs: block b runs on XCD b % 8, and each XCD receives a
+// contiguous range of tiles (M fastest), so its workgroups share their B rows (and A) in the
+// XCD's L2.
+// ---------------------------------------------------------------------------------------------
+constexpr int kSK = 128;  // k bytes per pipeline stage
+
+// Source of padding taps of the implicit convolution (global->LDS loads cannot write zeros).
+__device__ __attribute__((aligned(16))) int8_t g_zero16[16];
+
+__host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm)
+{
+    // s_waitcnt immediate (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    return (vm & 15) | (7 << 4) | ((vm >> 4) << 14);
+}
+
+template <int BM, int AM, int EPI>
+__global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int tiles_m, int tiles,
+                                                               int per_xcd)
+{
+    constexpr int WM = BM / 2;             // rows per wave
+    constexpr int MF = WM / 32;            // 32-row fragments per wave
+    constexpr int NF = 2;                  // 32-column fragments per wave (64 columns)
+    constexpr int A_DMA = BM / 32;         // 1 KB (8-row) load instructions per wave per stage
+    constexpr int B_DMA = kBN / 32;
+    constexpr int PER_STAGE = A_DMA + B_DMA;
+    constexpr int SA = BM * kSK;
+    constexpr int SB = kBN * kSK;
+
+    __shared__ __attribute__((aligned(16))) int8_t sa0[SA], sa1[SA], sa2[SA], sa3[SA];
+    __shared__ __attribute__((aligned(16))) int8_t sb0[SB], sb1[SB], sb2[SB], sb3[SB];
+    __shared__ int32_t s_mult[kBN];
+    __shared__ int32_t s_shift[kBN];
+
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= tiles) {
+        return;
+    }
+    const int tile_m = t % tiles_m;
+    const int m0 = tile_m * BM;
+    const int n0 = (t / tiles_m) * kBN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+
+    if constexpr (EPI == EPI_REQUANT_I8) {
+        if (tid < kBN && n0 + tid < a.N) {
+            column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, n0 + tid,
+                                  s_mult[tid], s_shift[tid]);
+        }
+    }
+
+    // Load-side lane roles: lane = 8 * row-in-block + LDS slot; the slot holds k-chunk
+    // slot ^ ((row >> 1) & 7) of that row.
+    const int lrow = lane >> 3;
+    const int lslot = lane & 7;
+    const int8_t *a_row[A_DMA];
+    int a_chunk[A_DMA];
+    int a_id0[A_DMA], a_ih0[A_DMA], a_iw0[A_DMA];
+#pragma unroll
+    for (int j = 0; j < A_DMA; ++j) {
+        const int r = 8 * (wave * A_DMA + j) + lrow;
+        a_chunk[j] = lslot ^ ((r >> 1) & 7);
+        const int gm = min(m0 + r, a.M - 1);
+        if constexpr (AM == A_MATRIX) {
+            a_row[j] = a.A + static_cast<long long>(gm) * a.lda + a_chunk[j] * 16;
+            a_id0[j] = a_ih0[j] = a_iw0[j] = 0;
+        } else {
+            const ConvGeom &g = a.cv;
+            const long long p = a.p0 + gm;
+            const long long ohw = static_cast<long long>(g.OH) * g.OW;
+            const int od = static_cast<int>(p / ohw);
+            const int oh = static_cast<int>((p / g.OW) % g.OH);
+            const int ow = static_cast<int>(p % g.OW);
+            a_id0[j] = od * g.SD - g.PD;
+            a_ih0[j] = oh * g.SH - g.PH;
+            a_iw0[j] = ow * g.SW - g.PW;
+            a_row[j] = nullptr;
+        }
+    }
+    const int8_t *b_row[B_DMA];
+#pragma unroll
+    for (int j = 0; j < B_DMA; ++j) {
+        const int r = 8 * (wave * B_DMA + j) + lrow;
+        const int gn = min(n0 + r, a.N - 1);
+        b_row[j] = a.B + static_cast<long long>(gn) * a.ldb + (lslot ^ ((r >> 1) & 7)) * 16;
+    }
+
+    auto issue = [&](int st, int8_t *sa, int8_t *sb) {
+        const int k0 = st * kSK;
+#pragma unroll
+        for (int j = 0; j < A_DMA; ++j) {
+            const int8_t *src;
+            if constexpr (AM == A_MATRIX) {
+                src = a_row[j] + k0;
+            } else {
+                const ConvGeom &g = a.cv;
+                const int k = k0 + a_chunk[j] * 16;
+                const int tap = k / g.ICg;
+                const int ic = k - tap * g.ICg;
+                const int kw = tap % g.KW;
+                const int t2 = tap / g.KW;
+                const int kh = t2 % g.KH;
+                const int kd = t2 / g.KH;
+                const int id = a_id0[j] + kd * g.DD;
+                const int ih = a_ih0[j] + kh * g.DH;
+                const int iw = a_iw0[j] + kw * g.DW;
+                const bool inb = id >= 0 && id < g.ID && ih >= 0 && ih < g.IH && iw >= 0 &&
+                                 iw < g.IW;
+                src = inb ? a.A + ((static_cast<long long>(id) * g.IH + ih) * g.IW + iw) * g.IC + ic
+                          : g_zero16;
+            }
+#if defined(__HIP_DEVICE_COMPILE__)
+            __builtin_amdgcn_global_load_lds(src, sa + (wave * A_DMA + j) * 1024, 16, 0, 0);
+#endif
+        }
+#pragma unroll
+        for (int j = 0; j < B_DMA; ++j) {
+#if defined(__HIP_DEVICE_COMPILE__)
+            __builtin_amdgcn_global_load_lds(b_row[j] + k0, sb + (wave * B_DMA + j) * 1024, 16, 0,
+                                             0);
+#endif
+        }
+    };
+
+    i32x16 acc[MF][NF];
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[i][j][r] = 0;
+            }
+        }
+    }
+
+    // MFMA operand lanes: row r32 of a 32-row fragment, k-chunk 2 * step + h.
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    constexpr int KS = kSK / 32;  // MFMA k-steps per stage
+    auto compute = [&](const int8_t *sa, const int8_t *sb) {
+        // All operand reads of the stage first, so their LDS latency overlaps.
+        i32x4 fa[KS][MF], fb[KS][NF];
+#pragma unroll
+        for (int step = 0; step < KS; ++step) {
+            const int c = 2 * step + h;
+#pragma unroll
+            for (int i = 0; i < MF; ++i) {
+                const int row = wm * WM + 32 * i + r32;
+                fa[step][i] =
+                    *reinterpret_cast<const i32x4 *>(sa + row * kSK + ((c ^ ((row >> 1) & 7)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < NF; ++j) {
+                const int row = wn * 64 + 32 * j + r32;
+                fb[step][j] =
+                    *reinterpret_cast<const i32x4 *>(sb + row * kSK + ((c ^ ((row >> 1) & 7)) << 4));
+            }
+        }
+#pragma unroll
+        for (int step = 0; step < KS; ++step) {
+#pragma unroll
+            for (int i = 0; i < MF; ++i) {
+#pragma unroll
+                for (int j = 0; j < NF; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[step][i], fb[step][j],
+                                                                      acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        // Keep that order through instruction scheduling: DS reads, then MFMAs.
+        __builtin_amdgcn_sched_group_barrier(0x100, KS * (MF + NF), 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, KS * MF * NF, 0);
+    };
+
+    const int nst = a.K / kSK;
+    // One pipeline step: wait until this wave's loads of stage st landed (the stages issued after
+    // it may stay in flight), meet the other waves, refill the buffer everyone finished reading
+    // in the previous step with stage st + 3, then compute stage st.
+    auto step = [&](int st, const int8_t *ca, const int8_t *cb, int8_t *na, int8_t *nb) {
+        if (st >= nst) {
+            return;
+        }
+        const int ahead = min(2, nst - 1 - st);
+        if (ahead == 2) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * PER_STAGE));
+        } else if (ahead == 1) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PER_STAGE));
+        } else {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (st + 3 < nst) {
+            issue(st + 3, na, nb);
+        }
+        compute(ca, cb);
+    };
+
+    if (nst > 0) {
+        issue(0, sa0, sb0);
+    }
+    if (nst > 1) {
+        issue(1, sa1, sb1);
+    }
+    if (nst > 2) {
+        issue(2, sa2, sb2);
+    }
+    for (int st = 0; st < nst; st += 4) {
+        step(st, sa0, sb0, sa3, sb3);
+        step(st + 1, sa1, sb1, sa0, sb0);
+        step(st + 2, sa2, sb2, sa1, sb1);
+        step(st + 3, sa3, sb3, sa2, sb2);
+    }
+    __syncthreads();  // s_mult / s_shift visible even when k == 0
+
+    // Epilogue: lane holds D[8 * (r / 4) + 4 * h + r % 4][r32] of each 32 x 32 fragment.
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        const int lc = wn * 64 + 32 * j + r32;
+        const int gn = n0 + lc;
+        if (gn >= a.N) {
+            continue;
+        }
+        const uint32_t bias = a.bias ? static_cast<uint32_t>(a.bias[gn]) : 0u;
+        int32_t mult = 0, shift = 0;
+        if constexpr (EPI == EPI_REQUANT_I8) {
+            mult = s_mult[lc];
+            shift = s_shift[lc];
+        }
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (gm >= a.M) {
+                    continue;
+                }
+                uint32_t v = static_cast<uint32_t>(acc[i][j][r]) + bias;
+                if (a.C) {
+                    v += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+                }
+                const long long drow = a.d_row0 + gm;
+                if constexpr (EPI == EPI_CLAMP_I32) {
+                    int32_t x = static_cast<int32_t>(v);
+                    x = x < a.cmin ? a.cmin : x;
+                    x = x > a.cmax ? a.cmax : x;
+                    static_cast<int32_t *>(a.D)[drow * a.ldd + gn] = x;
+                } else {
+                    static_cast<int8_t *>(a.D)[drow * a.ldd + gn] =
+                        requant_dev(static_cast<int32_t>(v), mult, shift, a.zp_d, a.cmin, a.cmax);
+                }
+            }
+        }
+    }
+}
+
 // Generic path: one thread per output, any strides and any K.
 template <int AM, int BMd, int EPI>
 __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
@@ -381,11 +659,44 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     }
 }
 
+template <int AM, int EPI>
+void launch_stream(const Int8Args &a, hipStream_t stream)
+{
+    const long long tiles_n = (a.N + kBN - 1) / kBN;
+    const long long tm128 = (a.M + 127) / 128;
+    const long long tm64 = (a.M + 63) / 64;
+    // 128-row tiles when they still give most of the 256 CUs a workgroup.
+    const bool big = tm128 * tiles_n >= 160;
+    const long long tiles_m = big ? tm128 : tm64;
+    const long long tiles = tiles_m * tiles_n;
+    const long long per_xcd = (tiles + 7) / 8;
+    TQT_REQUIRE(tiles < (1ll << 30), "grid too large");
+    if (big) {
+        hipLaunchKernelGGL((int8_stream_kernel<128, AM, EPI>), dim3(8 * per_xcd), dim3(kThreads), 0,
+                           stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
+                           static_cast<int>(per_xcd));
+    } else {
+        hipLaunchKernelGGL((int8_stream_kernel<64, AM, EPI>), dim3(8 * per_xcd), dim3(kThreads), 0,
+                           stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
+                           static_cast<int>(per_xcd));
+    }
+}
+
 template <int AM, int BMd, int EPI>
 void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *where)
 {
     if (a.M <= 0 || a.N <= 0) {
         return;
+    }
+    // The streaming kernel is for plain matrices: for the implicit convolution (k = 1152 at the
+    // config, nine stages) its 4-deep ring never reaches steady state and the double-buffered
+    // kernel is faster.
+    if constexpr (BMd == B_NK && AM == A_MATRIX) {
+        if (fast && a.K % kSK == 0) {
+            launch_stream<AM, EPI>(a, stream);
+            check_launch(where);
+            return;
+        }
     }
     if (fast) {
         const int tiles_n = (a.N + kBN - 1) / kBN;
