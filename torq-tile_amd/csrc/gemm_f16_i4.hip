@@ -1,6 +1,8 @@
 // gemm_1xnbias_clamp_f16_f16_qsi4c2t (W4A16, block-quantized int4 weights) on gfx950.
 //
-// Fast path (bl == 32, k % 128 == 0, k <= 4096): a workgroup of 8 wave64s owns a strip of
+// Two MFMA kernels share the math below: w4a16_regs_kernel (the strip kernel, for k in {2048,
+// 3072, 4096}: whole CUs, at most four tiles each, two tiles in flight) and w4a16_mfma_kernel
+// (any other k % 128 == 0, k <= 4096). In w4a16_mfma_kernel a workgroup of 8 wave64s owns a strip of
 // 16-channel weight tiles for one group of 32 activation rows. Wave w owns a fixed slice of k
 // (a run of 32-wide scale blocks) and keeps its slice of A (32 rows, f16) in registers for the
 // whole strip, so A is read from memory once per workgroup. For each 16-channel tile:
@@ -114,20 +116,27 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
     const int g_begin = min(ngroups, wave * gpw);
     const int g_cnt = min(ngroups, g_begin + gpw) - g_begin;
 
-    // A operand for every block of the slice and both 16-row tiles.
+    // A operand for every block of the slice and both 16-row tiles. Unconditional loads from
+    // clamped addresses keep them all in flight together; unused ones are zeroed afterwards.
+    u32x4 ra[kMaxGroupsPerWave * 4][2];
+#pragma unroll
+    for (int j = 0; j < kMaxGroupsPerWave * 4; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int row = min(mg0 + mt * 16 + fr, a.M - 1);
+            const int jj = min(j, max(g_cnt * 4 - 1, 0));
+            const int k = min((g_begin * 4 + jj) * 32, max(a.K - 32, 0)) + fg * 8;
+            ra[j][mt] = *reinterpret_cast<const u32x4 *>(a.A + static_cast<long long>(row) * a.lda + k);
+        }
+    }
     f16x8 fa[kMaxGroupsPerWave * 4][2];
 #pragma unroll
     for (int j = 0; j < kMaxGroupsPerWave * 4; ++j) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            const int row = mg0 + mt * 16 + fr;
-            if (j < g_cnt * 4 && row < a.M) {
-                const int k = (g_begin * 4 + j) * 32 + fg * 8;
-                fa[j][mt] = permute_a(*reinterpret_cast<const u32x4 *>(
-                    a.A + static_cast<long long>(row) * a.lda + k));
-            } else {
-                fa[j][mt] = f16x8{};
-            }
+            const bool ok = j < g_cnt * 4 && mg0 + mt * 16 + fr < a.M;
+            const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+            fa[j][mt] = permute_a(ok ? ra[j][mt] : z);
         }
     }
 
@@ -218,6 +227,175 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
             wcur[q] = wnext[q];
             scur[q] = snext[q];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Strip kernel (bl == 32, k in {2048, 3072, 4096}, any n): one workgroup of 8 wave64s per CU owns
+// up to four consecutive 16-channel tiles for one group of 32 activation rows. It loads its A
+// slice once (into registers, wave w owning k-blocks [w * BPW, (w + 1) * BPW)) and streams the
+// tiles' weights and scales from global memory straight into registers, 16 bytes per lane (one
+// 32-k block of one channel), two tiles in flight; a 4x4 lane-group transpose gives each lane its
+// 8-k slice of four consecutive blocks. Per tile the math is the one of w4a16_mfma_kernel above;
+// the eight waves' f32 partials meet in LDS. The weights do not pass through LDS: on gfx950 a
+// direct-to-LDS stream and the compute's LDS reads do not overlap. The register sets rotate by
+// unrolling, since a register copy would wait for the load still filling it.
+// ---------------------------------------------------------------------------------------------
+constexpr int kStripTiles = 4;
+constexpr int kStripMaxK = 4096;
+
+// 8 nibbles (k = 0..7 of one block slice, nibble i at bits 4i) -> 8 exact f16 values q - 8 in
+// slot order k = 0, 4, 1, 5, 2, 6, 3, 7 (the order permute_a gives the activations).
+// `magic` is 0x64006400 held in an SGPR, so each insert is one v_bfi_b32.
+__device__ __forceinline__ f16x8 unpack_q8_sgpr(uint32_t x, uint32_t magic)
+{
+    const f16x2 bias = f16x2{static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    f16x8 out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t d = ((x >> (4 * j)) & 0x000f000fu) | (magic & ~0x000f000fu);
+        const f16x2 h = __builtin_bit_cast(f16x2, d) + bias;
+        out[2 * j] = h[0];
+        out[2 * j + 1] = h[1];
+    }
+    return out;
+}
+
+template <int K>
+__global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
+{
+    constexpr int BPW = K / 256;  // 32-k blocks per wave (8, 12 or 16)
+    constexpr int NG = BPW / 4;   // 4-block groups per wave
+    static_assert(K % 1024 == 0 && K <= kStripMaxK, "strip kernel k");
+    __shared__ float s_part[kWaves * kMRows * kNTile];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int fr = lane & 15;
+    const int fg = lane >> 4;
+    const int mg0 = blockIdx.y * kMRows;
+
+    const int t_begin = static_cast<int>((static_cast<long long>(blockIdx.x) * a.ntiles) / nwg);
+    const int t_end = static_cast<int>((static_cast<long long>(blockIdx.x + 1) * a.ntiles) / nwg);
+    const int ntl = t_end - t_begin;  // 1 .. kStripTiles
+
+    // A slice of this wave (unconditional loads: all in flight together).
+    u32x4 ra[BPW][2];
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int row = min(mg0 + mt * 16 + fr, a.M - 1);
+            const int k = (wave * BPW + j) * 32 + fg * 8;
+            ra[j][mt] = *reinterpret_cast<const u32x4 *>(a.A + static_cast<long long>(row) * a.lda + k);
+        }
+    }
+
+    struct TileRegs
+    {
+        u32x4 w[NG];
+        uint64_t s[NG];
+    };
+    // Tile tl (clamped to the strip, so every call loads: a repeat hits the cache).
+    auto load = [&](int tl, TileRegs &r) {
+        const int t = t_begin + min(tl, ntl - 1);
+        const int n = min(t * kNTile + fr, a.N - 1);
+        const uint8_t *wrow = a.B + static_cast<long long>(n) * a.bstride;
+        const _Float16 *srow = a.scale_b + static_cast<long long>(n) * a.ldsb;
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            const int b0 = wave * BPW + 4 * q;
+            r.w[q] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(wrow + (b0 + fg) * 16));
+            r.s[q] = *reinterpret_cast<const uint64_t *>(srow + b0);
+        }
+    };
+    TileRegs r0, r1, r2;
+    load(0, r0);
+    load(1, r1);
+
+    // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
+    f16x8 fa[BPW][2];
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            fa[j][mt] = permute_a(ra[j][mt]);
+        }
+    }
+    uint32_t magic;
+    asm volatile("s_mov_b32 %0, 0x64006400" : "=s"(magic));
+
+    auto tile = [&](int tl, const TileRegs &cur, TileRegs &nxt) {
+        load(tl + 2, nxt);
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            uint32_t p[4] = {cur.w[q][0], cur.w[q][1], cur.w[q][2], cur.w[q][3]};
+            transpose_lane_groups(p);
+            f32x4 part[4][2];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f16x8 wq = unpack_q8_sgpr(p[j], magic);
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    part[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        fa[4 * q + j][mt], wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint16_t sbits = static_cast<uint16_t>(cur.s[q] >> (16 * j));
+                const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sbits));
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        acc[mt][r] = __builtin_fmaf(part[j][mt][r], sf, acc[mt][r]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s_part[(wave * kMRows + mt * 16 + 4 * fg + r) * kNTile + fr] = acc[mt][r];
+            }
+        }
+        __syncthreads();
+        const int orow = tid >> 4;
+        const int ocol = tid & 15;
+        const int gm = mg0 + orow;
+        const int gn = (t_begin + tl) * kNTile + ocol;
+        if (gm < a.M && gn < a.N) {
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                v += s_part[(w * kMRows + orow) * kNTile + ocol];
+            }
+            if (a.C) {
+                v += static_cast<float>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+            }
+            if (a.bias) {
+                v += static_cast<float>(a.bias[gn]);
+            }
+            v = fmaxf(v, a.cmin);
+            v = fminf(v, a.cmax);
+            a.D[static_cast<long long>(gm) * a.ldd + gn] = static_cast<_Float16>(v);
+        }
+        __syncthreads();  // s_part is rewritten by the next tile
+    };
+    tile(0, r0, r2);
+    if (ntl > 1) {
+        tile(1, r1, r0);
+    }
+    if (ntl > 2) {
+        tile(2, r2, r1);
+    }
+    if (ntl > 3) {
+        tile(3, r0, r2);
     }
 }
 
@@ -367,7 +545,27 @@ void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950_async(
     const bool fast = bl == 32 && k % 128 == 0 && k <= 128u * kWaves * kMaxGroupsPerWave &&
                       lda % 8 == 0 && (ldb / 2) % 16 == 0 && ldsb % 4 == 0 && aligned16(A) &&
                       aligned16(B) && (reinterpret_cast<uintptr_t>(scale_b) & 7u) == 0;
-    if (fast) {
+    const bool strip = bl == 32 && (k == 2048 || k == 3072 || k == 4096) && lda % 8 == 0 &&
+                       (ldb / 2) % 16 == 0 && ldsb % 8 == 0 && aligned16(A) && aligned16(B) &&
+                       aligned16(scale_b);
+    if (strip) {
+        static int cus = device_cu_count();
+        const long long need = (a.ntiles + kStripTiles - 1) / kStripTiles;
+        const long long nwg = need > cus ? need : (a.ntiles < cus ? a.ntiles : cus);
+        const unsigned long long gy = (m + kMRows - 1) / kMRows;
+        TQT_REQUIRE(gy < 65536 && nwg < (1ll << 31), "grid too large");
+        const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(gy));
+        if (k == 4096) {
+            hipLaunchKernelGGL(w4a16_regs_kernel<4096>, grid, dim3(512), 0, s, a,
+                               static_cast<int>(nwg));
+        } else if (k == 3072) {
+            hipLaunchKernelGGL(w4a16_regs_kernel<3072>, grid, dim3(512), 0, s, a,
+                               static_cast<int>(nwg));
+        } else {
+            hipLaunchKernelGGL(w4a16_regs_kernel<2048>, grid, dim3(512), 0, s, a,
+                               static_cast<int>(nwg));
+        }
+    } else if (fast) {
         static int cus = device_cu_count();
         const int gx = a.ntiles < cus ? a.ntiles : cus;
         const unsigned long long gy = (m + kMRows - 1) / kMRows;
