@@ -164,8 +164,11 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             b_ok[j] = gn < a.N;
             b_ptr[j] = a.B + static_cast<long long>(b_ok[j] ? gn : 0) * a.ldb + b_chk[j] * 16;
         } else {
-            b_row[j] = c >> 3;  // k within the tile
-            b_chk[j] = c & 7;   // 16-column chunk
+            // one wave covers 64 consecutive k of one 16-column chunk, so each byte store of
+            // the transpose below writes 64 consecutive bytes of one LDS row (no bank conflicts
+            // beyond the four lanes that share a dword)
+            b_row[j] = c & 63;  // k within the tile
+            b_chk[j] = c >> 6;  // 16-column chunk
             const int gn = n0 + b_chk[j] * 16;
             b_ok[j] = gn < a.N;
             b_ptr[j] = a.B + (b_ok[j] ? gn : 0);
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 
     i32x4 ra[A_CHUNKS], rb[B_CHUNKS];
 
-    auto load_tile = [&](int k0) {
+    auto load_tile = [&](int k0, i32x4 (&ra)[A_CHUNKS], i32x4 (&rb)[B_CHUNKS]) {
 #pragma unroll
         for (int j = 0; j < A_CHUNKS; ++j) {
             const int k = k0 + a_chk[j] * 16;
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
         }
     };
 
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int buf, const i32x4 (&ra)[A_CHUNKS], const i32x4 (&rb)[B_CHUNKS]) {
 #pragma unroll
         for (int j = 0; j < A_CHUNKS; ++j) {
             *reinterpret_cast<i32x4 *>(&lds_a[buf][lds_off(a_row[j], a_chk[j])]) = ra[j];
@@ -251,17 +254,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     const int frag_row = lane & 15;
     const int frag_chk = lane >> 4;
 
-    if (nk > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) {
-            load_tile((kt + 1) * kBK);
-        }
+    auto compute_step = [&](int buf) {
         i32x4 fa[MT], fb[NT];
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
@@ -280,8 +273,22 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
             }
         }
+    };
+
+    if (nk > 0) {
+        load_tile(0, ra, rb);
+        store_tile(0, ra, rb);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
         if (kt + 1 < nk) {
-            store_tile(buf ^ 1);
+            load_tile((kt + 1) * kBK, ra, rb);
+        }
+        compute_step(buf);
+        if (kt + 1 < nk) {
+            store_tile(buf ^ 1, ra, rb);
         }
         __syncthreads();
     }
