@@ -14,7 +14,8 @@ A step is one launch of the kernel over one batch of synthetic inputs already re
 HBM. Each launch reads a different copy of the weights (and activations): the copies together
 exceed the 256 MB Infinity Cache, so the GB/s figures are HBM figures. Kernel time comes from
 HIP events recorded on the stream the kernels are launched on, around exactly `--steps`
-back-to-back launches after `--warmup` untimed ones.
+back-to-back launches after `--warmup` untimed ones; the timed launches are captured into one
+HIP graph and replayed (`--no-graphs`: issued one by one; the headline legs report both).
 
 cpu_baseline: the portable C restatement of the reference kernel (oracle/, the same tile loop
 the reference runs with VLENB = 16), timed on this host's cores over a bounded sample.
@@ -60,25 +61,56 @@ def copies_for(bytes_per_copy):
 
 
 class Timer:
-    """HIP events on the launch stream around `steps` launches."""
+    """HIP events on the launch stream around exactly `steps` launches.
 
-    def __init__(self, torch, stream):
+    Default: the `steps` launches (each on its own weight copy) are captured once into a HIP
+    graph and the graph is replayed between the two events, so the figure is the kernels'
+    back-to-back cost without per-launch host overhead. `stream_ms` also times the same launches
+    issued one by one on the stream."""
+
+    def __init__(self, torch, stream, graphs=True):
         self.torch = torch
         self.stream = stream
+        self.graphs = graphs
 
-    def run(self, launch, copies, warmup, steps):
+    def _events(self):
+        torch = self.torch
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def stream_ms(self, launch, copies, warmup, steps):
         torch = self.torch
         for i in range(warmup):
             launch(i % copies)
         torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
+        start, end = self._events()
         start.record(self.stream)
         for i in range(steps):
             launch((warmup + i) % copies)
         end.record(self.stream)
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps  # ms per launch
+
+    def run(self, launch, copies, warmup, steps):
+        if not self.graphs:
+            return self.stream_ms(launch, copies, warmup, steps)
+        torch = self.torch
+        for i in range(warmup):
+            launch(i % copies)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=self.stream):
+            for i in range(steps):
+                launch((warmup + i) % copies)
+        graph.replay()  # untimed: first replay uploads the graph
+        torch.cuda.synchronize()
+        start, end = self._events()
+        start.record(self.stream)
+        graph.replay()
+        end.record(self.stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        del graph
+        return ms  # ms per launch
 
 
 # ------------------------------------------------------------------------------------------
@@ -135,10 +167,11 @@ def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng):
           dbias.data_ptr(), -128, 127, ctypes.byref(p), s)
 
     ms = timer.run(launch, nc, warmup, steps)
+    ms_stream = timer.stream_ms(launch, nc, warmup, steps) if timer.graphs else ms
     ops = 2.0 * m * n * k
     algo_bytes = A.nbytes + B.nbytes + 4 * n + 4 * n + m * n
     tops = ops / (ms * 1e-3) / 1e12
-    return dict(ms=ms, tops=tops, gbs=algo_bytes / (ms * 1e-3) / 1e9, ops=ops,
+    return dict(ms=ms, ms_stream=ms_stream, tops=tops, gbs=algo_bytes / (ms * 1e-3) / 1e9, ops=ops,
                 bytes=algo_bytes, copies=nc, inputs=(A, B, sb, bias, zp_a))
 
 
@@ -162,9 +195,10 @@ def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m):
           dbias.data_ptr(), -math.inf, math.inf, ctypes.byref(p), s)
 
     ms = timer.run(launch, nc, warmup, steps)
+    ms_stream = timer.stream_ms(launch, nc, warmup, steps) if timer.graphs else ms
     # B n*k/2 + scale_b 4n + bias 4n + A m*k + scale_a/zp_a 8m + D 4mn
     algo_bytes = n * k // 2 + 4 * n + 4 * n + m * k + 8 * m + 4 * m * n
-    return dict(ms=ms, gbs=algo_bytes / (ms * 1e-3) / 1e9, bytes=algo_bytes,
+    return dict(ms=ms, ms_stream=ms_stream, gbs=algo_bytes / (ms * 1e-3) / 1e9, bytes=algo_bytes,
                 ops=2.0 * m * n * k, copies=nc, inputs=(A, Bp, sa, za, sb, bias))
 
 
@@ -299,7 +333,7 @@ def pmc_pass(counter, timeout_s=120):
     out = tempfile.mkdtemp(prefix="tqt_pmc_", dir="/tmp")
     cmd = [prof, "--pmc", counter, "-d", out, "-o", "pmc", "--output-format", "csv", "--",
            sys.executable, os.path.abspath(__file__), "--only", PMC_LEGS, "--steps", "6",
-           "--warmup", "2"]
+           "--warmup", "2", "--no-graphs"]
     env = dict(os.environ, TMPDIR="/tmp")
     proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
                             stderr=subprocess.DEVNULL, start_new_session=True)
@@ -380,6 +414,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes that measure HBM traffic")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,conv,clamp,copy): "
                          "time just those and print one JSON line each (profiling runs)")
@@ -396,7 +432,7 @@ def main():
         sys.exit(1)
     mod, lib = load_lib()
     stream = torch.cuda.Stream()
-    timer = Timer(torch, stream)
+    timer = Timer(torch, stream, graphs=not args.no_graphs)
     rng = np.random.default_rng(42)
     K, W = args.steps, args.warmup
 
@@ -443,6 +479,9 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded BASELINE.json recipes), %d rotating weight copies > 256 MB "
                 "MALL" % w8["copies"],
+        "timing": ("HIP events around one replay of a HIP graph holding exactly `steps` launches"
+                   if not args.no_graphs else "HIP events around `steps` stream launches"),
+        "ms_per_step_stream_launches": round(w8["ms_stream"], 6),
         "config": {"workload": "gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt M=512 K=4096 "
                                "N=4096 (W8A8 prefill, int8 requantized out)",
                    "M": 512, "K": 4096, "N": 4096},
@@ -452,6 +491,7 @@ def main():
         "w4a8": {
             "workload": "gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt M=1 K=4096 N=11008 (W4A8 decode)",
             "value": round(w41["gbs"], 2), "unit": "GB/s", "us_per_launch": round(w41["ms"] * 1e3, 3),
+            "us_per_launch_stream_launches": round(w41["ms_stream"] * 1e3, 3),
             "roofline": {"bound": "hbm", "achieved": round(w41["gbs"], 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(w41["gbs"] / HBM_PEAK_GBS, 4),
                          "traffic": t_w4, "algorithmic_bytes": w41["bytes"]},
