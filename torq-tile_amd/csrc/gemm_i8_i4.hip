@@ -13,8 +13,9 @@
 //     sum is shifted right by 4 (exact: |16 * sum| < 2^31 for k <= 65536).
 //   * Activation row `rows` of the 16-row A operand is all ones, so that accumulator row is
 //     16 * sum_k (q - 8), the rsum_b of the reference; rows past it are zero.
-//   * Activations are permuted to the (even k, odd k) byte order of the decoded weights; they
-//     are staged in LDS once per workgroup when rows * k fits, else loaded per step.
+//   * Activations are permuted to the (even k, odd k) byte order of the decoded weights; each
+//     wave stages its own k-slice in LDS when it fits one 16-byte load per lane (decode-sized
+//     m), else they are loaded per step.
 // The eight waves' partial sums meet in LDS and the reference's f32 epilogue (zero-point
 // correction, two scale multiplies, C, bias, clamp; no FMA) runs per output.
 #include "tqt_hip_common.hpp"
@@ -28,7 +29,6 @@ constexpr int kNTile = 16;         // weight channels per workgroup
 constexpr int kWaves = 8;          // k is split eight ways inside the workgroup
 constexpr int kPairK = 256;        // k values per pair (128 bytes per weight row, 2 MFMA steps)
 constexpr int kPairsPerBatch = 2;  // pairs whose loads are in flight together per wave
-constexpr int kALdsBytes = 8192;   // activation bytes staged in LDS when rows * k fits
 
 struct W4A8Args
 {
@@ -106,7 +106,8 @@ template <bool kActInLds>
 __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 {
     __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][2 * kPairsPerBatch][1024];
-    __shared__ __attribute__((aligned(16))) int8_t s_a[kActInLds ? kALdsBytes : 16];
+    // activations of each wave's k-slice (one 16-byte chunk per lane at most)
+    __shared__ __attribute__((aligned(16))) int8_t s_a[kWaves][kActInLds ? 1024 : 16];
     __shared__ int32_t s_part[kWaves][16][16];
 
     const int tid = threadIdx.x;
@@ -150,16 +151,20 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
     const bool a_real = fr < rows;
     const bool a_ones = fr == rows;
 
+    // LDS path: this wave's activation slice, rows x [p_begin, p_end) pairs (row stride
+    // npw * 256 bytes), one 16-byte chunk per lane. It is loaded before the weights, so its
+    // ds_write below waits for this load only (loads complete in order), and no workgroup
+    // barrier is needed: a wave reads back only what it wrote.
+    const int npw = p_end - p_begin;
+    const int a_chunks = rows * npw * 16;
+    i32x4 a_chunk = zero;
     if constexpr (kActInLds) {
-        // Activations [rows, K] -> LDS (row stride K), loaded before the weights are issued.
-        const int cpr = a.K / 16;
-        for (int c = tid; c < rows * cpr; c += kWaves * 64) {
-            const int r = c / cpr;
-            const int off = (c - r * cpr) * 16;
-            *reinterpret_cast<i32x4 *>(&s_a[r * a.K + off]) =
-                *reinterpret_cast<const i32x4 *>(a.A + static_cast<long long>(m0 + r) * a.lda + off);
+        if (lane < a_chunks) {
+            const int r = lane / (npw * 16);
+            const int off = (lane - r * npw * 16) * 16;
+            a_chunk = *reinterpret_cast<const i32x4 *>(a.A + static_cast<long long>(m0 + r) * a.lda +
+                                                       p_begin * kPairK + off);
         }
-        __syncthreads();
     }
 
     i32x4 acc0 = zero, acc1 = zero;
@@ -169,30 +174,35 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         if constexpr (!kActInLds) {
 #pragma unroll
             for (int s = 0; s < 2 * kPairsPerBatch; ++s) {
-                const int pair = pb + (s >> 1);
-                if (a_real && pair < p_end) {
-                    const int8_t *p = a.A + static_cast<long long>(m0 + fr) * a.lda +
-                                      pair * kPairK + (s & 1) * 128 + fg * 32;
-                    av[s][0] = *reinterpret_cast<const i32x4 *>(p);
-                    av[s][1] = *reinterpret_cast<const i32x4 *>(p + 16);
-                } else {
-                    av[s][0] = a_ones ? ones : zero;
-                    av[s][1] = a_ones ? ones : zero;
-                }
+                // unconditional loads from a valid row (row rows - 1 for the ones/zero lanes)
+                const int pair = min(pb + (s >> 1), p_end - 1);
+                const int8_t *p = a.A + static_cast<long long>(m0 + min(fr, rows - 1)) * a.lda +
+                                  pair * kPairK + (s & 1) * 128 + fg * 32;
+                const i32x4 v0 = *reinterpret_cast<const i32x4 *>(p);
+                const i32x4 v1 = *reinterpret_cast<const i32x4 *>(p + 16);
+                const i32x4 fill = a_ones ? ones : zero;
+                av[s][0] = a_real ? v0 : fill;
+                av[s][1] = a_real ? v1 : fill;
             }
         }
-        // weights of this batch: load j covers rows 8 * (j & 1) .. +8, pair pb + j / 2
+        // weights of this batch: load j covers rows 8 * (j & 1) .. +8, pair pb + j / 2. The
+        // loads are unconditional (a pair past the slice reloads the last one; its MFMAs are
+        // skipped), so that no branch makes the compiler wait for all of them at once.
         u32x4 wr[2 * kPairsPerBatch];
 #pragma unroll
         for (int j = 0; j < 2 * kPairsPerBatch; ++j) {
-            const int pair = pb + (j >> 1);
+            const int pair = min(pb + (j >> 1), p_end - 1);
             const int row = 8 * (j & 1) + r8;
             const int grow = n0 + row < a.N ? n0 + row : n0;
-            if (pair < p_end) {
-                wr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
-                    a.B + static_cast<long long>(grow) * a.bstride + pair * (kPairK / 2) + c8 * 16));
-            } else {
-                wr[j] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // q = 8
+            wr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+                a.B + static_cast<long long>(grow) * a.bstride + pair * (kPairK / 2) + c8 * 16));
+        }
+        // keep every load of the batch ahead of the compute (the scheduler would sink them to
+        // their uses and serialize the stream); emits no instruction
+        asm volatile("" ::: "memory");
+        if constexpr (kActInLds) {
+            if (pb == p_begin && lane < a_chunks) {
+                *reinterpret_cast<i32x4 *>(&s_a[wave][lane * 16]) = a_chunk;
             }
         }
 #pragma unroll
@@ -204,12 +214,16 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 *reinterpret_cast<u32x4 *>(&s_w[wave][j][r8 * 128 + ((c8 ^ r8) << 4)]) = wr[j];
             }
             const int pair = pb + pp;
+            if (pair >= p_end) {
+                break;
+            }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 i32x4 v0, v1;
                 if constexpr (kActInLds) {
-                    if (a_real && pair < p_end) {
-                        const int8_t *p = &s_a[fr * a.K + pair * kPairK + h * 128 + fg * 32];
+                    if (a_real) {
+                        const int8_t *p = &s_a[wave][fr * npw * kPairK + (pair - p_begin) * kPairK +
+                                                     h * 128 + fg * 32];
                         v0 = *reinterpret_cast<const i32x4 *>(p);
                         v1 = *reinterpret_cast<const i32x4 *>(p + 16);
                     } else {
@@ -379,7 +393,9 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950_async(
         const unsigned gx = static_cast<unsigned>((n + kNTile - 1) / kNTile);
         const unsigned long long gy = (m + kRowsPerChunk - 1) / kRowsPerChunk;
         const size_t rows_max = m < static_cast<size_t>(kRowsPerChunk) ? m : kRowsPerChunk;
-        if (rows_max * k <= static_cast<size_t>(kALdsBytes)) {
+        const size_t npairs = k / kPairK;
+        const size_t ppw = (npairs + kWaves - 1) / kWaves;
+        if (rows_max * ppw * 16 <= 64) {  // each wave's activation slice: one chunk per lane
             hipLaunchKernelGGL(w4a8_mfma_kernel<true>, dim3(gx, static_cast<unsigned>(gy)),
                                dim3(kWaves * 64), 0, s, a);
         } else {
