@@ -25,6 +25,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kBN = 128;
 constexpr int kBK = 64;
+constexpr int kPrefetch = 4;  // k-steps in flight in registers (int8_mfma_kernel)
+constexpr int kConvMaxChunks = 1024;  // fast implicit convolution: k <= 16384
 
 enum AMode { A_MATRIX = 0, A_CONV_CL = 1 };
 enum BMode { B_NK = 0, B_KN = 1 };
@@ -73,27 +75,6 @@ __device__ __forceinline__ int lds_off(int row, int chunk)
     return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
-// A-side gather for the implicit convolution: 16 input bytes for local pixel `row` and
-// reduction index k (k % 16 == 0, a 16-byte run never crosses a tap because ICg % 16 == 0).
-__device__ __forceinline__ i32x4 conv_chunk(const Int8Args &a, int od, int oh, int ow, int k)
-{
-    const ConvGeom &g = a.cv;
-    const int tap = k / g.ICg;
-    const int ic = k - tap * g.ICg;
-    const int kw = tap % g.KW;
-    const int t2 = tap / g.KW;
-    const int kh = t2 % g.KH;
-    const int kd = t2 / g.KH;
-    const int id = od * g.SD + kd * g.DD - g.PD;
-    const int ih = oh * g.SH + kh * g.DH - g.PH;
-    const int iw = ow * g.SW + kw * g.DW - g.PW;
-    if (id < 0 || id >= g.ID || ih < 0 || ih >= g.IH || iw < 0 || iw >= g.IW) {
-        return i32x4{0, 0, 0, 0};
-    }
-    const long long pix = (static_cast<long long>(id) * g.IH + ih) * g.IW + iw;
-    return *reinterpret_cast<const i32x4 *>(a.A + pix * g.IC + ic);
-}
-
 template <int BM, int AM, int BMd, int EPI>
 __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 {
@@ -107,12 +88,32 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     __shared__ __attribute__((aligned(16))) int8_t lds_b[2][kBN * kBK];
     __shared__ int32_t s_mult[kBN];
     __shared__ int32_t s_shift[kBN];
+    // implicit convolution: per 16-byte k-chunk, the tap's input offset from the output pixel's
+    // base and its (kd * DD, kh * DH, kw * DW) packed 10 bits each
+    __shared__ int2 s_tap[AM == A_CONV_CL ? kConvMaxChunks : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 1;
     const int wn = wave & 1;
+
+    if constexpr (AM == A_CONV_CL) {
+        const ConvGeom &g = a.cv;
+        for (int c = tid; c < a.K / 16; c += kThreads) {
+            const int k = 16 * c;
+            const int tap = k / g.ICg;
+            const int ic = k - tap * g.ICg;
+            const int kw = tap % g.KW;
+            const int t2 = tap / g.KW;
+            const int kh = t2 % g.KH;
+            const int kd = t2 / g.KH;
+            const int dd = kd * g.DD, dh = kh * g.DH, dw = kw * g.DW;
+            const int off = ((dd * g.IH + dh) * g.IW + dw) * g.IC + ic;
+            s_tap[c] = int2{off, dd | (dh << 10) | (dw << 20)};
+        }
+        __syncthreads();
+    }
 
     const int tiles_n = (a.N + kBN - 1) / kBN;
     const int tile_m = blockIdx.x / tiles_n;
@@ -143,12 +144,15 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             a_ptr[j] = a.A + static_cast<long long>(a_ok[j] ? gm : 0) * a.lda + a_chk[j] * 16;
             a_od[j] = a_oh[j] = a_ow[j] = 0;
         } else {
+            // a_od/a_oh/a_ow hold the first input coordinate of the output pixel's window
+            const ConvGeom &g = a.cv;
             const long long p = a.p0 + (a_ok[j] ? gm : 0);
-            const long long ohw = static_cast<long long>(a.cv.OH) * a.cv.OW;
-            a_od[j] = static_cast<int>(p / ohw);
-            a_oh[j] = static_cast<int>((p / a.cv.OW) % a.cv.OH);
-            a_ow[j] = static_cast<int>(p % a.cv.OW);
-            a_ptr[j] = nullptr;
+            const long long ohw = static_cast<long long>(g.OH) * g.OW;
+            a_od[j] = static_cast<int>(p / ohw) * g.SD - g.PD;
+            a_oh[j] = static_cast<int>((p / g.OW) % g.OH) * g.SH - g.PH;
+            a_ow[j] = static_cast<int>(p % g.OW) * g.SW - g.PW;
+            a_ptr[j] = a.A + ((static_cast<long long>(a_od[j]) * g.IH + a_oh[j]) * g.IW + a_ow[j]) *
+                                 g.IC;
         }
     }
     int b_row[B_CHUNKS], b_chk[B_CHUNKS];
@@ -175,63 +179,82 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
         }
     }
 
-    i32x4 ra[A_CHUNKS], rb[B_CHUNKS];
-
-    auto load_tile = [&](int k0, i32x4 (&ra)[A_CHUNKS], i32x4 (&rb)[B_CHUNKS]) {
+    // One k-step of operands in registers: raw 16-byte loads plus a validity bit per chunk.
+    // Every load reads valid memory (an out-of-range chunk reads its row start or the image
+    // base instead) and the mask is applied when the step is stored to LDS, so no load sits in
+    // a branch (the compiler would wait for it at the join, serializing the stream).
+    struct Step
+    {
+        i32x4 a[A_CHUNKS];
+        i32x4 b[B_CHUNKS];
+        uint32_t am, bm;
+    };
+    auto load_tile = [&](int k0, Step &st) {
+        st.am = 0;
+        st.bm = 0;
 #pragma unroll
         for (int j = 0; j < A_CHUNKS; ++j) {
             const int k = k0 + a_chk[j] * 16;
-            if (a_ok[j] && k < a.K) {
-                if constexpr (AM == A_MATRIX) {
-                    ra[j] = *reinterpret_cast<const i32x4 *>(a_ptr[j] + k0);
-                } else {
-                    ra[j] = conv_chunk(a, a_od[j], a_oh[j], a_ow[j], k);
-                }
+            bool ok = a_ok[j] && k < a.K;
+            const int8_t *src;
+            if constexpr (AM == A_MATRIX) {
+                src = ok ? a_ptr[j] + k0 : a_ptr[j] - a_chk[j] * 16;
             } else {
-                ra[j] = i32x4{0, 0, 0, 0};
+                const ConvGeom &g = a.cv;
+                const int2 t = s_tap[ok ? k >> 4 : 0];
+                const int id = a_od[j] + (t.y & 1023);
+                const int ih = a_oh[j] + ((t.y >> 10) & 1023);
+                const int iw = a_ow[j] + ((t.y >> 20) & 1023);
+                ok = ok && id >= 0 && id < g.ID && ih >= 0 && ih < g.IH && iw >= 0 && iw < g.IW;
+                src = ok ? a_ptr[j] + t.x : a.A;
             }
+            st.a[j] = *reinterpret_cast<const i32x4 *>(src);
+            st.am |= ok ? (1u << j) : 0u;
         }
 #pragma unroll
         for (int j = 0; j < B_CHUNKS; ++j) {
             if constexpr (BMd == B_NK) {
                 const int k = k0 + b_chk[j] * 16;
-                rb[j] = (b_ok[j] && k < a.K) ? *reinterpret_cast<const i32x4 *>(b_ptr[j] + k0)
-                                             : i32x4{0, 0, 0, 0};
+                const bool ok = b_ok[j] && k < a.K;
+                st.b[j] = *reinterpret_cast<const i32x4 *>(ok ? b_ptr[j] + k0
+                                                              : b_ptr[j] - b_chk[j] * 16);
+                st.bm |= ok ? (1u << j) : 0u;
             } else {
                 const int k = k0 + b_row[j];
                 const int gn = n0 + b_chk[j] * 16;
-                if (b_ok[j] && k < a.K) {
-                    const int8_t *src = b_ptr[j] + static_cast<long long>(k) * a.ldb;
-                    if (gn + 16 <= a.N) {
-                        rb[j] = *reinterpret_cast<const i32x4 *>(src);
-                    } else {
-                        i32x4 tmp = i32x4{0, 0, 0, 0};
-                        int8_t *tb = reinterpret_cast<int8_t *>(&tmp);
-                        for (int i = 0; i < 16 && gn + i < a.N; ++i) {
-                            tb[i] = src[i];
-                        }
-                        rb[j] = tmp;
-                    }
+                const bool ok = b_ok[j] && k < a.K;
+                const int8_t *src = b_ptr[j] + static_cast<long long>(ok ? k : 0) * a.ldb;
+                if (gn + 16 <= a.N) {  // uniform per wave (one column chunk per wave)
+                    st.b[j] = *reinterpret_cast<const i32x4 *>(src);
                 } else {
-                    rb[j] = i32x4{0, 0, 0, 0};
+                    i32x4 tmp = i32x4{0, 0, 0, 0};
+                    int8_t *tb = reinterpret_cast<int8_t *>(&tmp);
+                    for (int i = 0; i < 16 && gn + i < a.N; ++i) {
+                        tb[i] = src[i];
+                    }
+                    st.b[j] = tmp;
                 }
+                st.bm |= ok ? (1u << j) : 0u;
             }
         }
     };
 
-    auto store_tile = [&](int buf, const i32x4 (&ra)[A_CHUNKS], const i32x4 (&rb)[B_CHUNKS]) {
+    auto store_tile = [&](int buf, const Step &st) {
+        const i32x4 z = i32x4{0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < A_CHUNKS; ++j) {
-            *reinterpret_cast<i32x4 *>(&lds_a[buf][lds_off(a_row[j], a_chk[j])]) = ra[j];
+            *reinterpret_cast<i32x4 *>(&lds_a[buf][lds_off(a_row[j], a_chk[j])]) =
+                (st.am >> j) & 1u ? st.a[j] : z;
         }
 #pragma unroll
         for (int j = 0; j < B_CHUNKS; ++j) {
+            const i32x4 v = (st.bm >> j) & 1u ? st.b[j] : z;
             if constexpr (BMd == B_NK) {
-                *reinterpret_cast<i32x4 *>(&lds_b[buf][lds_off(b_row[j], b_chk[j])]) = rb[j];
+                *reinterpret_cast<i32x4 *>(&lds_b[buf][lds_off(b_row[j], b_chk[j])]) = v;
             } else {
                 // Transpose 16 consecutive n of one k into the [n][k] tile.
                 const int k = b_row[j];
-                const int8_t *bytes = reinterpret_cast<const int8_t *>(&rb[j]);
+                const int8_t *bytes = reinterpret_cast<const int8_t *>(&v);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int n = b_chk[j] * 16 + i;
@@ -275,22 +298,45 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
         }
     };
 
+    // k-steps stream through registers PF steps ahead of the LDS pair (register set s holds
+    // step j with j % PF == s; the sets rotate by unrolling, since a register copy would wait
+    // for the load still filling it). Loads past the last step reload it, so every load is
+    // unconditional and the compiler tracks each set's loads exactly.
+    constexpr int PF = BMd == B_KN ? 2 : kPrefetch;  // the K x N transpose needs the registers
+    Step ps[PF];
+    auto step_k0 = [&](int st) { return min(st, nk - 1) * kBK; };
     if (nk > 0) {
-        load_tile(0, ra, rb);
-        store_tile(0, ra, rb);
+#pragma unroll
+        for (int st = 0; st < PF; ++st) {
+            load_tile(step_k0(st), ps[st]);
+        }
+        store_tile(0, ps[0]);
+        load_tile(step_k0(PF), ps[0]);
     }
     __syncthreads();
 
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) {
-            load_tile((kt + 1) * kBK, ra, rb);
-        }
-        compute_step(buf);
-        if (kt + 1 < nk) {
-            store_tile(buf ^ 1, ra, rb);
-        }
+    // Step kt: compute from LDS buffer kt & 1, store step kt + 1 (set (kt + 1) % PF) into the
+    // other buffer, refill that set with step kt + 1 + PF. A store past the last step writes a
+    // buffer nobody reads. Whole groups of PF steps run without branches (a join inside the
+    // group makes the compiler wait for every load in flight); the last nk % PF steps follow.
+    auto step = [&](int kt, Step &set) {
+        compute_step(kt & 1);
+        store_tile((kt + 1) & 1, set);
+        load_tile(step_k0(kt + 1 + PF), set);
         __syncthreads();
+    };
+    int kt0 = 0;
+    for (; kt0 + PF <= nk; kt0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            step(kt0 + u, ps[(u + 1) % PF]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < PF - 1; ++u) {
+        if (kt0 + u < nk) {
+            step(kt0 + u, ps[(u + 1) % PF]);
+        }
     }
 
     // Epilogue: lane holds D[4 * (lane / 16) + r][lane % 16] of every 16x16 sub-tile.
@@ -1062,8 +1108,15 @@ void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx95
     g.IC = static_cast<int>(p.input_channel);
     g.ICg = static_cast<int>(icg);
     TQT_REQUIRE(g.OH > 0 && g.OW > 0 && icg > 0, "empty conv geometry");
+    // fast path: 16-byte channel runs, a tap table that fits LDS, tap extents that pack into
+    // 10 bits each, and input offsets that fit 31 bits
+    const size_t in_bytes = p.input_shape[0] * p.input_shape[1] * p.input_shape[2] *
+                            static_cast<size_t>(p.input_channel);
     const bool fast = (icg % 16 == 0) && (p.input_channel % 16 == 0) && (ldb % 16 == 0) &&
-                      aligned16(a.A) && aligned16(B);
+                      aligned16(a.A) && aligned16(B) && kfull / 16 <= kConvMaxChunks &&
+                      (p.kernel_shape[0] - 1) * p.dilation[0] < 1024 &&
+                      (p.kernel_shape[1] - 1) * p.dilation[1] < 1024 &&
+                      (p.kernel_shape[2] - 1) * p.dilation[2] < 1024 && in_bytes < (1ull << 31);
     launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8>(
         a, fast, as_stream(stream),
         "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
