@@ -18,6 +18,18 @@
 #include "tqt_gemm_clamp_i32_i8_i8_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_interface.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_clamp_i32_i8p_i8p_interface.h"
+#include "tqt_gemm_clamp_i32_i8p_i8p_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_interface.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_interface.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
+#include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_interface.h"
+#include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
 
 static const struct tqt_gemm_clamp_i32_i8_i8_ukernel k_clamp = {
     tqt_get_m_step_gemm_clamp_i32_i8_i8_mfma_gfx950,
@@ -78,9 +90,100 @@ static const struct tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_ukern
     tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
 };
 
+static const struct tqt_gemm_clamp_i32_i8p_i8p_ukernel k_clampp = {
+    tqt_get_m_step_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_n_step_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_c_offset_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_d_offset_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_d_size_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_run_a_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_run_b_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_run_bt_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+    tqt_run_gemm_clamp_i32_i8p_i8p_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_ukernel k_w8a8pb = {
+    tqt_get_m_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_run_b_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_ukernel k_w8a8p = {
+    tqt_get_m_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_run_b_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_ukernel k_w4a8p = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_ukernel k_w4a16p = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_scale_b_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950,
+};
+
+static const struct tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_ukernel k_igemmp = {
+    tqt_get_m_step_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_n_step_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_c_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_bias_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_d_offset_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_get_d_size_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_run_bt_pack_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+    tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
+};
+
 /* m_step and n_step of each kernel type read through its interface struct:
- * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl. */
-void tqts_steps_via_interfaces(size_t out[10])
+ * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl, then the packed types
+ * clamp_i32_i8p_i8p, qai8_qai8_qsi8cxp, qai8_qai8p_qsi8cxp, qai8dxp_qsi4cxp, f16p_qsi4c2p,
+ * igemmcl qsi8cxp. */
+void tqts_steps_via_interfaces(size_t out[22])
 {
     out[0] = k_clamp.get_m_step();
     out[1] = k_clamp.get_n_step();
@@ -92,6 +195,18 @@ void tqts_steps_via_interfaces(size_t out[10])
     out[7] = k_w4a16.get_n_step();
     out[8] = k_igemm.get_m_step();
     out[9] = k_igemm.get_n_step();
+    out[10] = k_clampp.get_m_step();
+    out[11] = k_clampp.get_n_step();
+    out[12] = k_w8a8pb.get_m_step();
+    out[13] = k_w8a8pb.get_n_step();
+    out[14] = k_w8a8p.get_m_step();
+    out[15] = k_w8a8p.get_n_step();
+    out[16] = k_w4a8p.get_m_step();
+    out[17] = k_w4a8p.get_n_step();
+    out[18] = k_w4a16p.get_m_step();
+    out[19] = k_w4a16p.get_n_step();
+    out[20] = k_igemmp.get_m_step();
+    out[21] = k_igemmp.get_n_step();
 }
 
 /* W4A16 run through the interface struct with _Float16 clamps given as binary16 bits. */
@@ -150,4 +265,25 @@ void tqts_run_igemmcl(size_t m, size_t n, const void *input, size_t group_idx, s
 {
     k_igemm.run_igemm(m, n, 0, input, group_idx, m_idx, 0, B, ldb, 0, NULL, 0, D, ldd, bias, cmin,
                       cmax, conv, params);
+}
+
+/* Packed W4A16 run (A and B packed by this library's packers) with _Float16 clamps given as
+ * binary16 bits: through the interface struct, or stream-ordered when stream != NULL. */
+void tqts_run_w4a16p(size_t m, size_t n, size_t k, size_t bl, const void *A_packed, size_t lda,
+                     size_t k_idx_a, const void *B_packed, size_t ldb, size_t k_idx_b,
+                     const void *scale_b, size_t ldsb, const void *C, size_t ldc, void *D,
+                     size_t ldd, const void *bias, uint16_t cmin_bits, uint16_t cmax_bits,
+                     void *stream)
+{
+    float16_t cmin, cmax;
+    memcpy(&cmin, &cmin_bits, 2);
+    memcpy(&cmax, &cmax_bits, 2);
+    if (stream) {
+        tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950_async(
+            m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb, C, ldc, D,
+            ldd, bias, cmin, cmax, stream);
+    } else {
+        k_w4a16p.run_gemm(m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b,
+                          ldsb, C, ldc, D, ldd, bias, cmin, cmax);
+    }
 }

@@ -1,0 +1,183 @@
+"""Packed (p) kernel types without a GPU: the numpy restatement of the packed layout against
+hand-worked layouts, its permutation property, the offset getters against that restatement,
+the entry points the reference's packed headers declare, and their interface structs.
+
+The device packers and packed runs are checked against the same restatement, and against the
+unpacked runs, in test_gpu_packed.py."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import tqt_testlib as T
+
+V = "_mfma_gfx950"
+PACKED = {
+    "clampp": "gemm_clamp_i32_i8p_i8p",
+    "w8a8pb": "gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp",
+    "w8a8p": "gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp",
+    "w4a8p": "gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp",
+    "w4a16p": "gemm_1xnbias_clamp_f16_f16p_qsi4c2p",
+    "igemmclp": "igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp",
+}
+# Functions each reference packed header declares (…_4x1vl_rvv.h / …_8x2vl_rvv.h).
+REF_FUNCS = {
+    "clampp": ["get_m_step", "get_n_step", "get_a_packed_offset", "get_b_packed_offset",
+               "get_c_offset", "get_d_offset", "get_d_size", "get_a_packed_size",
+               "get_b_packed_size", "run_a_pack", "run_b_pack", "run_bt_pack", "run"],
+    "w8a8pb": ["get_m_step", "get_n_step", "get_a_offset", "get_b_packed_offset", "get_c_offset",
+               "get_bias_offset", "get_d_offset", "get_d_size", "get_b_packed_size",
+               "run_b_pack", "run_bt_pack", "run"],
+    "w8a8p": ["get_m_step", "get_n_step", "get_a_packed_offset", "get_b_packed_offset",
+              "get_c_offset", "get_bias_offset", "get_d_offset", "get_d_size",
+              "get_a_packed_size", "get_b_packed_size", "run_a_pack", "run_b_pack",
+              "run_bt_pack", "run"],
+    "w4a8p": ["get_m_step", "get_n_step", "get_a_packed_offset", "get_b_packed_offset",
+              "get_c_offset", "get_bias_offset", "get_d_offset", "get_d_size",
+              "get_a_packed_size", "get_b_packed_size", "run_a_pack", "run_bt_pack", "run"],
+    "w4a16p": ["get_m_step", "get_n_step", "get_a_packed_offset", "get_b_packed_offset",
+               "get_scale_b_offset", "get_c_offset", "get_bias_offset", "get_d_offset",
+               "get_d_size", "get_a_packed_size", "get_b_packed_size", "run_a_pack",
+               "run_bt_pack", "run"],
+    "igemmclp": ["get_m_step", "get_n_step", "get_b_packed_offset", "get_c_offset",
+                 "get_bias_offset", "get_d_offset", "get_d_size", "get_b_packed_size",
+                 "run_bt_pack", "run"],
+}
+
+
+@pytest.fixture(scope="module")
+def mod():
+    return T.load_product_module()
+
+
+@pytest.fixture(scope="module")
+def lib(mod):
+    return mod.load()
+
+
+def sym(mod, kind, action):
+    return mod._sym(kind, action)
+
+
+def test_layout_restatement_hand_worked():
+    # 3 rows of 20 bytes, panels of 2 rows: panel 0 = chunk 0 of rows 0, 1, then the 4-byte
+    # tails of rows 0, 1; panel 1 (one row) starts at 2 * 20
+    X = np.arange(60).reshape(3, 20)
+    exp = (list(range(0, 16)) + list(range(20, 36)) + [16, 17, 18, 19, 36, 37, 38, 39] +
+           list(range(40, 56)) + [56, 57, 58, 59])
+    np.testing.assert_array_equal(T.pack_panels(X, 2), exp)
+    # a k_idx = 3 sub-buffer: the narrower panel 1 starts 3 * (2 - 1) bytes earlier
+    out = np.full(80, -1)
+    T.pack_panels(X[:, :4], 2, ld_packed=20, shift=3, out=out, base=3 * 2)
+    assert list(out[6:14]) == [0, 1, 2, 3, 20, 21, 22, 23]
+    assert list(out[6 + 40 - 3:6 + 40 - 3 + 4]) == [40, 41, 42, 43]
+
+
+@pytest.mark.parametrize("rows,kb,step", [(1, 16, 16), (37, 100, 16), (130, 64, 128),
+                                          (5, 7, 4), (256, 2048, 128), (33, 8192, 32)])
+def test_layout_is_a_permutation(rows, kb, step):
+    idx = np.arange(rows * kb).reshape(rows, kb)
+    out = T.pack_panels(idx, step)
+    np.testing.assert_array_equal(np.sort(out), np.arange(rows * kb))
+    # inverse: each element found where the chunk rule puts it
+    rng = np.random.default_rng(rows + kb)
+    for _ in range(200):
+        r, c = int(rng.integers(rows)), int(rng.integers(kb))
+        p, rl = divmod(r, step)
+        w = min(step, rows - p * step)
+        ch = c // 16
+        cw = min(16, kb - 16 * ch)
+        assert out[p * step * kb + 16 * ch * w + rl * cw + c % 16] == r * kb + c
+
+
+def test_fragment_order_is_an_involution_on_whole_groups():
+    for kb in (64, 100, 128, 2048, 2050):
+        p = T.frag_perm(kb)
+        np.testing.assert_array_equal(np.sort(p), np.arange(kb))
+        np.testing.assert_array_equal(p[p], np.arange(kb))
+        np.testing.assert_array_equal(p[kb // 64 * 64:], np.arange(kb // 64 * 64, kb))
+    # chunk c of a group holds 4-byte word c of each of the group's four 16-byte blocks
+    p = T.frag_perm(64)
+    for c in range(4):
+        np.testing.assert_array_equal(p[16 * c:16 * c + 16],
+                                      np.concatenate([np.arange(4) + 16 * b + 4 * c
+                                                      for b in range(4)]))
+
+
+def test_packed_entry_points_follow_reference_names(lib, mod):
+    exported = set(lib.symbol_names())
+    for kind, funcs in REF_FUNCS.items():
+        for f in funcs:
+            assert sym(mod, kind, f) in exported, (kind, f)
+            if f.startswith("run"):
+                assert sym(mod, kind, f + "_async") in exported
+
+
+def _getter(lib, name, nargs):
+    f = getattr(lib.dll, name)
+    f.restype = ctypes.c_size_t
+    f.argtypes = [ctypes.c_size_t] * nargs
+    return f
+
+
+# (kind, getter, element bytes (0 = int4), rows, k, step kind, frag)
+OPERANDS = [
+    ("clampp", "get_a_packed_offset", 1, 300, 192, "m", False),
+    ("clampp", "get_b_packed_offset", 1, 260, 192, "n", False),
+    ("w8a8pb", "get_b_packed_offset", 1, 129, 256, "n", False),
+    ("w8a8p", "get_a_packed_offset", 1, 257, 320, "m", False),
+    ("w8a8p", "get_b_packed_offset", 1, 200, 320, "n", False),
+    ("w4a8p", "get_a_packed_offset", 1, 37, 512, "m", False),
+    ("w4a8p", "get_b_packed_offset", 0, 45, 512, "n", False),
+    ("w4a16p", "get_a_packed_offset", 2, 70, 384, "m", False),
+    ("w4a16p", "get_b_packed_offset", 0, 40, 384, "n", True),
+    ("igemmclp", "get_b_packed_offset", 1, 200, 288, "n", False),
+]
+
+
+@pytest.mark.parametrize("kind,getter,esize,rows,k,which,frag", OPERANDS)
+def test_packed_offsets_address_the_restated_layout(lib, mod, kind, getter, esize, rows, k,
+                                                    which, frag):
+    """get_{a,b}_packed_offset(idx, k_idx, ld = k, actual = rows - idx), the reference's formula
+    (idx * ld + k_idx * min(actual, step)) in elements, lands on element (idx, k_idx) of the
+    restated layout for every panel start and every chunk-aligned k_idx (whole 64-byte groups
+    for the fragment-ordered W4A16 weights)."""
+    step = _getter(lib, sym(mod, kind, "get_%s_step" % which), 0)()
+    f = _getter(lib, sym(mod, kind, getter), 4)
+    kbytes = k // 2 if esize == 0 else k * esize
+    idx = np.arange(rows * kbytes).reshape(rows, kbytes)
+    out = T.pack_panels(idx, step, frag=frag)
+    kstep = 128 if frag else (32 if esize == 0 else 16 // esize)
+    for r0 in range(0, rows, step):
+        for k_idx in range(0, k, kstep):
+            off = f(r0, k_idx, k, rows - r0)
+            kb = k_idx // 2 if esize == 0 else k_idx * esize
+            assert out[off] == r0 * kbytes + kb, (r0, k_idx)
+
+
+def test_packed_sizes_equal_unpacked_sizes(lib, mod):
+    m, n, k = 37, 91, 256
+    g = lambda kind, what: _getter(lib, sym(mod, kind, what), 2)
+    for kind in ("clampp", "w8a8p"):
+        assert g(kind, "get_a_packed_size")(m, k) == m * k
+        assert g(kind, "get_b_packed_size")(n, k) == n * k
+    assert g("w8a8pb", "get_b_packed_size")(n, k) == n * k
+    assert g("igemmclp", "get_b_packed_size")(n, k) == n * k
+    assert g("w4a8p", "get_a_packed_size")(m, k) == m * k
+    assert g("w4a8p", "get_b_packed_size")(n, k) == n * k // 2
+    assert g("w4a16p", "get_a_packed_size")(m, k) == 2 * m * k
+    assert g("w4a16p", "get_b_packed_size")(n, k) == n * k // 2
+    assert g("clampp", "get_d_size")(m, n) == 4 * m * n
+    assert g("w8a8p", "get_d_size")(m, n) == m * n
+    assert g("w4a8p", "get_d_size")(m, n) == 4 * m * n
+    assert g("w4a16p", "get_d_size")(m, n) == 2 * m * n
+
+
+def test_packed_steps_via_interface_structs(lib, mod, shim):
+    out = (ctypes.c_size_t * 22)()
+    shim.tqts_steps_via_interfaces(out)
+    kinds = ["clamp", "w8a8", "w4a8", "w4a16", "igemmcl"] + list(PACKED)
+    for t, kind in enumerate(kinds):
+        assert out[2 * t] == _getter(lib, sym(mod, kind, "get_m_step"), 0)()
+        assert out[2 * t + 1] == _getter(lib, sym(mod, kind, "get_n_step"), 0)()

@@ -324,3 +324,47 @@ def gen_igemmcl(ID, IH, IW, IC, OC, KH, KW, stride=(1, 1), pad=(0, 0), dil=(1, 1
     oracle().tqto_fuse_zp_to_bias(ptr(fused), ptr(bias), ptr(W), zp_a, OC, K)
     return dict(inp=inp, W=W, bias=fused, conv=conv, scale_a=np.float32(scale_a), zp_a=zp_a,
                 scale_b=scale_b, scale_d=np.float32(scale_d), zp_d=zp_d)
+
+
+# ------------------------------------------------------------------------------------------
+# Packed layout of the p-variants, restated independently of the device code (the library's
+# packers must produce exactly these bytes): panels of `step` rows, panel p at
+# p * step * ld_packed (minus shift * (step - w) for a narrower panel after the first),
+# 16-byte chunks stored chunk-major inside a panel, the last chunk of a row cw < 16 bytes wide.
+# W4A16 weights are first permuted inside each whole 64-byte group of a row (4 x 4 transpose
+# of 4-byte words).
+# ------------------------------------------------------------------------------------------
+
+def frag_perm(kbytes):
+    """perm[P] = logical byte stored at position P of a fragment-ordered W4A16 weight row."""
+    P = np.arange(kbytes)
+    g = P >> 6
+    full = 64 * (g + 1) <= kbytes
+    swapped = 64 * g + 16 * ((P >> 2) & 3) + 4 * ((P >> 4) & 3) + (P & 3)
+    return np.where(full, swapped, P)
+
+
+def pack_panels(X, step, ld_packed=None, shift=0, frag=False, out=None, base=0):
+    """X: [rows, kbytes] (any dtype of 1 byte, or an index array) -> flat packed buffer.
+    ld_packed, shift: bytes. Writes into `out` at offset `base` when given."""
+    X = np.asarray(X)
+    rows, kb = X.shape
+    if ld_packed is None:
+        ld_packed = kb
+    if frag:
+        X = X[:, frag_perm(kb)]
+    if out is None:
+        out = np.zeros(rows * ld_packed if rows else 0, X.dtype)
+    kb16 = kb // 16 * 16
+    for p in range((rows + step - 1) // step):
+        r0 = p * step
+        w = min(step, rows - r0)
+        pb = base + r0 * ld_packed
+        if p > 0 and w < step:
+            pb -= shift * (step - w)
+        blk = X[r0:r0 + w]
+        full = blk[:, :kb16].reshape(w, kb16 // 16, 16).transpose(1, 0, 2).ravel()
+        out[pb:pb + full.size] = full
+        tail = blk[:, kb16:].ravel()
+        out[pb + full.size:pb + full.size + tail.size] = tail
+    return out

@@ -19,6 +19,7 @@
 // oracle's exact operation order (reference test/common/reference_gemm.cpp:132-179).
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -47,7 +48,35 @@ struct W4A16Args
     const _Float16 *bias;
     float cmin, cmax;
     int bl;
+    PackDesc pa, pb;  // packed A / B of the p-variant (read when the kernel's PK bit is set)
 };
+
+// Row pointer (bytes) and k multiplier of activation row `row`: f16 element k of the row is at
+// row pointer + 2 * k * mul for k a multiple of 8 (one 16-byte chunk).
+template <int PK>
+__device__ __forceinline__ const uint8_t *a_row_ptr(const W4A16Args &a, int row, int &mul)
+{
+    const uint8_t *base = reinterpret_cast<const uint8_t *>(a.A);
+    if constexpr ((PK & PK_A) != 0) {
+        return base + pack_row(a.pa, row, mul);
+    } else {
+        mul = 1;
+        return base + static_cast<long long>(row) * a.lda * 2;
+    }
+}
+
+// Weight row pointer and k multiplier of channel n: byte kb (a multiple of 16) is at pointer +
+// kb * mul.
+template <int PK>
+__device__ __forceinline__ const uint8_t *b_row_ptr(const W4A16Args &a, int n, int &mul)
+{
+    if constexpr ((PK & PK_B) != 0) {
+        return a.B + pack_row(a.pb, n, mul);
+    } else {
+        mul = 1;
+        return a.B + static_cast<long long>(n) * a.bstride;
+    }
+}
 
 // 4x4 transpose of 32-bit values across the four 16-lane groups: on entry p[j] of lane group
 // g holds element (g, j); on exit p[j] of lane group g holds element (j, g).
@@ -95,6 +124,7 @@ __device__ __forceinline__ f16x8 permute_a(u32x4 v)
     return __builtin_bit_cast(f16x8, o);
 }
 
+template <int PK>
 __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
 {
     __shared__ float s_part[2][kWaves][kMRows][kNTile];
@@ -126,7 +156,9 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
             const int row = min(mg0 + mt * 16 + fr, a.M - 1);
             const int jj = min(j, max(g_cnt * 4 - 1, 0));
             const int k = min((g_begin * 4 + jj) * 32, max(a.K - 32, 0)) + fg * 8;
-            ra[j][mt] = *reinterpret_cast<const u32x4 *>(a.A + static_cast<long long>(row) * a.lda + k);
+            int mul;
+            const uint8_t *arow = a_row_ptr<PK>(a, row, mul);
+            ra[j][mt] = *reinterpret_cast<const u32x4 *>(arow + 2ll * k * mul);
         }
     }
     f16x8 fa[kMaxGroupsPerWave * 4][2];
@@ -146,14 +178,15 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
     auto load_tile = [&](int t, u32x4 (&w)[kMaxGroupsPerWave], uint64_t (&s)[kMaxGroupsPerWave]) {
         const int n = t * kNTile + fr;
         const bool ok = (t < t_end) && (n < a.N);
-        const uint8_t *wrow = a.B + static_cast<long long>(ok ? n : 0) * a.bstride;
+        int wmul;
+        const uint8_t *wrow = b_row_ptr<PK>(a, ok ? n : 0, wmul);
         const _Float16 *srow = a.scale_b + static_cast<long long>(ok ? n : 0) * a.ldsb;
 #pragma unroll
         for (int q = 0; q < kMaxGroupsPerWave; ++q) {
             if (ok && q < g_cnt) {
                 const int grp = g_begin + q;
                 w[q] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4 *>(wrow + grp * 64 + fg * 16));
+                    reinterpret_cast<const u32x4 *>(wrow + static_cast<long long>(grp * 64 + fg * 16) * wmul));
                 s[q] = *reinterpret_cast<const uint64_t *>(srow + grp * 4);
             } else {
                 w[q] = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
@@ -172,7 +205,9 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
         for (int q = 0; q < kMaxGroupsPerWave; ++q) {
             if (q < g_cnt) {
                 uint32_t p[4] = {wcur[q][0], wcur[q][1], wcur[q][2], wcur[q][3]};
-                transpose_lane_groups(p);
+                if constexpr ((PK & PK_B) == 0) {
+                    transpose_lane_groups(p);  // packed weights are stored transposed already
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const f16x8 wb = unpack_q8(p[j]);
@@ -261,7 +296,7 @@ __device__ __forceinline__ f16x8 unpack_q8_sgpr(uint32_t x, uint32_t magic)
     return out;
 }
 
-template <int K>
+template <int K, int PK>
 __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
 {
     constexpr int BPW = K / 256;  // 32-k blocks per wave (8, 12 or 16)
@@ -288,7 +323,9 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
         for (int mt = 0; mt < 2; ++mt) {
             const int row = min(mg0 + mt * 16 + fr, a.M - 1);
             const int k = (wave * BPW + j) * 32 + fg * 8;
-            ra[j][mt] = *reinterpret_cast<const u32x4 *>(a.A + static_cast<long long>(row) * a.lda + k);
+            int mul;
+            const uint8_t *arow = a_row_ptr<PK>(a, row, mul);
+            ra[j][mt] = *reinterpret_cast<const u32x4 *>(arow + 2ll * k * mul);
         }
     }
 
@@ -301,13 +338,14 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
     auto load = [&](int tl, TileRegs &r) {
         const int t = t_begin + min(tl, ntl - 1);
         const int n = min(t * kNTile + fr, a.N - 1);
-        const uint8_t *wrow = a.B + static_cast<long long>(n) * a.bstride;
+        int wmul;
+        const uint8_t *wrow = b_row_ptr<PK>(a, n, wmul);
         const _Float16 *srow = a.scale_b + static_cast<long long>(n) * a.ldsb;
 #pragma unroll
         for (int q = 0; q < NG; ++q) {
             const int b0 = wave * BPW + 4 * q;
             r.w[q] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4 *>(wrow + (b0 + fg) * 16));
+                reinterpret_cast<const u32x4 *>(wrow + static_cast<long long>((b0 + fg) * 16) * wmul));
             r.s[q] = *reinterpret_cast<const uint64_t *>(srow + b0);
         }
     };
@@ -333,7 +371,9 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
 #pragma unroll
         for (int q = 0; q < NG; ++q) {
             uint32_t p[4] = {cur.w[q][0], cur.w[q][1], cur.w[q][2], cur.w[q][3]};
-            transpose_lane_groups(p);
+            if constexpr ((PK & PK_B) == 0) {
+                transpose_lane_groups(p);  // packed weights are stored transposed already
+            }
             f32x4 part[4][2];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -401,6 +441,7 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
 
 // Generic path: the reference test oracle's operation order, one thread per output
 // (acc = C; acc += a * (f32(q - 8) * f32(s)) in k order without FMA; acc += bias; clamp).
+template <int PK>
 __global__ __launch_bounds__(256) void w4a16_generic_kernel(W4A16Args a)
 {
     const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -416,12 +457,20 @@ __global__ __launch_bounds__(256) void w4a16_generic_kernel(W4A16Args a)
     const _Float16 *arow = a.A + static_cast<long long>(gm) * a.lda;
     const uint8_t *brow = a.B + static_cast<long long>(gn) * a.bstride;
     const _Float16 *srow = a.scale_b + static_cast<long long>(gn) * a.ldsb;
+    // packed operands: the run functions describe an unpacked one with step 0 (row-major)
+    const PackRow ra = pack_row_info(a.pa, gm);
+    const PackRow rb = pack_row_info(a.pb, gn);
     for (int p = 0; p < a.K; ++p) {
-        const uint8_t byte = brow[p >> 1];
+        const uint8_t byte =
+            (PK & PK_B) ? a.B[pack_row_byte(rb, w4a16_frag_pos(p >> 1, rb.kbytes))] : brow[p >> 1];
         const int q = (p & 1) ? (byte >> 4) - 8 : (byte & 0xf) - 8;
         const float s = static_cast<float>(srow[p / a.bl]);
         const float bd = __fmul_rn(static_cast<float>(q), s);
-        acc = __fadd_rn(acc, __fmul_rn(static_cast<float>(arow[p]), bd));
+        const _Float16 av =
+            (PK & PK_A) ? *reinterpret_cast<const _Float16 *>(
+                              reinterpret_cast<const uint8_t *>(a.A) + pack_row_byte(ra, 2ll * p))
+                        : arow[p];
+        acc = __fadd_rn(acc, __fmul_rn(static_cast<float>(av), bd));
     }
     if (a.bias) {
         acc = __fadd_rn(acc, static_cast<float>(a.bias[gn]));
@@ -438,6 +487,110 @@ int device_cu_count()
     int cus = 0;
     TQT_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     return cus > 0 ? cus : 1;
+}
+
+// Shared body of the W4A16 runs. `packed`: A (f16 rows) and B (int4 rows, fragment-ordered)
+// are in the packed layout; k_idx_a / k_idx_b apply the packers' tail rule.
+void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda,
+               size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b, const void *scale_b,
+               size_t ldsb, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+               float16_t clamp_min, float16_t clamp_max, bool packed, hipStream_t s,
+               const char *where)
+{
+    if (m == 0 || n == 0) {
+        return;
+    }
+    // reference …qsi4c2t_8x2vl_rvv.h:59 / .cpp:38-40: bl even and >= 2, k % bl == 0
+    TQT_REQUIRE(bl >= 2 && bl % 2 == 0, "bl >= 2 && bl % 2 == 0");
+    TQT_REQUIRE(k % bl == 0, "k % bl == 0");
+    TQT_REQUIRE(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "dimension exceeds 2^31-1");
+    TQT_REQUIRE((A && B && scale_b) || k == 0, "A/B/scale_b == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    W4A16Args a = {};
+    a.M = static_cast<int>(m);
+    a.N = static_cast<int>(n);
+    a.K = static_cast<int>(k);
+    a.ntiles = static_cast<int>((n + kNTile - 1) / kNTile);
+    a.A = static_cast<const _Float16 *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const uint8_t *>(B);
+    a.bstride = static_cast<long long>(ldb / 2);
+    a.scale_b = static_cast<const _Float16 *>(scale_b);
+    a.ldsb = static_cast<long long>(ldsb);
+    a.C = static_cast<const _Float16 *>(C);
+    a.ldc = static_cast<long long>(ldc);
+    a.D = static_cast<_Float16 *>(D);
+    a.ldd = static_cast<long long>(ldd);
+    a.bias = static_cast<const _Float16 *>(bias);
+    a.cmin = static_cast<float>(clamp_min);
+    a.cmax = static_cast<float>(clamp_max);
+    a.bl = static_cast<int>(bl);
+    bool layout_fast;
+    if (packed) {
+        TQT_REQUIRE(lda >= k && ldb >= k && ldb % 2 == 0 && k_idx_b % 2 == 0,
+                    "packed W4A16 needs lda, ldb >= k and even ldb, k_idx_b");
+        a.pa = make_pack(kPackW4A16MStep, m, 2 * lda, 2 * k, 2 * k_idx_a);
+        a.pb = make_pack(kPackW4A16NStep, n, ldb / 2, k / 2, k_idx_b / 2);
+        // every 16-byte chunk of a packed row starts 16-byte aligned
+        layout_fast = ((2 * k_idx_a) % 16 == 0) && ((k_idx_b / 2) % 16 == 0);
+    } else {
+        a.pa = make_pack(0, m, 2 * lda, 2 * k, 0);
+        a.pb = make_pack(0, n, ldb / 2, k / 2, 0);
+        layout_fast = lda % 8 == 0 && (ldb / 2) % 16 == 0;
+    }
+    const bool fast = bl == 32 && k % 128 == 0 && k <= 128u * kWaves * kMaxGroupsPerWave &&
+                      layout_fast && ldsb % 4 == 0 && aligned16(A) && aligned16(B) &&
+                      (reinterpret_cast<uintptr_t>(scale_b) & 7u) == 0;
+    const bool strip = bl == 32 && (k == 2048 || k == 3072 || k == 4096) && layout_fast &&
+                       ldsb % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(scale_b);
+    if (strip) {
+        static int cus = device_cu_count();
+        const long long need = (a.ntiles + kStripTiles - 1) / kStripTiles;
+        const long long nwg = need > cus ? need : (a.ntiles < cus ? a.ntiles : cus);
+        const unsigned long long gy = (m + kMRows - 1) / kMRows;
+        TQT_REQUIRE(gy < 65536 && nwg < (1ll << 31), "grid too large");
+        const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(gy));
+        const int nw = static_cast<int>(nwg);
+        if (packed) {
+            if (k == 4096) {
+                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_AB>), grid, dim3(512), 0, s, a, nw);
+            } else if (k == 3072) {
+                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_AB>), grid, dim3(512), 0, s, a, nw);
+            } else {
+                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_AB>), grid, dim3(512), 0, s, a, nw);
+            }
+        } else {
+            if (k == 4096) {
+                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_NONE>), grid, dim3(512), 0, s, a, nw);
+            } else if (k == 3072) {
+                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_NONE>), grid, dim3(512), 0, s, a, nw);
+            } else {
+                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_NONE>), grid, dim3(512), 0, s, a, nw);
+            }
+        }
+    } else if (fast) {
+        static int cus = device_cu_count();
+        const int gx = a.ntiles < cus ? a.ntiles : cus;
+        const unsigned long long gy = (m + kMRows - 1) / kMRows;
+        TQT_REQUIRE(gy < 65536, "m too large");
+        const dim3 grid(gx, static_cast<unsigned>(gy));
+        if (packed) {
+            hipLaunchKernelGGL(w4a16_mfma_kernel<PK_AB>, grid, dim3(512), 0, s, a);
+        } else {
+            hipLaunchKernelGGL(w4a16_mfma_kernel<PK_NONE>, grid, dim3(512), 0, s, a);
+        }
+    } else {
+        const long long total = static_cast<long long>(m) * static_cast<long long>(n);
+        const long long blocks = (total + 255) / 256;
+        TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
+        const dim3 grid(static_cast<unsigned>(blocks));
+        if (packed) {
+            hipLaunchKernelGGL(w4a16_generic_kernel<PK_AB>, grid, dim3(256), 0, s, a);
+        } else {
+            hipLaunchKernelGGL(w4a16_generic_kernel<PK_NONE>, grid, dim3(256), 0, s, a);
+        }
+    }
+    check_launch(where);
 }
 
 }  // namespace
@@ -511,75 +664,9 @@ void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950_async(
     size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min, float16_t clamp_max,
     void *stream)
 {
-    (void)k_idx_a;
-    (void)k_idx_b;
-    if (m == 0 || n == 0) {
-        return;
-    }
-    // reference …qsi4c2t_8x2vl_rvv.h:59 / .cpp:38-40: bl even and >= 2, k % bl == 0
-    TQT_REQUIRE(bl >= 2 && bl % 2 == 0, "bl >= 2 && bl % 2 == 0");
-    TQT_REQUIRE(k % bl == 0, "k % bl == 0");
-    TQT_REQUIRE(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "dimension exceeds 2^31-1");
-    TQT_REQUIRE((A && B && scale_b) || k == 0, "A/B/scale_b == NULL");
-    TQT_REQUIRE(D != nullptr, "D == NULL");
-    W4A16Args a = {};
-    a.M = static_cast<int>(m);
-    a.N = static_cast<int>(n);
-    a.K = static_cast<int>(k);
-    a.ntiles = static_cast<int>((n + kNTile - 1) / kNTile);
-    a.A = static_cast<const _Float16 *>(A);
-    a.lda = static_cast<long long>(lda);
-    a.B = static_cast<const uint8_t *>(B);
-    a.bstride = static_cast<long long>(ldb / 2);
-    a.scale_b = static_cast<const _Float16 *>(scale_b);
-    a.ldsb = static_cast<long long>(ldsb);
-    a.C = static_cast<const _Float16 *>(C);
-    a.ldc = static_cast<long long>(ldc);
-    a.D = static_cast<_Float16 *>(D);
-    a.ldd = static_cast<long long>(ldd);
-    a.bias = static_cast<const _Float16 *>(bias);
-    a.cmin = static_cast<float>(clamp_min);
-    a.cmax = static_cast<float>(clamp_max);
-    a.bl = static_cast<int>(bl);
-    hipStream_t s = as_stream(stream);
-    const bool fast = bl == 32 && k % 128 == 0 && k <= 128u * kWaves * kMaxGroupsPerWave &&
-                      lda % 8 == 0 && (ldb / 2) % 16 == 0 && ldsb % 4 == 0 && aligned16(A) &&
-                      aligned16(B) && (reinterpret_cast<uintptr_t>(scale_b) & 7u) == 0;
-    const bool strip = bl == 32 && (k == 2048 || k == 3072 || k == 4096) && lda % 8 == 0 &&
-                       (ldb / 2) % 16 == 0 && ldsb % 8 == 0 && aligned16(A) && aligned16(B) &&
-                       aligned16(scale_b);
-    if (strip) {
-        static int cus = device_cu_count();
-        const long long need = (a.ntiles + kStripTiles - 1) / kStripTiles;
-        const long long nwg = need > cus ? need : (a.ntiles < cus ? a.ntiles : cus);
-        const unsigned long long gy = (m + kMRows - 1) / kMRows;
-        TQT_REQUIRE(gy < 65536 && nwg < (1ll << 31), "grid too large");
-        const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(gy));
-        if (k == 4096) {
-            hipLaunchKernelGGL(w4a16_regs_kernel<4096>, grid, dim3(512), 0, s, a,
-                               static_cast<int>(nwg));
-        } else if (k == 3072) {
-            hipLaunchKernelGGL(w4a16_regs_kernel<3072>, grid, dim3(512), 0, s, a,
-                               static_cast<int>(nwg));
-        } else {
-            hipLaunchKernelGGL(w4a16_regs_kernel<2048>, grid, dim3(512), 0, s, a,
-                               static_cast<int>(nwg));
-        }
-    } else if (fast) {
-        static int cus = device_cu_count();
-        const int gx = a.ntiles < cus ? a.ntiles : cus;
-        const unsigned long long gy = (m + kMRows - 1) / kMRows;
-        TQT_REQUIRE(gy < 65536, "m too large");
-        hipLaunchKernelGGL(w4a16_mfma_kernel, dim3(gx, static_cast<unsigned>(gy)), dim3(512), 0, s,
-                           a);
-    } else {
-        const long long total = static_cast<long long>(m) * static_cast<long long>(n);
-        const long long blocks = (total + 255) / 256;
-        TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
-        hipLaunchKernelGGL(w4a16_generic_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                           s, a);
-    }
-    check_launch("tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950");
+    w4a16_run(m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd, bias,
+              clamp_min, clamp_max, false, as_stream(stream),
+              "tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950");
 }
 
 void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(
@@ -594,6 +681,34 @@ void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(
         m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd, bias,
         clamp_min, clamp_max, nullptr);
     finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950");
+}
+
+// gemm_1xnbias_clamp_f16_f16p_qsi4c2p (reference …f16p_qsi4c2p_8x2vl_rvv.cpp:121-230; geometry
+// getters and packers in packing.hip).
+void tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, size_t bl, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb,
+    const void *C, size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min,
+    float16_t clamp_max, void *stream)
+{
+    w4a16_run(m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb, C, ldc,
+              D, ldd, bias, clamp_min, clamp_max, true, as_stream(stream),
+              "tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(
+    size_t m, size_t n, size_t k, size_t bl, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb,
+    const void *C, size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min,
+    float16_t clamp_max)
+{
+    if (m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950_async(
+        m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd,
+        bias, clamp_min, clamp_max, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
 }
 
 }  // extern "C"

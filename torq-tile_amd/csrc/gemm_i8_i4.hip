@@ -20,6 +20,7 @@
 // correction, two scale multiplies, C, bias, clamp; no FMA) runs per output.
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -46,6 +47,7 @@ struct W4A8Args
     const float *scale_a;
     const int32_t *zp_a;
     const float *scale_b;
+    PackDesc pa, pb;  // packed A / B of the p-variant (read when the kernel's PK bit is set)
 };
 
 // reference tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:234-419: zp correction (int32), RNE convert, two
@@ -102,7 +104,7 @@ __device__ __forceinline__ void decode_w16(const u32x4 w, i32x4 &q0, i32x4 &q1)
     q1[3] = static_cast<int32_t>((w[3] & 0xf0f0f0f0u) ^ 0x80808080u);
 }
 
-template <bool kActInLds>
+template <bool kActInLds, int PK>
 __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 {
     __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][2 * kPairsPerBatch][1024];
@@ -162,8 +164,40 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         if (lane < a_chunks) {
             const int r = lane / (npw * 16);
             const int off = (lane - r * npw * 16) * 16;
-            a_chunk = *reinterpret_cast<const i32x4 *>(a.A + static_cast<long long>(m0 + r) * a.lda +
-                                                       p_begin * kPairK + off);
+            int mul = 1;  // byte kb of a packed row is at kb * (panel width) from its chunk 0
+            long long base;
+            if constexpr ((PK & PK_A) != 0) {
+                base = pack_row(a.pa, m0 + r, mul);
+            } else {
+                base = static_cast<long long>(m0 + r) * a.lda;
+            }
+            a_chunk = *reinterpret_cast<const i32x4 *>(
+                a.A + base + static_cast<long long>(p_begin * kPairK + off) * mul);
+        }
+    }
+    // register path: this lane's activation row (row rows - 1 for the ones/zero lanes) and the
+    // two weight rows it loads
+    int a_mul = 1;
+    const int8_t *a_rowp = a.A;
+    if constexpr (!kActInLds) {
+        const int r = m0 + min(fr, rows - 1);
+        if constexpr ((PK & PK_A) != 0) {
+            a_rowp = a.A + pack_row(a.pa, r, a_mul);
+        } else {
+            a_rowp = a.A + static_cast<long long>(r) * a.lda;
+        }
+    }
+    const uint8_t *w_rowp[2];
+    int w_mul[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 8 * h + r8;
+        const int grow = n0 + row < a.N ? n0 + row : n0;
+        w_mul[h] = 1;
+        if constexpr ((PK & PK_B) != 0) {
+            w_rowp[h] = a.B + pack_row(a.pb, grow, w_mul[h]);
+        } else {
+            w_rowp[h] = a.B + static_cast<long long>(grow) * a.bstride;
         }
     }
 
@@ -176,10 +210,10 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
             for (int s = 0; s < 2 * kPairsPerBatch; ++s) {
                 // unconditional loads from a valid row (row rows - 1 for the ones/zero lanes)
                 const int pair = min(pb + (s >> 1), p_end - 1);
-                const int8_t *p = a.A + static_cast<long long>(m0 + min(fr, rows - 1)) * a.lda +
-                                  pair * kPairK + (s & 1) * 128 + fg * 32;
+                const int8_t *p =
+                    a_rowp + static_cast<long long>(pair * kPairK + (s & 1) * 128 + fg * 32) * a_mul;
                 const i32x4 v0 = *reinterpret_cast<const i32x4 *>(p);
-                const i32x4 v1 = *reinterpret_cast<const i32x4 *>(p + 16);
+                const i32x4 v1 = *reinterpret_cast<const i32x4 *>(p + 16 * a_mul);
                 const i32x4 fill = a_ones ? ones : zero;
                 av[s][0] = a_real ? v0 : fill;
                 av[s][1] = a_real ? v1 : fill;
@@ -192,10 +226,8 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 #pragma unroll
         for (int j = 0; j < 2 * kPairsPerBatch; ++j) {
             const int pair = min(pb + (j >> 1), p_end - 1);
-            const int row = 8 * (j & 1) + r8;
-            const int grow = n0 + row < a.N ? n0 + row : n0;
             wr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
-                a.B + static_cast<long long>(grow) * a.bstride + pair * (kPairK / 2) + c8 * 16));
+                w_rowp[j & 1] + static_cast<long long>(pair * (kPairK / 2) + c8 * 16) * w_mul[j & 1]));
         }
         // keep every load of the batch ahead of the compute (the scheduler would sink them to
         // their uses and serialize the stream); emits no instruction
@@ -268,6 +300,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 }
 
 // Generic path: one thread per output, any alignment, any even k.
+template <int PK>
 __global__ __launch_bounds__(256) void w4a8_generic_kernel(W4A8Args a)
 {
     const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -278,19 +311,115 @@ __global__ __launch_bounds__(256) void w4a8_generic_kernel(W4A8Args a)
     const int gn = static_cast<int>(idx - static_cast<long long>(gm) * a.N);
     const int8_t *arow = a.A + static_cast<long long>(gm) * a.lda;
     const uint8_t *brow = a.B + static_cast<long long>(gn) * a.bstride;
+    // packed operands: the run functions describe an unpacked one with step 0 (row-major)
+    const PackRow ra = pack_row_info(a.pa, gm);
+    const PackRow rb = pack_row_info(a.pb, gn);
     uint32_t acc = 0, rsum = 0;
     for (int k = 0; k < a.K; k += 2) {
-        const uint8_t byte = brow[k >> 1];
+        const uint8_t byte = (PK & PK_B) ? a.B[pack_row_byte(rb, k >> 1)] : brow[k >> 1];
         const int32_t lo = static_cast<int32_t>(byte & 0xf) - 8;
         const int32_t hi = static_cast<int32_t>(byte >> 4) - 8;
         rsum += static_cast<uint32_t>(lo + hi);
-        acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * lo);
-        acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k + 1]) * hi);
+        const int32_t a0 = (PK & PK_A) ? a.A[pack_row_byte(ra, k)] : arow[k];
+        const int32_t a1 = (PK & PK_A) ? a.A[pack_row_byte(ra, k + 1)] : arow[k + 1];
+        acc += static_cast<uint32_t>(a0 * lo);
+        acc += static_cast<uint32_t>(a1 * hi);
     }
     a.D[static_cast<long long>(gm) * a.ldd + gn] = epilogue_f32(
         static_cast<int32_t>(acc), static_cast<int32_t>(rsum), a.zp_a[gm], a.scale_a[gm],
         a.scale_b[gn], a.C ? &a.C[static_cast<long long>(gm) * a.ldc + gn] : nullptr,
         a.bias ? &a.bias[gn] : nullptr, a.cmin, a.cmax);
+}
+
+// Shared body of the W4A8 runs. `packed`: A and B are in the packed layout (A rows of k bytes,
+// B rows of k/2 bytes; k_idx_a / k_idx_b apply the packers' tail rule).
+void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a,
+              const void *B, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+              size_t ldd, const void *bias, float clamp_min, float clamp_max,
+              const struct tqt_qai8dx_qsi4cx_params *params, bool packed, hipStream_t s,
+              const char *where)
+{
+    if (!params) {
+        return;  // reference …qai8dx_qsi4cxt_4x1vl_rvv.cpp:165-167
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    TQT_REQUIRE(k % 2 == 0, "k % 2 == 0");
+    TQT_REQUIRE(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "dimension exceeds 2^31-1");
+    TQT_REQUIRE(params->scale_a && params->zero_point_a && params->scale_b,
+                "params arrays must be non-NULL");
+    TQT_REQUIRE((A != nullptr && B != nullptr) || k == 0, "A/B == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    W4A8Args a = {};
+    a.M = static_cast<int>(m);
+    a.N = static_cast<int>(n);
+    a.K = static_cast<int>(k);
+    a.A = static_cast<const int8_t *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const uint8_t *>(B);
+    a.bstride = static_cast<long long>(ldb / 2);
+    a.C = static_cast<const float *>(C);
+    a.ldc = static_cast<long long>(ldc);
+    a.D = static_cast<float *>(D);
+    a.ldd = static_cast<long long>(ldd);
+    a.bias = static_cast<const float *>(bias);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    a.scale_a = params->scale_a;
+    a.zp_a = params->zero_point_a;
+    a.scale_b = params->scale_b;
+    bool layout_fast;
+    if (packed) {
+        TQT_REQUIRE(lda >= k && ldb >= k && ldb % 2 == 0 && k_idx_b % 2 == 0,
+                    "packed W4A8 needs lda, ldb >= k and even ldb, k_idx_b");
+        a.pa = make_pack(kPackW4A8MStep, m, lda, k, k_idx_a);
+        a.pb = make_pack(kPackW4A8NStep, n, ldb / 2, k / 2, k_idx_b / 2);
+        // every 16-byte chunk of a packed row starts 16-byte aligned
+        layout_fast = (k_idx_a % 16 == 0) && ((k_idx_b / 2) % 16 == 0);
+    } else {
+        a.pa = make_pack(0, m, lda, k, 0);
+        a.pb = make_pack(0, n, ldb / 2, k / 2, 0);
+        layout_fast = (lda % 16 == 0) && ((ldb / 2) % 16 == 0);
+    }
+    const bool fast = (k % kPairK == 0) && k <= 65536 && layout_fast && aligned16(A) &&
+                      aligned16(B) && (m + kRowsPerChunk - 1) / kRowsPerChunk < 65536;
+    if (fast) {
+        const unsigned gx = static_cast<unsigned>((n + kNTile - 1) / kNTile);
+        const unsigned long long gy = (m + kRowsPerChunk - 1) / kRowsPerChunk;
+        const size_t rows_max = m < static_cast<size_t>(kRowsPerChunk) ? m : kRowsPerChunk;
+        const size_t npairs = k / kPairK;
+        const size_t ppw = (npairs + kWaves - 1) / kWaves;
+        const dim3 grid(gx, static_cast<unsigned>(gy));
+        if (rows_max * ppw * 16 <= 64) {  // each wave's activation slice: one chunk per lane
+            if (packed) {
+                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_AB>), grid, dim3(kWaves * 64), 0, s, a);
+            } else {
+                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_NONE>), grid, dim3(kWaves * 64), 0, s,
+                                   a);
+            }
+        } else {
+            if (packed) {
+                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_AB>), grid, dim3(kWaves * 64), 0, s,
+                                   a);
+            } else {
+                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_NONE>), grid, dim3(kWaves * 64), 0,
+                                   s, a);
+            }
+        }
+    } else {
+        const long long total = static_cast<long long>(m) * static_cast<long long>(n);
+        const long long blocks = (total + 255) / 256;
+        TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
+        if (packed) {
+            hipLaunchKernelGGL(w4a8_generic_kernel<PK_AB>, dim3(static_cast<unsigned>(blocks)),
+                               dim3(256), 0, s, a);
+        } else {
+            hipLaunchKernelGGL(w4a8_generic_kernel<PK_NONE>, dim3(static_cast<unsigned>(blocks)),
+                               dim3(256), 0, s, a);
+        }
+    }
+    check_launch(where);
 }
 
 }  // namespace
@@ -353,63 +482,9 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950_async(
     size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
     float clamp_min, float clamp_max, const struct tqt_qai8dx_qsi4cx_params *params, void *stream)
 {
-    (void)k_idx_a;
-    (void)k_idx_b;
-    if (!params) {
-        return;  // reference …qai8dx_qsi4cxt_4x1vl_rvv.cpp:165-167
-    }
-    if (m == 0 || n == 0) {
-        return;
-    }
-    TQT_REQUIRE(k % 2 == 0, "k % 2 == 0");
-    TQT_REQUIRE(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "dimension exceeds 2^31-1");
-    TQT_REQUIRE(params->scale_a && params->zero_point_a && params->scale_b,
-                "params arrays must be non-NULL");
-    TQT_REQUIRE((A != nullptr && B != nullptr) || k == 0, "A/B == NULL");
-    TQT_REQUIRE(D != nullptr, "D == NULL");
-    W4A8Args a = {};
-    a.M = static_cast<int>(m);
-    a.N = static_cast<int>(n);
-    a.K = static_cast<int>(k);
-    a.A = static_cast<const int8_t *>(A);
-    a.lda = static_cast<long long>(lda);
-    a.B = static_cast<const uint8_t *>(B);
-    a.bstride = static_cast<long long>(ldb / 2);
-    a.C = static_cast<const float *>(C);
-    a.ldc = static_cast<long long>(ldc);
-    a.D = static_cast<float *>(D);
-    a.ldd = static_cast<long long>(ldd);
-    a.bias = static_cast<const float *>(bias);
-    a.cmin = clamp_min;
-    a.cmax = clamp_max;
-    a.scale_a = params->scale_a;
-    a.zp_a = params->zero_point_a;
-    a.scale_b = params->scale_b;
-    hipStream_t s = as_stream(stream);
-    const bool fast = (k % kPairK == 0) && k <= 65536 && (lda % 16 == 0) &&
-                      ((ldb / 2) % 16 == 0) && aligned16(A) && aligned16(B) &&
-                      (m + kRowsPerChunk - 1) / kRowsPerChunk < 65536;
-    if (fast) {
-        const unsigned gx = static_cast<unsigned>((n + kNTile - 1) / kNTile);
-        const unsigned long long gy = (m + kRowsPerChunk - 1) / kRowsPerChunk;
-        const size_t rows_max = m < static_cast<size_t>(kRowsPerChunk) ? m : kRowsPerChunk;
-        const size_t npairs = k / kPairK;
-        const size_t ppw = (npairs + kWaves - 1) / kWaves;
-        if (rows_max * ppw * 16 <= 64) {  // each wave's activation slice: one chunk per lane
-            hipLaunchKernelGGL(w4a8_mfma_kernel<true>, dim3(gx, static_cast<unsigned>(gy)),
-                               dim3(kWaves * 64), 0, s, a);
-        } else {
-            hipLaunchKernelGGL(w4a8_mfma_kernel<false>, dim3(gx, static_cast<unsigned>(gy)),
-                               dim3(kWaves * 64), 0, s, a);
-        }
-    } else {
-        const long long total = static_cast<long long>(m) * static_cast<long long>(n);
-        const long long blocks = (total + 255) / 256;
-        TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
-        hipLaunchKernelGGL(w4a8_generic_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                           s, a);
-    }
-    check_launch("tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950");
+    w4a8_run(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min, clamp_max,
+             params, false, as_stream(stream),
+             "tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950");
 }
 
 void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950(
@@ -427,6 +502,36 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950(
         m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min, clamp_max,
         params, nullptr);
     finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950");
+}
+
+// gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp (reference …qai8dxp_qsi4cxp_4x1vl_rvv.cpp:113-190; its
+// geometry getters and packers are in packing.hip). The reference run reads tile bases as
+// m_idx * k and n_idx * k / 2 and ignores k_idx; this run reads panels with lda / ldb and the
+// k_idx tail rule, as the packers write them (the same bytes for the packers' lda = k, k_idx = 0).
+void tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, float clamp_min, float clamp_max,
+    const struct tqt_qai8dx_qsi4cx_params *params, void *stream)
+{
+    w4a8_run(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd, bias,
+             clamp_min, clamp_max, params, true, as_stream(stream),
+             "tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, float clamp_min, float clamp_max,
+    const struct tqt_qai8dx_qsi4cx_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950_async(
+        m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min,
+        clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
 }
 
 }  // extern "C"

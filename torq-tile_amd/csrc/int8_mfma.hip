@@ -18,6 +18,10 @@
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
 #include "tqt_gemm_clamp_i32_i8_i8_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_clamp_i32_i8p_i8p_mfma_gfx950.h"
+#include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -65,6 +69,7 @@ struct Int8Args
     float scale_d;
     int32_t zp_d;
     ConvGeom cv;
+    PackDesc pa, pb;  // packed A / B of the p-variants (read when the kernel's PK bit is set)
 };
 
 // LDS tile of R rows x 64 bytes. The 16-byte column chunk of row r is XOR-swizzled with
@@ -75,7 +80,7 @@ __device__ __forceinline__ int lds_off(int row, int chunk)
     return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
-template <int BM, int AM, int BMd, int EPI>
+template <int BM, int AM, int BMd, int EPI, int PK>
 __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 {
     constexpr int WM = BM / 2;        // rows per wave
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     }
 
     // Per-thread load assignment (fixed across the K loop).
-    int a_row[A_CHUNKS], a_chk[A_CHUNKS];
+    int a_row[A_CHUNKS], a_chk[A_CHUNKS], a_mul[A_CHUNKS];
     bool a_ok[A_CHUNKS];
     int a_od[A_CHUNKS], a_oh[A_CHUNKS], a_ow[A_CHUNKS];
     const int8_t *a_ptr[A_CHUNKS];
@@ -140,8 +145,16 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
         a_chk[j] = c & 3;
         const int gm = m0 + a_row[j];
         a_ok[j] = gm < a.M;
+        a_mul[j] = 1;  // byte kb of a packed row is at kb * (panel width) from its chunk 0
         if constexpr (AM == A_MATRIX) {
-            a_ptr[j] = a.A + static_cast<long long>(a_ok[j] ? gm : 0) * a.lda + a_chk[j] * 16;
+            const int r = a_ok[j] ? gm : 0;
+            long long base;
+            if constexpr ((PK & PK_A) != 0) {
+                base = pack_row(a.pa, r, a_mul[j]);
+            } else {
+                base = static_cast<long long>(r) * a.lda;
+            }
+            a_ptr[j] = a.A + base + a_chk[j] * 16 * a_mul[j];
             a_od[j] = a_oh[j] = a_ow[j] = 0;
         } else {
             // a_od/a_oh/a_ow hold the first input coordinate of the output pixel's window
@@ -155,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                                  g.IC;
         }
     }
-    int b_row[B_CHUNKS], b_chk[B_CHUNKS];
+    int b_row[B_CHUNKS], b_chk[B_CHUNKS], b_mul[B_CHUNKS];
     bool b_ok[B_CHUNKS];
     const int8_t *b_ptr[B_CHUNKS];
 #pragma unroll
@@ -166,7 +179,15 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             b_chk[j] = c & 3;   // 16-byte k chunk
             const int gn = n0 + b_row[j];
             b_ok[j] = gn < a.N;
-            b_ptr[j] = a.B + static_cast<long long>(b_ok[j] ? gn : 0) * a.ldb + b_chk[j] * 16;
+            const int r = b_ok[j] ? gn : 0;
+            long long base;
+            b_mul[j] = 1;
+            if constexpr ((PK & PK_B) != 0) {
+                base = pack_row(a.pb, r, b_mul[j]);
+            } else {
+                base = static_cast<long long>(r) * a.ldb;
+            }
+            b_ptr[j] = a.B + base + b_chk[j] * 16 * b_mul[j];
         } else {
             // one wave covers 64 consecutive k of one 16-column chunk, so each byte store of
             // the transpose below writes 64 consecutive bytes of one LDS row (no bank conflicts
@@ -175,6 +196,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             b_chk[j] = c >> 6;  // 16-column chunk
             const int gn = n0 + b_chk[j] * 16;
             b_ok[j] = gn < a.N;
+            b_mul[j] = 1;
             b_ptr[j] = a.B + (b_ok[j] ? gn : 0);
         }
     }
@@ -198,7 +220,8 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             bool ok = a_ok[j] && k < a.K;
             const int8_t *src;
             if constexpr (AM == A_MATRIX) {
-                src = ok ? a_ptr[j] + k0 : a_ptr[j] - a_chk[j] * 16;
+                src = ok ? a_ptr[j] + static_cast<long long>(k0) * a_mul[j]
+                         : a_ptr[j] - a_chk[j] * 16 * a_mul[j];
             } else {
                 const ConvGeom &g = a.cv;
                 const int2 t = s_tap[ok ? k >> 4 : 0];
@@ -216,8 +239,9 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             if constexpr (BMd == B_NK) {
                 const int k = k0 + b_chk[j] * 16;
                 const bool ok = b_ok[j] && k < a.K;
-                st.b[j] = *reinterpret_cast<const i32x4 *>(ok ? b_ptr[j] + k0
-                                                              : b_ptr[j] - b_chk[j] * 16);
+                st.b[j] = *reinterpret_cast<const i32x4 *>(
+                    ok ? b_ptr[j] + static_cast<long long>(k0) * b_mul[j]
+                       : b_ptr[j] - b_chk[j] * 16 * b_mul[j]);
                 st.bm |= ok ? (1u << j) : 0u;
             } else {
                 const int k = k0 + b_row[j];
@@ -401,7 +425,7 @@ __host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm)
     return (vm & 15) | (7 << 4) | ((vm >> 4) << 14);
 }
 
-template <int BM, int AM, int EPI>
+template <int BM, int AM, int EPI, int PK>
 __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int tiles_m, int tiles,
                                                                int per_xcd)
 {
@@ -445,15 +469,22 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     const int lrow = lane >> 3;
     const int lslot = lane & 7;
     const int8_t *a_row[A_DMA];
-    int a_chunk[A_DMA];
+    int a_chunk[A_DMA], a_mul[A_DMA];
     int a_id0[A_DMA], a_ih0[A_DMA], a_iw0[A_DMA];
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) {
         const int r = 8 * (wave * A_DMA + j) + lrow;
         a_chunk[j] = lslot ^ ((r >> 1) & 7);
         const int gm = min(m0 + r, a.M - 1);
+        a_mul[j] = 1;  // byte kb of a packed row is at kb * (panel width) from its chunk 0
         if constexpr (AM == A_MATRIX) {
-            a_row[j] = a.A + static_cast<long long>(gm) * a.lda + a_chunk[j] * 16;
+            long long base;
+            if constexpr ((PK & PK_A) != 0) {
+                base = pack_row(a.pa, gm, a_mul[j]);
+            } else {
+                base = static_cast<long long>(gm) * a.lda;
+            }
+            a_row[j] = a.A + base + a_chunk[j] * 16 * a_mul[j];
             a_id0[j] = a_ih0[j] = a_iw0[j] = 0;
         } else {
             const ConvGeom &g = a.cv;
@@ -469,11 +500,19 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         }
     }
     const int8_t *b_row[B_DMA];
+    int b_mul[B_DMA];
 #pragma unroll
     for (int j = 0; j < B_DMA; ++j) {
         const int r = 8 * (wave * B_DMA + j) + lrow;
         const int gn = min(n0 + r, a.N - 1);
-        b_row[j] = a.B + static_cast<long long>(gn) * a.ldb + (lslot ^ ((r >> 1) & 7)) * 16;
+        long long base;
+        b_mul[j] = 1;
+        if constexpr ((PK & PK_B) != 0) {
+            base = pack_row(a.pb, gn, b_mul[j]);
+        } else {
+            base = static_cast<long long>(gn) * a.ldb;
+        }
+        b_row[j] = a.B + base + (lslot ^ ((r >> 1) & 7)) * 16 * b_mul[j];
     }
 
     auto issue = [&](int st, int8_t *sa, int8_t *sb) {
@@ -482,7 +521,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         for (int j = 0; j < A_DMA; ++j) {
             const int8_t *src;
             if constexpr (AM == A_MATRIX) {
-                src = a_row[j] + k0;
+                src = a_row[j] + static_cast<long long>(k0) * a_mul[j];
             } else {
                 const ConvGeom &g = a.cv;
                 const int k = k0 + a_chunk[j] * 16;
@@ -507,8 +546,8 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
 #pragma unroll
         for (int j = 0; j < B_DMA; ++j) {
 #if defined(__HIP_DEVICE_COMPILE__)
-            __builtin_amdgcn_global_load_lds(b_row[j] + k0, sb + (wave * B_DMA + j) * 1024, 16, 0,
-                                             0);
+            __builtin_amdgcn_global_load_lds(b_row[j] + static_cast<long long>(k0) * b_mul[j],
+                                             sb + (wave * B_DMA + j) * 1024, 16, 0, 0);
 #endif
         }
     };
@@ -648,7 +687,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
 }
 
 // Generic path: one thread per output, any strides and any K.
-template <int AM, int BMd, int EPI>
+template <int AM, int BMd, int EPI, int PK>
 __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
 {
     const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -660,11 +699,22 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     const int gn = static_cast<int>(idx - static_cast<long long>(gm) * a.N);
     uint32_t acc = 0;
     if constexpr (AM == A_MATRIX) {
-        const int8_t *arow = a.A + static_cast<long long>(gm) * a.lda;
-        for (int k = 0; k < a.K; ++k) {
-            const int32_t bv = (BMd == B_NK) ? a.B[static_cast<long long>(gn) * a.ldb + k]
-                                             : a.B[static_cast<long long>(k) * a.ldb + gn];
-            acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * bv);
+        if constexpr (PK == PK_NONE) {
+            const int8_t *arow = a.A + static_cast<long long>(gm) * a.lda;
+            for (int k = 0; k < a.K; ++k) {
+                const int32_t bv = (BMd == B_NK) ? a.B[static_cast<long long>(gn) * a.ldb + k]
+                                                 : a.B[static_cast<long long>(k) * a.ldb + gn];
+                acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * bv);
+            }
+        } else {
+            // packed operands (B_NK): the same sum, addressed through the panel layout; the run
+            // functions of the p-variants describe an unpacked operand with step 0 (row-major)
+            const PackRow ra = pack_row_info(a.pa, gm);
+            const PackRow rb = pack_row_info(a.pb, gn);
+            for (int k = 0; k < a.K; ++k) {
+                acc += static_cast<uint32_t>(static_cast<int32_t>(a.A[pack_row_byte(ra, k)]) *
+                                             static_cast<int32_t>(a.B[pack_row_byte(rb, k)]));
+            }
         }
     } else {
         const ConvGeom &g = a.cv;
@@ -674,6 +724,8 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
         const int oh = static_cast<int>((p / g.OW) % g.OH);
         const int ow = static_cast<int>(p % g.OW);
         const int8_t *w = a.B + static_cast<long long>(gn) * a.ldb;
+        const PackRow rw = pack_row_info(a.pb, gn);  // used when the weights are packed
+        long long kb = 0;                            // k of the current tap's first channel
         const int taps = a.K / g.ICg;
         for (int tap = 0; tap < taps; ++tap) {
             const int kw = tap % g.KW;
@@ -687,9 +739,12 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
                 inb ? a.A + ((static_cast<long long>(id) * g.IH + ih) * g.IW + iw) * g.IC : nullptr;
             for (int ic = 0; ic < g.ICg; ++ic) {
                 const int32_t av = src ? static_cast<int32_t>(src[ic]) : 0;
-                acc += static_cast<uint32_t>(av * static_cast<int32_t>(w[ic]));
+                const int32_t wv = (PK & PK_B) ? static_cast<int32_t>(a.B[pack_row_byte(rw, kb + ic)])
+                                               : static_cast<int32_t>(w[ic]);
+                acc += static_cast<uint32_t>(av * wv);
             }
             w += g.ICg;
+            kb += g.ICg;
         }
     }
     if (a.C) {
@@ -712,7 +767,7 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     }
 }
 
-template <int AM, int EPI>
+template <int AM, int EPI, int PK>
 void launch_stream(const Int8Args &a, hipStream_t stream)
 {
     const long long tiles_n = (a.N + kBN - 1) / kBN;
@@ -725,17 +780,17 @@ void launch_stream(const Int8Args &a, hipStream_t stream)
     const long long per_xcd = (tiles + 7) / 8;
     TQT_REQUIRE(tiles < (1ll << 30), "grid too large");
     if (big) {
-        hipLaunchKernelGGL((int8_stream_kernel<128, AM, EPI>), dim3(8 * per_xcd), dim3(kThreads), 0,
+        hipLaunchKernelGGL((int8_stream_kernel<128, AM, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
                            stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
                            static_cast<int>(per_xcd));
     } else {
-        hipLaunchKernelGGL((int8_stream_kernel<64, AM, EPI>), dim3(8 * per_xcd), dim3(kThreads), 0,
+        hipLaunchKernelGGL((int8_stream_kernel<64, AM, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
                            stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
                            static_cast<int>(per_xcd));
     }
 }
 
-template <int AM, int BMd, int EPI>
+template <int AM, int BMd, int EPI, int PK = PK_NONE>
 void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *where)
 {
     if (a.M <= 0 || a.N <= 0) {
@@ -746,7 +801,7 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
     // kernel is faster.
     if constexpr (BMd == B_NK && AM == A_MATRIX) {
         if (fast && a.K % kSK == 0) {
-            launch_stream<AM, EPI>(a, stream);
+            launch_stream<AM, EPI, PK>(a, stream);
             check_launch(where);
             return;
         }
@@ -758,19 +813,19 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
         if (tiles_m128 * tiles_n >= 256) {
             const long long blocks = tiles_m128 * tiles_n;
             TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
-            hipLaunchKernelGGL((int8_mfma_kernel<128, AM, BMd, EPI>), dim3(blocks), dim3(kThreads),
+            hipLaunchKernelGGL((int8_mfma_kernel<128, AM, BMd, EPI, PK>), dim3(blocks), dim3(kThreads),
                                0, stream, a);
         } else {
             const long long blocks = ((a.M + 63) / 64) * static_cast<long long>(tiles_n);
             TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
-            hipLaunchKernelGGL((int8_mfma_kernel<64, AM, BMd, EPI>), dim3(blocks), dim3(kThreads),
+            hipLaunchKernelGGL((int8_mfma_kernel<64, AM, BMd, EPI, PK>), dim3(blocks), dim3(kThreads),
                                0, stream, a);
         }
     } else {
         const long long total = static_cast<long long>(a.M) * a.N;
         const long long blocks = (total + 255) / 256;
         TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
-        hipLaunchKernelGGL((int8_generic_kernel<AM, BMd, EPI>), dim3(blocks), dim3(256), 0, stream,
+        hipLaunchKernelGGL((int8_generic_kernel<AM, BMd, EPI, PK>), dim3(blocks), dim3(256), 0, stream,
                            a);
     }
     check_launch(where);
@@ -784,6 +839,135 @@ Int8Args base_args(size_t m, size_t n, size_t k)
     a.N = static_cast<int>(n);
     a.K = static_cast<int>(k);
     return a;
+}
+
+
+// Shared body of the igemmcl runs: fills the arguments from the conv geometry and launches.
+// `packed`: the weights are in the packed layout (k_idx_b applies the tail rule).
+void igemm_run(size_t m, size_t n, const void *input, size_t group_idx, size_t m_idx,
+               const void *B, size_t ldb, size_t k_idx_b, void *D, size_t ldd, const void *bias,
+               int8_t clamp_min, int8_t clamp_max, const tqt_conv_params *conv_params,
+               const struct tqt_qai8_qai8_qsi8cx_params *quant_params, bool packed,
+               hipStream_t stream, const char *where)
+{
+    if (!conv_params || !quant_params) {
+        return;  // reference …igemmcl…cpp:206-208
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    const tqt_conv_params &p = *conv_params;
+    TQT_REQUIRE(p.groups >= 1 && p.input_channel % p.groups == 0, "input_channel % groups != 0");
+    TQT_REQUIRE(quant_params->scale_b != nullptr, "quant_params->scale_b == NULL");
+    TQT_REQUIRE(input != nullptr && B != nullptr && D != nullptr, "NULL tensor pointer");
+    const size_t icg = p.input_channel / p.groups;
+    const size_t kfull = p.kernel_shape[0] * p.kernel_shape[1] * p.kernel_shape[2] * icg;
+    for (int i = 0; i < 3; ++i) {
+        TQT_REQUIRE(p.input_shape[i] < (1u << 30) && p.output_shape[i] < (1u << 30) &&
+                        p.kernel_shape[i] < (1u << 15) && p.stride[i] < (1u << 15) &&
+                        p.dilation[i] < (1u << 15) && p.pad[i] < (1u << 15),
+                    "conv geometry out of range");
+    }
+    TQT_REQUIRE(p.input_channel < (1u << 30), "input_channel out of range");
+    Int8Args a = base_args(m, n, kfull);
+    a.A = static_cast<const int8_t *>(input) + group_idx * icg;
+    a.B = static_cast<const int8_t *>(B);
+    a.ldb = static_cast<long long>(ldb);
+    a.D = D;
+    a.ldd = static_cast<long long>(ldd);
+    a.d_row0 = static_cast<long long>(m_idx);
+    a.p0 = static_cast<long long>(m_idx);
+    a.bias = static_cast<const int32_t *>(bias);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    a.scale_a = quant_params->scale_a;
+    a.scale_b = quant_params->scale_b;
+    a.quant_channel_b = quant_params->quant_channel_b;
+    a.scale_d = quant_params->scale_d;
+    a.zp_d = quant_params->zero_point_d;
+    ConvGeom &g = a.cv;
+    g.ID = static_cast<int>(p.input_shape[0]);
+    g.IH = static_cast<int>(p.input_shape[1]);
+    g.IW = static_cast<int>(p.input_shape[2]);
+    g.OH = static_cast<int>(p.output_shape[1]);
+    g.OW = static_cast<int>(p.output_shape[2]);
+    g.KH = static_cast<int>(p.kernel_shape[1]);
+    g.KW = static_cast<int>(p.kernel_shape[2]);
+    g.SD = static_cast<int>(p.stride[0]);
+    g.SH = static_cast<int>(p.stride[1]);
+    g.SW = static_cast<int>(p.stride[2]);
+    g.DD = static_cast<int>(p.dilation[0]);
+    g.DH = static_cast<int>(p.dilation[1]);
+    g.DW = static_cast<int>(p.dilation[2]);
+    g.PD = static_cast<int>(p.pad[0]);
+    g.PH = static_cast<int>(p.pad[1]);
+    g.PW = static_cast<int>(p.pad[2]);
+    g.IC = static_cast<int>(p.input_channel);
+    g.ICg = static_cast<int>(icg);
+    TQT_REQUIRE(g.OH > 0 && g.OW > 0 && icg > 0, "empty conv geometry");
+    // fast path: 16-byte channel runs, a tap table that fits LDS, tap extents that pack into
+    // 10 bits each, and input offsets that fit 31 bits
+    const size_t in_bytes = p.input_shape[0] * p.input_shape[1] * p.input_shape[2] *
+                            static_cast<size_t>(p.input_channel);
+    const bool geo_fast = (icg % 16 == 0) && (p.input_channel % 16 == 0) && aligned16(a.A) &&
+                          aligned16(B) && kfull / 16 <= kConvMaxChunks &&
+                          (p.kernel_shape[0] - 1) * p.dilation[0] < 1024 &&
+                          (p.kernel_shape[1] - 1) * p.dilation[1] < 1024 &&
+                          (p.kernel_shape[2] - 1) * p.dilation[2] < 1024 && in_bytes < (1ull << 31);
+    if (packed) {
+        TQT_REQUIRE(ldb >= kfull, "ldb < k");
+        a.pb = make_pack(kPackI8NStep, n, ldb, kfull, k_idx_b);
+        launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8, PK_B>(a, geo_fast && k_idx_b % 16 == 0,
+                                                           stream, where);
+    } else {
+        launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8>(a, geo_fast && ldb % 16 == 0, stream, where);
+    }
+}
+
+// Requantization parameters of the qai8 x qsi8cx kernels.
+void set_requant(Int8Args &a, const void *bias, int8_t clamp_min, int8_t clamp_max,
+                 const struct tqt_qai8_qai8_qsi8cx_params *params)
+{
+    a.bias = static_cast<const int32_t *>(bias);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    a.scale_a = params->scale_a;
+    a.scale_b = params->scale_b;
+    a.quant_channel_b = params->quant_channel_b;
+    a.scale_d = params->scale_d;
+    a.zp_d = params->zero_point_d;
+}
+
+// Shared body of the packed int8 GEMM runs: A packed when a_packed (else row-major with lda),
+// B always packed; k_idx_a / k_idx_b apply the packers' tail rule.
+template <int EPI>
+void packed_gemm_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a,
+                     bool a_packed, const void *B, size_t ldb, size_t k_idx_b, const void *C,
+                     size_t ldc, void *D, size_t ldd, Int8Args a, hipStream_t stream,
+                     const char *where)
+{
+    TQT_REQUIRE(A != nullptr || k == 0, "A == NULL");
+    TQT_REQUIRE(B != nullptr || k == 0, "B == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    TQT_REQUIRE(ldb >= k && lda >= k, "lda or ldb < k");
+    a.A = static_cast<const int8_t *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const int8_t *>(B);
+    a.ldb = static_cast<long long>(ldb);
+    a.C = static_cast<const int32_t *>(C);
+    a.ldc = static_cast<long long>(ldc);
+    a.D = D;
+    a.ldd = static_cast<long long>(ldd);
+    a.pa = make_pack(a_packed ? kPackI8MStep : 0, m, lda, k, a_packed ? k_idx_a : 0);
+    a.pb = make_pack(kPackI8NStep, n, ldb, k, k_idx_b);
+    // fast paths read 16-byte chunks: every chunk of a packed row must start 16-byte aligned
+    const bool fast = (k % 16 == 0) && aligned16(A) && aligned16(B) && (k_idx_b % 16 == 0) &&
+                      (a_packed ? k_idx_a % 16 == 0 : lda % 16 == 0);
+    if (a_packed) {
+        launch_int8<A_MATRIX, B_NK, EPI, PK_AB>(a, fast, stream, where);
+    } else {
+        launch_int8<A_MATRIX, B_NK, EPI, PK_B>(a, fast, stream, where);
+    }
 }
 
 }  // namespace
@@ -1050,76 +1234,11 @@ void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx95
 {
     (void)k;
     (void)k_idx_a;
-    (void)k_idx_b;
     (void)C;
     (void)ldc;
-    if (!conv_params || !quant_params) {
-        return;  // reference …igemmcl…cpp:206-208
-    }
-    if (m == 0 || n == 0) {
-        return;
-    }
-    const tqt_conv_params &p = *conv_params;
-    TQT_REQUIRE(p.groups >= 1 && p.input_channel % p.groups == 0, "input_channel % groups != 0");
-    TQT_REQUIRE(quant_params->scale_b != nullptr, "quant_params->scale_b == NULL");
-    TQT_REQUIRE(input != nullptr && B != nullptr && D != nullptr, "NULL tensor pointer");
-    const size_t icg = p.input_channel / p.groups;
-    const size_t kfull = p.kernel_shape[0] * p.kernel_shape[1] * p.kernel_shape[2] * icg;
-    for (int i = 0; i < 3; ++i) {
-        TQT_REQUIRE(p.input_shape[i] < (1u << 30) && p.output_shape[i] < (1u << 30) &&
-                        p.kernel_shape[i] < (1u << 15) && p.stride[i] < (1u << 15) &&
-                        p.dilation[i] < (1u << 15) && p.pad[i] < (1u << 15),
-                    "conv geometry out of range");
-    }
-    TQT_REQUIRE(p.input_channel < (1u << 30), "input_channel out of range");
-    Int8Args a = base_args(m, n, kfull);
-    a.A = static_cast<const int8_t *>(input) + group_idx * icg;
-    a.B = static_cast<const int8_t *>(B);
-    a.ldb = static_cast<long long>(ldb);
-    a.D = D;
-    a.ldd = static_cast<long long>(ldd);
-    a.d_row0 = static_cast<long long>(m_idx);
-    a.p0 = static_cast<long long>(m_idx);
-    a.bias = static_cast<const int32_t *>(bias);
-    a.cmin = clamp_min;
-    a.cmax = clamp_max;
-    a.scale_a = quant_params->scale_a;
-    a.scale_b = quant_params->scale_b;
-    a.quant_channel_b = quant_params->quant_channel_b;
-    a.scale_d = quant_params->scale_d;
-    a.zp_d = quant_params->zero_point_d;
-    ConvGeom &g = a.cv;
-    g.ID = static_cast<int>(p.input_shape[0]);
-    g.IH = static_cast<int>(p.input_shape[1]);
-    g.IW = static_cast<int>(p.input_shape[2]);
-    g.OH = static_cast<int>(p.output_shape[1]);
-    g.OW = static_cast<int>(p.output_shape[2]);
-    g.KH = static_cast<int>(p.kernel_shape[1]);
-    g.KW = static_cast<int>(p.kernel_shape[2]);
-    g.SD = static_cast<int>(p.stride[0]);
-    g.SH = static_cast<int>(p.stride[1]);
-    g.SW = static_cast<int>(p.stride[2]);
-    g.DD = static_cast<int>(p.dilation[0]);
-    g.DH = static_cast<int>(p.dilation[1]);
-    g.DW = static_cast<int>(p.dilation[2]);
-    g.PD = static_cast<int>(p.pad[0]);
-    g.PH = static_cast<int>(p.pad[1]);
-    g.PW = static_cast<int>(p.pad[2]);
-    g.IC = static_cast<int>(p.input_channel);
-    g.ICg = static_cast<int>(icg);
-    TQT_REQUIRE(g.OH > 0 && g.OW > 0 && icg > 0, "empty conv geometry");
-    // fast path: 16-byte channel runs, a tap table that fits LDS, tap extents that pack into
-    // 10 bits each, and input offsets that fit 31 bits
-    const size_t in_bytes = p.input_shape[0] * p.input_shape[1] * p.input_shape[2] *
-                            static_cast<size_t>(p.input_channel);
-    const bool fast = (icg % 16 == 0) && (p.input_channel % 16 == 0) && (ldb % 16 == 0) &&
-                      aligned16(a.A) && aligned16(B) && kfull / 16 <= kConvMaxChunks &&
-                      (p.kernel_shape[0] - 1) * p.dilation[0] < 1024 &&
-                      (p.kernel_shape[1] - 1) * p.dilation[1] < 1024 &&
-                      (p.kernel_shape[2] - 1) * p.dilation[2] < 1024 && in_bytes < (1ull << 31);
-    launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8>(
-        a, fast, as_stream(stream),
-        "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
+    igemm_run(m, n, input, group_idx, m_idx, B, ldb, k_idx_b, D, ldd, bias, clamp_min, clamp_max,
+              conv_params, quant_params, false, as_stream(stream),
+              "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
 }
 
 void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(
@@ -1139,6 +1258,149 @@ void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx95
         clamp_min, clamp_max, conv_params, quant_params, nullptr);
     finish_sync(nullptr,
                 "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950");
+}
+
+// =============================================================================================
+// Packed int8 runs (geometry getters and packers: packing.hip). The reference runs walk
+// m_step x n_step tiles of panel pointers (…gemm_clamp_i32_i8p_i8p_4x1vl_rvv.cpp,
+// …qai8_qai8_qsi8cxp…cpp, …qai8_qai8p_qsi8cxp…cpp, igemmcl…qsi8cxp…cpp:202-300); here one
+// launch covers the problem and each row finds its panel. Panel 0 is never shifted by k_idx
+// (the packers' rule; the reference's runs would read before the buffer for n < n_step).
+// =============================================================================================
+
+void tqt_run_gemm_clamp_i32_i8p_i8p_mfma_gfx950_async(size_t m, size_t n, size_t k,
+                                                      const void *A_packed, size_t lda,
+                                                      size_t k_idx_a, const void *B_packed,
+                                                      size_t ldb, size_t k_idx_b, const void *C,
+                                                      size_t ldc, void *D, size_t ldd,
+                                                      int32_t clamp_min, int32_t clamp_max,
+                                                      void *stream)
+{
+    if (m == 0 || n == 0) {
+        return;
+    }
+    Int8Args a = base_args(m, n, k);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    packed_gemm_run<EPI_CLAMP_I32>(m, n, k, A_packed, lda, k_idx_a, true, B_packed, ldb, k_idx_b,
+                                   C, ldc, D, ldd, a, as_stream(stream),
+                                   "tqt_run_gemm_clamp_i32_i8p_i8p_mfma_gfx950");
+}
+
+void tqt_run_gemm_clamp_i32_i8p_i8p_mfma_gfx950(size_t m, size_t n, size_t k, const void *A_packed,
+                                                size_t lda, size_t k_idx_a, const void *B_packed,
+                                                size_t ldb, size_t k_idx_b, const void *C,
+                                                size_t ldc, void *D, size_t ldd,
+                                                int32_t clamp_min, int32_t clamp_max)
+{
+    if (m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_clamp_i32_i8p_i8p_mfma_gfx950_async(m, n, k, A_packed, lda, k_idx_a, B_packed,
+                                                     ldb, k_idx_b, C, ldc, D, ldd, clamp_min,
+                                                     clamp_max, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_clamp_i32_i8p_i8p_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B_packed,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qai8_qsi8cx_params *params,
+    void *stream)
+{
+    if (!params) {
+        return;  // reference …qai8_qai8_qsi8cxp…cpp (as …qsi8cxt…cpp:148-150)
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    TQT_REQUIRE(params->scale_b != nullptr, "params->scale_b == NULL");
+    Int8Args a = base_args(m, n, k);
+    set_requant(a, bias, clamp_min, clamp_max, params);
+    packed_gemm_run<EPI_REQUANT_I8>(
+        m, n, k, A, lda, k_idx_a, false, B_packed, ldb, k_idx_b, C, ldc, D, ldd, a,
+        as_stream(stream), "tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B_packed,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qai8_qsi8cx_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950_async(
+        m, n, k, A, lda, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min,
+        clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const struct tqt_qai8_qai8_qsi8cx_params *params, void *stream)
+{
+    if (!params) {
+        return;  // reference …qai8_qai8p_qsi8cxp…cpp (as …qsi8cxt…cpp:148-150)
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    TQT_REQUIRE(params->scale_b != nullptr, "params->scale_b == NULL");
+    Int8Args a = base_args(m, n, k);
+    set_requant(a, bias, clamp_min, clamp_max, params);
+    packed_gemm_run<EPI_REQUANT_I8>(
+        m, n, k, A_packed, lda, k_idx_a, true, B_packed, ldb, k_idx_b, C, ldc, D, ldd, a,
+        as_stream(stream), "tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const struct tqt_qai8_qai8_qsi8cx_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950_async(
+        m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min,
+        clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950");
+}
+
+void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t m_idx,
+    size_t k_idx_a, const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qai8_qsi8cx_params *quant_params,
+    void *stream)
+{
+    (void)k;
+    (void)k_idx_a;
+    (void)C;
+    (void)ldc;
+    igemm_run(m, n, input, group_idx, m_idx, B_packed, ldb, k_idx_b, D, ldd, bias, clamp_min,
+              clamp_max, conv_params, quant_params, true, as_stream(stream),
+              "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
+}
+
+void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t m_idx,
+    size_t k_idx_a, const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qai8_qsi8cx_params *quant_params)
+{
+    if (!conv_params || !quant_params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950_async(
+        m, n, k, input, group_idx, m_idx, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd, bias,
+        clamp_min, clamp_max, conv_params, quant_params, nullptr);
+    finish_sync(nullptr,
+                "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
 }
 
 const char *tqt_gfx950_target(void)

@@ -146,6 +146,134 @@ __device__ __forceinline__ void column_multiplier_dev(float scale_a, const float
     quantize_multiplier_dev(real, mult, shift);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Packed operand layout of the p-variants (the reference's packers are permutations A [m, k] ->
+// [m/MR, k, MR] and B^T [n, k] -> [n/vl, k, vl], tqt_gemm_pack_rvv.h:542-567, 740-856; this is
+// the gfx950 one). Rows (m of A, n of B) form panels of `step` rows: panel p holds rows
+// [p*step, p*step + w), w = min(step, rows - p*step), and starts at byte p*step*ld, moved back by
+// shift*(step - w) bytes when a panel after the first is narrower (shift = k_idx in bytes: the
+// reference's tail-tile rule, tqt_gemm_pack_rvv.h:314-318). Inside a panel each row is cut into
+// 16-byte chunks - one MFMA lane fragment, 16 consecutive k bytes of one row - stored chunk-major:
+// chunk c of local row r at 16*c*w + r*cw, cw = min(16, kbytes - 16*c). One k-step of a whole
+// panel is thus one contiguous block whose fragments come in the order MFMA lanes take them
+// (lane l <-> row l mod 16 or 32), and when kbytes % 16 == 0 byte kb (a multiple of 16) of row r
+// sits at row_base(r) + kb * w. A panel of w rows holds w * kbytes bytes, so the packed sizes are
+// the unpacked ones (m*k, n*k, n*k/2).
+// ---------------------------------------------------------------------------------------------
+// Panel heights (m_step / n_step) of the packed kernel types.
+constexpr size_t kPackI8MStep = 128;   // int8 GEMMs and igemmcl (A and B panels)
+constexpr size_t kPackI8NStep = 128;
+constexpr size_t kPackW4A8MStep = 16;  // W4A8: one 16-channel weight tile per panel
+constexpr size_t kPackW4A8NStep = 16;
+constexpr size_t kPackW4A16MStep = 32; // W4A16: one 32-row activation group, 16 channels
+constexpr size_t kPackW4A16NStep = 16;
+
+// Which operands of a kernel instance are in the packed layout; plain row-major otherwise.
+enum PackMode { PK_NONE = 0, PK_A = 1, PK_B = 2, PK_AB = 3 };
+
+struct PackDesc
+{
+    long long ld;      // bytes per row of panel stride: panel p starts at p * step * ld
+    long long kbytes;  // bytes of each row held in the panels
+    long long shift;   // k_idx in bytes (tail panels after the first start shift*(step-w) earlier)
+    int step;          // rows per panel; 0 = plain row-major (row r at r * ld)
+    int rows;          // rows of the operand
+};
+
+__host__ __device__ inline long long pack_panel_base(const PackDesc &d, int p, int w)
+{
+    long long b = static_cast<long long>(p) * d.step * d.ld;
+    if (p > 0 && w < d.step) {
+        b -= d.shift * (d.step - w);
+    }
+    return b;
+}
+
+// Placement of one row: its panel's base, the panel width and the row's index in the panel
+// (a plain row-major operand is the case w = 1, rl = 0, base = r * ld).
+struct PackRow
+{
+    long long base;
+    long long kbytes;
+    int w, rl;
+};
+
+__host__ __device__ inline PackRow pack_row_info(const PackDesc &d, int r)
+{
+    PackRow pr;
+    pr.kbytes = d.kbytes;
+    if (d.step == 0) {
+        pr.base = static_cast<long long>(r) * d.ld;
+        pr.w = 1;
+        pr.rl = 0;
+        return pr;
+    }
+    const int p = r / d.step;
+    const int left = d.rows - p * d.step;
+    pr.w = left < d.step ? left : d.step;
+    pr.rl = r - p * d.step;
+    pr.base = pack_panel_base(d, p, pr.w);
+    return pr;
+}
+
+// Byte offset of byte kb (any kb < kbytes) of the row.
+__host__ __device__ inline long long pack_row_byte(const PackRow &pr, long long kb)
+{
+    const long long c = kb >> 4;
+    const long long rem = pr.kbytes - 16 * c;
+    const long long cw = rem < 16 ? rem : 16;
+    return pr.base + 16 * c * pr.w + pr.rl * cw + (kb & 15);
+}
+
+__host__ __device__ inline long long pack_offset(const PackDesc &d, int r, long long kb)
+{
+    return pack_row_byte(pack_row_info(d, r), kb);
+}
+
+// For kbytes % 16 == 0: byte kb (a multiple of 16) of row r is at the returned offset + kb * mul.
+__host__ __device__ inline long long pack_row(const PackDesc &d, int r, int &mul)
+{
+    if (d.step == 0) {
+        mul = 1;
+        return static_cast<long long>(r) * d.ld;
+    }
+    const int p = r / d.step;
+    const int left = d.rows - p * d.step;
+    const int w = left < d.step ? left : d.step;
+    mul = w;
+    return pack_panel_base(d, p, w) + 16ll * (r - p * d.step);
+}
+
+// Host-side description of a packed operand: `rows` rows of `kbytes` bytes, panel height `step`,
+// leading dimension `ld_bytes`, k_idx `shift_bytes`.
+inline PackDesc make_pack(size_t step, size_t rows, size_t ld_bytes, size_t kbytes,
+                          size_t shift_bytes)
+{
+    TQT_REQUIRE(rows < (1u << 31), "dimension exceeds 2^31-1");
+    PackDesc d;
+    d.ld = static_cast<long long>(ld_bytes);
+    d.kbytes = static_cast<long long>(kbytes);
+    d.shift = static_cast<long long>(shift_bytes);
+    d.step = static_cast<int>(step);
+    d.rows = static_cast<int>(rows);
+    return d;
+}
+
+// Byte order inside one row of a packed W4A16 weight: each whole 64-byte group (four 32-k blocks
+// of 16 bytes) is a 4 x 4 transpose of dwords, so 16-byte chunk c of the group holds dword c of
+// blocks 0..3 - the 8-k slice lane group c feeds to the four MFMAs of the group. Bytes of a
+// trailing partial group keep their place. Returns the stored position of logical byte kb.
+__host__ __device__ inline long long w4a16_frag_pos(long long kb, long long kbytes)
+{
+    const long long g = kb >> 6;
+    if (64 * (g + 1) > kbytes) {
+        return kb;
+    }
+    const long long blk = (kb >> 4) & 3;  // 32-k block within the group
+    const long long dw = (kb >> 2) & 3;   // 8-k dword within the block
+    return 64 * g + 16 * dw + 4 * blk + (kb & 3);
+}
+
 // One output of the requantization epilogue (reference tqt_kernel_gemm_i8_i8_4x1vl_rvv.h:
 // requantize_1xn :334-408 = vmulh, vsra by shift & 31, vadd zp, vnclip to i16 then i8;
 // clamp_i8 :231-259 = vmax then vmin).

@@ -25,6 +25,13 @@ KERNELS = {
     "w4a8": "gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt",
     "w4a16": "gemm_1xnbias_clamp_f16_f16_qsi4c2t",
     "igemmcl": "igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt",
+    # packed (p) siblings
+    "clampp": "gemm_clamp_i32_i8p_i8p",
+    "w8a8pb": "gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp",
+    "w8a8p": "gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp",
+    "w4a8p": "gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp",
+    "w4a16p": "gemm_1xnbias_clamp_f16_f16p_qsi4c2p",
+    "igemmclp": "igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp",
 }
 
 
@@ -86,8 +93,10 @@ def conv_params(input_shape, kernel_shape, stride, dilation, pad, ic, oc, groups
 
 def _sym(kind, action):
     name = KERNELS[kind]
+    if action.endswith("_async"):
+        return _sym(kind, action[:-len("_async")]) + "_async"
     if action == "run":
-        verb = "run_igemm" if kind == "igemmcl" else "run"
+        verb = "run_igemm" if name.startswith("igemmcl") else "run"
         return "tqt_%s_%s_%s" % (verb, name, VARIANT)
     return "tqt_%s_%s_%s" % (action, name, VARIANT)
 
@@ -166,6 +175,57 @@ _SIGS = {
 }
 
 
+_PACK = [c_size] * 5 + [c_vp, c_vp]  # (rows, k, ld, ld_packed, k_idx, src, dst)
+_OFFP = [c_size] * 4                  # (idx, k_idx, ld, actual)
+
+
+def _packed_sigs(base, packers, run_args, offsets):
+    sig = {
+        "get_m_step": (c_size, []),
+        "get_n_step": (c_size, []),
+        "get_c_offset": (c_size, [c_size] * 3),
+        "get_d_offset": (c_size, [c_size] * 3),
+        "get_d_size": (c_size, [c_size] * 2),
+    }
+    for what in offsets:
+        sig[what] = (c_size, _OFFP if "packed_offset" in what else
+                     ([c_size] * 3 if what == "get_a_offset" else [c_size] * 2))
+    if base != "clamp":
+        sig["get_bias_offset"] = (c_size, [c_size])
+    for pk in packers:
+        sig[pk] = (None, _PACK)
+        sig[pk + "_async"] = (None, _PACK + [c_vp])
+    if run_args is not None:
+        sig["run"] = (None, run_args)
+        sig["run_async"] = (None, run_args + [c_vp])
+    return sig
+
+
+_I8_REQ = [c_vp, ctypes.c_int8, ctypes.c_int8, ctypes.POINTER(QAI8QSI8CXParams)]
+_SIGS["clampp"] = _packed_sigs(
+    "clamp", ["run_a_pack", "run_b_pack", "run_bt_pack"],
+    _GEMM_I8_ARGS + [ctypes.c_int32, ctypes.c_int32],
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SIGS["w8a8pb"] = _packed_sigs(
+    "w8a8", ["run_b_pack", "run_bt_pack"], _GEMM_I8_ARGS + _I8_REQ,
+    ["get_a_offset", "get_b_packed_offset", "get_b_packed_size"])
+_SIGS["w8a8p"] = _packed_sigs(
+    "w8a8", ["run_a_pack", "run_b_pack", "run_bt_pack"], _GEMM_I8_ARGS + _I8_REQ,
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SIGS["w4a8p"] = _packed_sigs(
+    "w4a8", ["run_a_pack", "run_bt_pack"],
+    _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float, ctypes.POINTER(QAI8DXQSI4CXParams)],
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+# float16 clamps: the run is reached through the test shim (tqts_run_w4a16p)
+_SIGS["w4a16p"] = _packed_sigs(
+    "w4a16", ["run_a_pack", "run_bt_pack"], None,
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SIGS["w4a16p"]["get_scale_b_offset"] = (c_size, [c_size] * 3)
+_SIGS["igemmclp"] = _packed_sigs(
+    "igemmcl", ["run_bt_pack"], _SIGS["igemmcl"]["run"][1],
+    ["get_b_packed_offset", "get_b_packed_size"])
+
+
 class Lib:
     """Typed access to every exported function: ``lib.fn(kind, action)``."""
 
@@ -178,11 +238,7 @@ class Lib:
         self._fns = {}
         for kind, actions in _SIGS.items():
             for action, (res, args) in actions.items():
-                if action == "run_async":
-                    name = _sym(kind, "run") + "_async"
-                else:
-                    name = _sym(kind, action)
-                f = getattr(self.dll, name)
+                f = getattr(self.dll, _sym(kind, action))
                 f.restype = res
                 f.argtypes = args
                 self._fns[(kind, action)] = f
@@ -193,9 +249,10 @@ class Lib:
         return self._fns[(kind, action)]
 
     def symbol_names(self):
-        names = [_sym(k, a) if a != "run_async" else _sym(k, "run") + "_async"
-                 for (k, a) in self._fns]
-        names += [_sym("w4a16", "run"), _sym("w4a16", "run") + "_async", "tqt_gfx950_target"]
+        names = [_sym(k, a) for (k, a) in self._fns]
+        for kind in ("w4a16", "w4a16p"):
+            names += [_sym(kind, "run"), _sym(kind, "run_async")]
+        names.append("tqt_gfx950_target")
         return sorted(set(names))
 
 
