@@ -7,8 +7,9 @@ Headline (BASELINE.json metric "W4A8 GEMV HBM GB/s (M=1) + W8A8 GEMM int8 TOPS (
               M=512, K=4096, N=4096), with its MFMA roofline;
   * w4a8    = W4A8 decode GEMV HBM GB/s on configs[2] at M=1 (K=4096, N=11008), with its HBM
               roofline; M=4 and M=8 are reported beside it.
-The remaining configurations (int8->int32 GEMM, W4A16, int8 implicit-GEMM conv) are timed the
-same way and reported under "configs".
+The remaining configurations (int8->int32 GEMM, W4A16, int8 implicit-GEMM conv), and the packed
+siblings of W8A8, W4A8 and W4A16 on the same shapes (operands packed by the library's packers
+before timing), are timed the same way and reported under "configs".
 
 A step is one launch of the kernel over one batch of synthetic inputs already resident in
 HBM. Each launch reads a different copy of the weights (and activations): the copies together
@@ -145,13 +146,25 @@ def inputs_w4a8(rng, m, n, k):
 # Per-config measurements
 # ------------------------------------------------------------------------------------------
 
-def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng):
+def pack_dev(torch, lib, kind, action, rows, k, src, nbytes):
+    """One packed copy of `src` (device tensor) by the library's packer (synchronous)."""
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    lib.fn(kind, action)(rows, k, k, k, 0, src.data_ptr(), dst.data_ptr())
+    return dst
+
+
+def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng, packed=False):
+    """packed: the qai8_qai8p_qsi8cxp sibling on the same inputs, A and B packed once by the
+    library's packers before timing."""
     m, n, k = W8A8["m"], W8A8["n"], W8A8["k"]
     A, B, sb, bias, zp_a = inputs_w8a8(rng, m, n, k)
     per_copy = A.nbytes + B.nbytes
     nc = copies_for(per_copy)
     dA = [torch.from_numpy(A).cuda()]
     dB = [torch.from_numpy(B).cuda()]
+    if packed:
+        dA = [pack_dev(torch, lib, "w8a8p", "run_a_pack", m, k, dA[0], A.nbytes)]
+        dB = [pack_dev(torch, lib, "w8a8p", "run_bt_pack", n, k, dB[0], B.nbytes)]
     for _ in range(nc - 1):
         dA.append(dA[0].clone())
         dB.append(dB[0].clone())
@@ -159,7 +172,7 @@ def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng):
     dbias = torch.from_numpy(bias).cuda()
     dD = torch.empty((m, n), dtype=torch.int8, device="cuda")
     p = mod.QAI8QSI8CXParams(0.02, zp_a, dsb.data_ptr(), n, 0.05, 0)
-    f = lib.fn("w8a8", "run_async")
+    f = lib.fn("w8a8p" if packed else "w8a8", "run_async")
     s = timer.stream.cuda_stream
 
     def launch(i):
@@ -175,19 +188,24 @@ def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng):
                 bytes=algo_bytes, copies=nc, inputs=(A, B, sb, bias, zp_a))
 
 
-def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m):
+def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m, packed=False):
+    """packed: the qai8dxp_qsi4cxp sibling on the same inputs (packed once before timing)."""
     n, k = W4A8["n"], W4A8["k"]
     A, Bp, sa, za, sb, bias = inputs_w4a8(rng, m, n, k)
     nc = copies_for(Bp.nbytes)
     dB = [torch.from_numpy(Bp).cuda()]
+    dA0 = torch.from_numpy(A).cuda()
+    if packed:
+        dB = [pack_dev(torch, lib, "w4a8p", "run_bt_pack", n, k, dB[0], Bp.nbytes)]
+        dA0 = pack_dev(torch, lib, "w4a8p", "run_a_pack", m, k, dA0, A.nbytes)
     for _ in range(nc - 1):
         dB.append(dB[0].clone())
-    dA = [torch.from_numpy(A).cuda() for _ in range(nc)]
+    dA = [dA0.clone() for _ in range(nc)]
     dsa, dza, dsb = (torch.from_numpy(x).cuda() for x in (sa, za, sb))
     dbias = torch.from_numpy(bias).cuda()
     dD = torch.empty((m, n), dtype=torch.float32, device="cuda")
     p = mod.QAI8DXQSI4CXParams(dsa.data_ptr(), dza.data_ptr(), dsb.data_ptr())
-    f = lib.fn("w4a8", "run_async")
+    f = lib.fn("w4a8p" if packed else "w4a8", "run_async")
     s = timer.stream.cuda_stream
 
     def launch(i):
@@ -202,7 +220,8 @@ def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m):
                 ops=2.0 * m * n * k, copies=nc, inputs=(A, Bp, sa, za, sb, bias))
 
 
-def bench_w4a16(torch, mod, lib, timer, warmup, steps, rng):
+def bench_w4a16(torch, mod, lib, timer, warmup, steps, rng, packed=False):
+    """packed: the f16p_qsi4c2p sibling on the same inputs (packed once before timing)."""
     m, n, k, bl = W4A16["m"], W4A16["n"], W4A16["k"], W4A16["bl"]
     A = rng.standard_normal((m, k)).astype(np.float16)
     Bp = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
@@ -211,10 +230,13 @@ def bench_w4a16(torch, mod, lib, timer, warmup, steps, rng):
     nc = copies_for(Bp.nbytes + S.nbytes)
     dB = [torch.from_numpy(Bp).cuda()]
     dS = [torch.from_numpy(S).cuda()]
+    dA = torch.from_numpy(A).cuda()
+    if packed:
+        dB = [pack_dev(torch, lib, "w4a16p", "run_bt_pack", n, k, dB[0], Bp.nbytes)]
+        dA = pack_dev(torch, lib, "w4a16p", "run_a_pack", m, k, dA, A.nbytes)
     for _ in range(nc - 1):
         dB.append(dB[0].clone())
         dS.append(dS[0].clone())
-    dA = torch.from_numpy(A).cuda()
     dbias = torch.from_numpy(bias).cuda()
     dD = torch.empty((m, n), dtype=torch.float16, device="cuda")
     shim = ctypes.CDLL(os.path.join(ROOT, "tests", "abi_shim", "libtqt_test_shim.so"))
@@ -228,10 +250,22 @@ def bench_w4a16(torch, mod, lib, timer, warmup, steps, rng):
     cmin = int(np.float16(-65504.0).view(np.uint16))
     cmax = int(np.float16(65504.0).view(np.uint16))
     s = timer.stream.cuda_stream
+    if packed:
+        fp = shim.tqts_run_w4a16p
+        fp.restype = None
+        fp.argtypes = ([ctypes.c_size_t] * 4 +
+                       [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p,
+                        ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
+                        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
+                        ctypes.c_void_p, ctypes.c_uint16, ctypes.c_uint16, ctypes.c_void_p])
 
     def launch(i):
-        f(m, n, k, bl, dA.data_ptr(), k, dB[i].data_ptr(), k, dS[i].data_ptr(), k // bl, None, n,
-          dD.data_ptr(), n, dbias.data_ptr(), cmin, cmax, s)
+        if packed:
+            fp(m, n, k, bl, dA.data_ptr(), k, 0, dB[i].data_ptr(), k, 0, dS[i].data_ptr(),
+               k // bl, None, n, dD.data_ptr(), n, dbias.data_ptr(), cmin, cmax, s)
+        else:
+            f(m, n, k, bl, dA.data_ptr(), k, dB[i].data_ptr(), k, dS[i].data_ptr(), k // bl, None,
+              n, dD.data_ptr(), n, dbias.data_ptr(), cmin, cmax, s)
 
     ms = timer.run(launch, nc, warmup, steps)
     algo_bytes = Bp.nbytes + S.nbytes + A.nbytes + bias.nbytes + 2 * m * n
@@ -427,7 +461,8 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,conv,clamp,copy): "
+                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,w4a16p,conv,"
+                         "clamp,copy): "
                          "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -453,6 +488,9 @@ def main():
             "w4a8m4": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 4),
             "w4a8m8": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 8),
             "w4a16": lambda: bench_w4a16(torch, mod, lib, timer, W, K, rng),
+            "w8a8p": lambda: bench_w8a8(torch, mod, lib, timer, W, K, rng, packed=True),
+            "w4a8p": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True),
+            "w4a16p": lambda: bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True),
             "conv": lambda: bench_conv(torch, mod, lib, timer, W, K, rng),
             "clamp": lambda: bench_clamp(torch, mod, lib, timer, W, K, rng),
             "copy": lambda: bench_copy(torch, timer, W, K),
@@ -470,6 +508,9 @@ def main():
         w416 = bench_w4a16(torch, mod, lib, timer, W, K, rng)
         cv = bench_conv(torch, mod, lib, timer, W, K, rng)
         cl = bench_clamp(torch, mod, lib, timer, W, K, rng)
+        w8p = bench_w8a8(torch, mod, lib, timer, W, K, rng, packed=True)
+        w4p = bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True)
+        w416p = bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True)
 
     w41 = w4[1]
     traffic = None if args.no_traffic else hbm_traffic()
@@ -521,6 +562,16 @@ def main():
             "igemmcl 8x56x56x128 3x3 OC128": {"us": round(cv["ms"] * 1e3, 3),
                                               "TOPS": round(cv["tops"], 3),
                                               "mfma_frac": round(cv["tops"] / INT8_PEAK_TOPS, 4)},
+            # packed siblings on the same configurations (operands packed before timing)
+            "packed qai8_qai8p_qsi8cxp 512x4096x4096": {
+                "us": round(w8p["ms"] * 1e3, 3), "TOPS": round(w8p["tops"], 3),
+                "mfma_frac": round(w8p["tops"] / INT8_PEAK_TOPS, 4)},
+            "packed qai8dxp_qsi4cxp M=1 K=4096 N=11008": {
+                "us": round(w4p["ms"] * 1e3, 3), "GB/s": round(w4p["gbs"], 2),
+                "hbm_frac": round(w4p["gbs"] / HBM_PEAK_GBS, 4)},
+            "packed f16p_qsi4c2p 32x14336x4096 bl32": {
+                "us": round(w416p["ms"] * 1e3, 3), "GB/s": round(w416p["gbs"], 2),
+                "hbm_frac": round(w416p["gbs"] / HBM_PEAK_GBS, 4)},
         },
     }
     if traffic:

@@ -13,12 +13,13 @@
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,
  * moved back by k_idx*(step - w) elements when a panel after the first is narrower (the
  * reference's tail rule, tqt_gemm_pack_rvv.h:314-318). Inside a panel each row is cut into
- * 16-byte chunks (one MFMA lane fragment: 16 consecutive k bytes of one row) stored
- * chunk-major: chunk c of local row r at byte 16*c*w + r*cw, cw = min(16, row bytes - 16*c).
+ * 16-byte chunks stored chunk-major: chunk c of local row r at byte 16*c*w + r*cw,
+ * cw = min(16, row bytes - 16*c). A chunk is one MFMA lane fragment (8 f16 values or
+ * 32 int4 values); 16 channels x 16 bytes make one lane group's contiguous load.
  * The packed_offset getters keep the reference's formula (idx*ld + k_idx*min(actual, step))
  * elements; it addresses element (idx, k_idx) of a full-K packing when k_idx is a whole number
- * of 16-byte chunks, and the start of a k_idx sub-buffer packed with that k_idx in any case.
- * Packed sizes equal the unpacked ones.
+ * of chunks, and the start of a k_idx sub-buffer packed with that k_idx in any case. Packed
+ * sizes equal the unpacked ones.
  *
  * Drop-in for src/gemm/gemm_f16_i4/gemm_1xnbias_clamp_f16_f16p_qsi4c2p/tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_8x2vl_rvv.h
  * (the line of each declaration is given below). Every pointer, source and packed

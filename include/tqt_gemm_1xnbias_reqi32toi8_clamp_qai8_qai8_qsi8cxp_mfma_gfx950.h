@@ -12,12 +12,14 @@
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,
  * moved back by k_idx*(step - w) elements when a panel after the first is narrower (the
  * reference's tail rule, tqt_gemm_pack_rvv.h:314-318). Inside a panel each row is cut into
- * 16-byte chunks (one MFMA lane fragment: 16 consecutive k bytes of one row) stored
- * chunk-major: chunk c of local row r at byte 16*c*w + r*cw, cw = min(16, row bytes - 16*c).
+ * 16-byte chunks stored chunk-major: chunk c of local row r at byte 16*c*w + r*cw,
+ * cw = min(16, row bytes - 16*c). A chunk is one MFMA lane fragment (16 k bytes, or
+ * 32 int4 values); the kernels load one chunk of 8 or more consecutive rows per group of
+ * consecutive lanes, whole cache lines.
  * The packed_offset getters keep the reference's formula (idx*ld + k_idx*min(actual, step))
  * elements; it addresses element (idx, k_idx) of a full-K packing when k_idx is a whole number
- * of 16-byte chunks, and the start of a k_idx sub-buffer packed with that k_idx in any case.
- * Packed sizes equal the unpacked ones.
+ * of chunks, and the start of a k_idx sub-buffer packed with that k_idx in any case. Packed
+ * sizes equal the unpacked ones.
  *
  * Drop-in for src/gemm/gemm_i8_i8/gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp/tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_4x1vl_rvv.h
  * (the line of each declaration is given below). Every pointer, source and packed

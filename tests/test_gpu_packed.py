@@ -112,7 +112,7 @@ def test_packer_writes_restated_layout(gpu, kind, action, src, which, rows, k):
     kb = kbytes_of(src, k)
     dst = dbuf(rows * kb)
     pack(kind, action, rows, k, ld, k, 0, dsrc, dst)
-    exp = T.pack_panels(X, step, frag=src == "i4f")
+    exp = T.pack_panels(X, step, kc=T.PACK_CHUNK[kind], frag=src == "i4f")
     np.testing.assert_array_equal(host(dst), exp)
 
 
@@ -130,7 +130,7 @@ def test_packer_ld_packed_and_k_idx_sub_buffers(gpu, kind, action, src, which):
     full = dbuf(nbytes)
     pack(kind, action, rows, k, ld, ldp, 0, dsrc, full)
     exp = np.full(nbytes, SENTINEL, np.uint8)
-    T.pack_panels(X, step, ld_packed=kbp, frag=src == "i4f", out=exp)
+    T.pack_panels(X, step, kc=T.PACK_CHUNK[kind], ld_packed=kbp, frag=src == "i4f", out=exp)
     np.testing.assert_array_equal(host(full), exp)
 
     # halves: the second starts at the offset of element (0, k/2); its source pointer moves

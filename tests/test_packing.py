@@ -74,11 +74,22 @@ def test_layout_restatement_hand_worked():
     assert list(out[6 + 40 - 3:6 + 40 - 3 + 4]) == [40, 41, 42, 43]
 
 
-@pytest.mark.parametrize("rows,kb,step", [(1, 16, 16), (37, 100, 16), (130, 64, 128),
-                                          (5, 7, 4), (256, 2048, 128), (33, 8192, 32)])
-def test_layout_is_a_permutation(rows, kb, step):
+def test_layout_restatement_hand_worked_wide_chunks():
+    # 2 rows of 200 bytes in one panel, 128-byte chunks: row 0 bytes 0-127, row 1 bytes
+    # 0-127, then the 72-byte tails of rows 0 and 1
+    X = np.arange(400).reshape(2, 200)
+    exp = (list(range(0, 128)) + list(range(200, 328)) + list(range(128, 200)) +
+           list(range(328, 400)))
+    np.testing.assert_array_equal(T.pack_panels(X, 16, kc=128), exp)
+
+
+@pytest.mark.parametrize("rows,kb,step,kc", [(1, 16, 16, 16), (37, 100, 16, 16),
+                                             (130, 64, 128, 16), (5, 7, 4, 16),
+                                             (256, 2048, 128, 128), (33, 8192, 32, 16),
+                                             (300, 1000, 128, 128), (45, 2048, 16, 128)])
+def test_layout_is_a_permutation(rows, kb, step, kc):
     idx = np.arange(rows * kb).reshape(rows, kb)
-    out = T.pack_panels(idx, step)
+    out = T.pack_panels(idx, step, kc=kc)
     np.testing.assert_array_equal(np.sort(out), np.arange(rows * kb))
     # inverse: each element found where the chunk rule puts it
     rng = np.random.default_rng(rows + kb)
@@ -86,9 +97,9 @@ def test_layout_is_a_permutation(rows, kb, step):
         r, c = int(rng.integers(rows)), int(rng.integers(kb))
         p, rl = divmod(r, step)
         w = min(step, rows - p * step)
-        ch = c // 16
-        cw = min(16, kb - 16 * ch)
-        assert out[p * step * kb + 16 * ch * w + rl * cw + c % 16] == r * kb + c
+        ch = c // kc
+        cw = min(kc, kb - kc * ch)
+        assert out[p * step * kb + kc * ch * w + rl * cw + c % kc] == r * kb + c
 
 
 def test_fragment_order_is_an_involution_on_whole_groups():
@@ -147,8 +158,9 @@ def test_packed_offsets_address_the_restated_layout(lib, mod, kind, getter, esiz
     f = _getter(lib, sym(mod, kind, getter), 4)
     kbytes = k // 2 if esize == 0 else k * esize
     idx = np.arange(rows * kbytes).reshape(rows, kbytes)
-    out = T.pack_panels(idx, step, frag=frag)
-    kstep = 128 if frag else (32 if esize == 0 else 16 // esize)
+    kc = T.PACK_CHUNK[kind]
+    out = T.pack_panels(idx, step, kc=kc, frag=frag)
+    kstep = 128 if frag else (2 * kc if esize == 0 else kc // esize)
     for r0 in range(0, rows, step):
         for k_idx in range(0, k, kstep):
             off = f(r0, k_idx, k, rows - r0)

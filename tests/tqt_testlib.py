@@ -329,11 +329,16 @@ def gen_igemmcl(ID, IH, IW, IC, OC, KH, KW, stride=(1, 1), pad=(0, 0), dil=(1, 1
 # ------------------------------------------------------------------------------------------
 # Packed layout of the p-variants, restated independently of the device code (the library's
 # packers must produce exactly these bytes): panels of `step` rows, panel p at
-# p * step * ld_packed (minus shift * (step - w) for a narrower panel after the first),
-# 16-byte chunks stored chunk-major inside a panel, the last chunk of a row cw < 16 bytes wide.
-# W4A16 weights are first permuted inside each whole 64-byte group of a row (4 x 4 transpose
-# of 4-byte words).
+# p * step * ld_packed (minus shift * (step - w) for a narrower panel after the first), chunks
+# of `kc` bytes stored chunk-major inside a panel, the last chunk of a row narrower when the
+# row length is not a multiple of kc. W4A16 weights are first permuted inside each whole
+# 64-byte group of a row (4 x 4 transpose of 4-byte words).
 # ------------------------------------------------------------------------------------------
+
+# chunk bytes per packed kernel type (one MFMA lane fragment for every type)
+PACK_CHUNK = {"clampp": 16, "w8a8pb": 16, "w8a8p": 16, "igemmclp": 16, "w4a8p": 16,
+              "w4a16p": 16}
+
 
 def frag_perm(kbytes):
     """perm[P] = logical byte stored at position P of a fragment-ordered W4A16 weight row."""
@@ -344,7 +349,7 @@ def frag_perm(kbytes):
     return np.where(full, swapped, P)
 
 
-def pack_panels(X, step, ld_packed=None, shift=0, frag=False, out=None, base=0):
+def pack_panels(X, step, kc=16, ld_packed=None, shift=0, frag=False, out=None, base=0):
     """X: [rows, kbytes] (any dtype of 1 byte, or an index array) -> flat packed buffer.
     ld_packed, shift: bytes. Writes into `out` at offset `base` when given."""
     X = np.asarray(X)
@@ -355,7 +360,7 @@ def pack_panels(X, step, ld_packed=None, shift=0, frag=False, out=None, base=0):
         X = X[:, frag_perm(kb)]
     if out is None:
         out = np.zeros(rows * ld_packed if rows else 0, X.dtype)
-    kb16 = kb // 16 * 16
+    kfull = kb // kc * kc
     for p in range((rows + step - 1) // step):
         r0 = p * step
         w = min(step, rows - r0)
@@ -363,8 +368,8 @@ def pack_panels(X, step, ld_packed=None, shift=0, frag=False, out=None, base=0):
         if p > 0 and w < step:
             pb -= shift * (step - w)
         blk = X[r0:r0 + w]
-        full = blk[:, :kb16].reshape(w, kb16 // 16, 16).transpose(1, 0, 2).ravel()
+        full = blk[:, :kfull].reshape(w, kfull // kc, kc).transpose(1, 0, 2).ravel()
         out[pb:pb + full.size] = full
-        tail = blk[:, kb16:].ravel()
+        tail = blk[:, kfull:].ravel()
         out[pb + full.size:pb + full.size + tail.size] = tail
     return out

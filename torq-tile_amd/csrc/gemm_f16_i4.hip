@@ -529,13 +529,13 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
     if (packed) {
         TQT_REQUIRE(lda >= k && ldb >= k && ldb % 2 == 0 && k_idx_b % 2 == 0,
                     "packed W4A16 needs lda, ldb >= k and even ldb, k_idx_b");
-        a.pa = make_pack(kPackW4A16MStep, m, 2 * lda, 2 * k, 2 * k_idx_a);
-        a.pb = make_pack(kPackW4A16NStep, n, ldb / 2, k / 2, k_idx_b / 2);
+        a.pa = make_pack(kPackW4A16MStep, kPackW4A16Chunk, m, 2 * lda, 2 * k, 2 * k_idx_a);
+        a.pb = make_pack(kPackW4A16NStep, kPackW4A16Chunk, n, ldb / 2, k / 2, k_idx_b / 2);
         // every 16-byte chunk of a packed row starts 16-byte aligned
         layout_fast = ((2 * k_idx_a) % 16 == 0) && ((k_idx_b / 2) % 16 == 0);
     } else {
-        a.pa = make_pack(0, m, 2 * lda, 2 * k, 0);
-        a.pb = make_pack(0, n, ldb / 2, k / 2, 0);
+        a.pa = make_pack(0, kPackW4A16Chunk, m, 2 * lda, 2 * k, 0);
+        a.pb = make_pack(0, kPackW4A16Chunk, n, ldb / 2, k / 2, 0);
         layout_fast = lda % 8 == 0 && (ldb / 2) % 16 == 0;
     }
     const bool fast = bl == 32 && k % 128 == 0 && k <= 128u * kWaves * kMaxGroupsPerWave &&

@@ -117,8 +117,11 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
     const int wave = tid >> 6;
     const int fr = lane & 15;  // A-operand row (activation) / B-operand column (channel)
     const int fg = lane >> 4;  // 16-k slot group of the MFMA step
-    const int r8 = lane >> 3;  // row within an 8-row load
-    const int c8 = lane & 7;   // 16-byte chunk within a 128-byte row segment
+    // weight load roles: row within an 8-row load and 16-byte chunk within a 128-byte row
+    // segment; 8 consecutive lanes read one row's 128 bytes, or for packed weights (16-byte chunks
+    // stored chunk-major in the panel) one chunk of 8 consecutive rows
+    const int r8 = (PK & PK_B) ? (lane & 7) : (lane >> 3);
+    const int c8 = (PK & PK_B) ? (lane >> 3) : (lane & 7);
     const int n0 = blockIdx.x * kNTile;
     const int m0 = blockIdx.y * kRowsPerChunk;
     const int rows = min(kRowsPerChunk, a.M - m0);
@@ -164,7 +167,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         if (lane < a_chunks) {
             const int r = lane / (npw * 16);
             const int off = (lane - r * npw * 16) * 16;
-            int mul = 1;  // byte kb of a packed row is at kb * (panel width) from its chunk 0
+            int mul = 1;  // k multiplier of a packed row (its panel width)
             long long base;
             if constexpr ((PK & PK_A) != 0) {
                 base = pack_row(a.pa, m0 + r, mul);
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 base = static_cast<long long>(m0 + r) * a.lda;
             }
             a_chunk = *reinterpret_cast<const i32x4 *>(
-                a.A + base + static_cast<long long>(p_begin * kPairK + off) * mul);
+                a.A + base + pack_k<kPackW4A8Chunk, (PK & PK_A) != 0>(p_begin * kPairK + off, mul));
         }
     }
     // register path: this lane's activation row (row rows - 1 for the ones/zero lanes) and the
@@ -210,10 +213,11 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
             for (int s = 0; s < 2 * kPairsPerBatch; ++s) {
                 // unconditional loads from a valid row (row rows - 1 for the ones/zero lanes)
                 const int pair = min(pb + (s >> 1), p_end - 1);
-                const int8_t *p =
-                    a_rowp + static_cast<long long>(pair * kPairK + (s & 1) * 128 + fg * 32) * a_mul;
-                const i32x4 v0 = *reinterpret_cast<const i32x4 *>(p);
-                const i32x4 v1 = *reinterpret_cast<const i32x4 *>(p + 16 * a_mul);
+                const int kb = pair * kPairK + (s & 1) * 128 + fg * 32;
+                const i32x4 v0 = *reinterpret_cast<const i32x4 *>(
+                    a_rowp + pack_k<kPackW4A8Chunk, (PK & PK_A) != 0>(kb, a_mul));
+                const i32x4 v1 = *reinterpret_cast<const i32x4 *>(
+                    a_rowp + pack_k<kPackW4A8Chunk, (PK & PK_A) != 0>(kb + 16, a_mul));
                 const i32x4 fill = a_ones ? ones : zero;
                 av[s][0] = a_real ? v0 : fill;
                 av[s][1] = a_real ? v1 : fill;
@@ -227,7 +231,8 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         for (int j = 0; j < 2 * kPairsPerBatch; ++j) {
             const int pair = min(pb + (j >> 1), p_end - 1);
             wr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
-                w_rowp[j & 1] + static_cast<long long>(pair * (kPairK / 2) + c8 * 16) * w_mul[j & 1]));
+                w_rowp[j & 1] +
+                pack_k<kPackW4A8Chunk, (PK & PK_B) != 0>(pair * (kPairK / 2) + c8 * 16, w_mul[j & 1])));
         }
         // keep every load of the batch ahead of the compute (the scheduler would sink them to
         // their uses and serialize the stream); emits no instruction
@@ -373,13 +378,13 @@ void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_
     if (packed) {
         TQT_REQUIRE(lda >= k && ldb >= k && ldb % 2 == 0 && k_idx_b % 2 == 0,
                     "packed W4A8 needs lda, ldb >= k and even ldb, k_idx_b");
-        a.pa = make_pack(kPackW4A8MStep, m, lda, k, k_idx_a);
-        a.pb = make_pack(kPackW4A8NStep, n, ldb / 2, k / 2, k_idx_b / 2);
+        a.pa = make_pack(kPackW4A8MStep, kPackW4A8Chunk, m, lda, k, k_idx_a);
+        a.pb = make_pack(kPackW4A8NStep, kPackW4A8Chunk, n, ldb / 2, k / 2, k_idx_b / 2);
         // every 16-byte chunk of a packed row starts 16-byte aligned
         layout_fast = (k_idx_a % 16 == 0) && ((k_idx_b / 2) % 16 == 0);
     } else {
-        a.pa = make_pack(0, m, lda, k, 0);
-        a.pb = make_pack(0, n, ldb / 2, k / 2, 0);
+        a.pa = make_pack(0, kPackW4A8Chunk, m, lda, k, 0);
+        a.pb = make_pack(0, kPackW4A8Chunk, n, ldb / 2, k / 2, 0);
         layout_fast = (lda % 16 == 0) && ((ldb / 2) % 16 == 0);
     }
     const bool fast = (k % kPairK == 0) && k <= 65536 && layout_fast && aligned16(A) &&

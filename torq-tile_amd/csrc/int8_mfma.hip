@@ -133,7 +133,10 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
         }
     }
 
-    // Per-thread load assignment (fixed across the K loop).
+    // Per-thread load assignment (fixed across the K loop): 4 consecutive threads read one row's
+    // 64 bytes of a plain operand; for a packed one (16-byte chunks stored chunk-major in the
+    // panel) consecutive threads take consecutive rows of one chunk, so a wave reads 64 rows x
+    // 16 contiguous bytes.
     int a_row[A_CHUNKS], a_chk[A_CHUNKS], a_mul[A_CHUNKS];
     bool a_ok[A_CHUNKS];
     int a_od[A_CHUNKS], a_oh[A_CHUNKS], a_ow[A_CHUNKS];
@@ -141,11 +144,11 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 #pragma unroll
     for (int j = 0; j < A_CHUNKS; ++j) {
         const int c = tid + j * kThreads;
-        a_row[j] = c >> 2;
-        a_chk[j] = c & 3;
+        a_row[j] = (PK & PK_A) ? c % BM : c >> 2;
+        a_chk[j] = (PK & PK_A) ? c / BM : c & 3;
         const int gm = m0 + a_row[j];
         a_ok[j] = gm < a.M;
-        a_mul[j] = 1;  // byte kb of a packed row is at kb * (panel width) from its chunk 0
+        a_mul[j] = 1;  // k multiplier of a packed row (its panel width)
         if constexpr (AM == A_MATRIX) {
             const int r = a_ok[j] ? gm : 0;
             long long base;
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             } else {
                 base = static_cast<long long>(r) * a.lda;
             }
-            a_ptr[j] = a.A + base + a_chk[j] * 16 * a_mul[j];
+            a_ptr[j] = a.A + base + pack_k<kPackI8Chunk, (PK & PK_A) != 0>(a_chk[j] * 16, a_mul[j]);
             a_od[j] = a_oh[j] = a_ow[j] = 0;
         } else {
             // a_od/a_oh/a_ow hold the first input coordinate of the output pixel's window
@@ -175,8 +178,8 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     for (int j = 0; j < B_CHUNKS; ++j) {
         const int c = tid + j * kThreads;
         if constexpr (BMd == B_NK) {
-            b_row[j] = c >> 2;  // n within the tile
-            b_chk[j] = c & 3;   // 16-byte k chunk
+            b_row[j] = (PK & PK_B) ? c % kBN : c >> 2;  // n within the tile
+            b_chk[j] = (PK & PK_B) ? c / kBN : c & 3;   // 16-byte k chunk
             const int gn = n0 + b_row[j];
             b_ok[j] = gn < a.N;
             const int r = b_ok[j] ? gn : 0;
@@ -187,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             } else {
                 base = static_cast<long long>(r) * a.ldb;
             }
-            b_ptr[j] = a.B + base + b_chk[j] * 16 * b_mul[j];
+            b_ptr[j] = a.B + base + pack_k<kPackI8Chunk, (PK & PK_B) != 0>(b_chk[j] * 16, b_mul[j]);
         } else {
             // one wave covers 64 consecutive k of one 16-column chunk, so each byte store of
             // the transpose below writes 64 consecutive bytes of one LDS row (no bank conflicts
@@ -202,8 +205,8 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     }
 
     // One k-step of operands in registers: raw 16-byte loads plus a validity bit per chunk.
-    // Every load reads valid memory (an out-of-range chunk reads its row start or the image
-    // base instead) and the mask is applied when the step is stored to LDS, so no load sits in
+    // Every load reads valid memory (an out-of-range chunk reads the operand's first 16 bytes
+    // instead) and the mask is applied when the step is stored to LDS, so no load sits in
     // a branch (the compiler would wait for it at the join, serializing the stream).
     struct Step
     {
@@ -220,8 +223,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             bool ok = a_ok[j] && k < a.K;
             const int8_t *src;
             if constexpr (AM == A_MATRIX) {
-                src = ok ? a_ptr[j] + static_cast<long long>(k0) * a_mul[j]
-                         : a_ptr[j] - a_chk[j] * 16 * a_mul[j];
+                src = ok ? a_ptr[j] + pack_k<kPackI8Chunk, (PK & PK_A) != 0>(k0, a_mul[j]) : a.A;
             } else {
                 const ConvGeom &g = a.cv;
                 const int2 t = s_tap[ok ? k >> 4 : 0];
@@ -240,8 +242,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                 const int k = k0 + b_chk[j] * 16;
                 const bool ok = b_ok[j] && k < a.K;
                 st.b[j] = *reinterpret_cast<const i32x4 *>(
-                    ok ? b_ptr[j] + static_cast<long long>(k0) * b_mul[j]
-                       : b_ptr[j] - b_chk[j] * 16 * b_mul[j]);
+                    ok ? b_ptr[j] + pack_k<kPackI8Chunk, (PK & PK_B) != 0>(k0, b_mul[j]) : a.B);
                 st.bm |= ok ? (1u << j) : 0u;
             } else {
                 const int k = k0 + b_row[j];
@@ -464,19 +465,24 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         }
     }
 
-    // Load-side lane roles: lane = 8 * row-in-block + LDS slot; the slot holds k-chunk
-    // slot ^ ((row >> 1) & 7) of that row.
-    const int lrow = lane >> 3;
-    const int lslot = lane & 7;
+    // Load-side lane roles. Plain rows: lane = 8 * row-in-block + LDS slot, the slot holding
+    // k-chunk slot ^ ((row >> 1) & 7) of that row, so 8 consecutive lanes read one row's 128
+    // bytes. Packed rows (16-byte chunks stored chunk-major in the panel): lane = 8 * slot +
+    // row-in-block, so 8 consecutive lanes read one chunk of 8 consecutive rows (128 contiguous
+    // bytes), and an 8-row block of LDS holds its chunks chunk-major, chunk c in slot
+    // c ^ (block & 1) (lds_pos below).
+    constexpr bool kAP = (PK & PK_A) != 0;
+    constexpr bool kBP = (PK & PK_B) != 0;
     const int8_t *a_row[A_DMA];
     int a_chunk[A_DMA], a_mul[A_DMA];
     int a_id0[A_DMA], a_ih0[A_DMA], a_iw0[A_DMA];
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) {
-        const int r = 8 * (wave * A_DMA + j) + lrow;
-        a_chunk[j] = lslot ^ ((r >> 1) & 7);
+        const int blk = wave * A_DMA + j;
+        const int r = 8 * blk + (kAP ? (lane & 7) : (lane >> 3));
+        a_chunk[j] = kAP ? ((lane >> 3) ^ (blk & 1)) : ((lane & 7) ^ ((r >> 1) & 7));
         const int gm = min(m0 + r, a.M - 1);
-        a_mul[j] = 1;  // byte kb of a packed row is at kb * (panel width) from its chunk 0
+        a_mul[j] = 1;  // k multiplier of a packed row (its panel width)
         if constexpr (AM == A_MATRIX) {
             long long base;
             if constexpr ((PK & PK_A) != 0) {
@@ -484,7 +490,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
             } else {
                 base = static_cast<long long>(gm) * a.lda;
             }
-            a_row[j] = a.A + base + a_chunk[j] * 16 * a_mul[j];
+            a_row[j] = a.A + base + pack_k<kPackI8Chunk, kAP>(a_chunk[j] * 16, a_mul[j]);
             a_id0[j] = a_ih0[j] = a_iw0[j] = 0;
         } else {
             const ConvGeom &g = a.cv;
@@ -503,7 +509,9 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     int b_mul[B_DMA];
 #pragma unroll
     for (int j = 0; j < B_DMA; ++j) {
-        const int r = 8 * (wave * B_DMA + j) + lrow;
+        const int blk = wave * B_DMA + j;
+        const int r = 8 * blk + (kBP ? (lane & 7) : (lane >> 3));
+        const int chunk = kBP ? ((lane >> 3) ^ (blk & 1)) : ((lane & 7) ^ ((r >> 1) & 7));
         const int gn = min(n0 + r, a.N - 1);
         long long base;
         b_mul[j] = 1;
@@ -512,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         } else {
             base = static_cast<long long>(gn) * a.ldb;
         }
-        b_row[j] = a.B + base + (lslot ^ ((r >> 1) & 7)) * 16 * b_mul[j];
+        b_row[j] = a.B + base + pack_k<kPackI8Chunk, kBP>(chunk * 16, b_mul[j]);
     }
 
     auto issue = [&](int st, int8_t *sa, int8_t *sb) {
@@ -521,7 +529,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         for (int j = 0; j < A_DMA; ++j) {
             const int8_t *src;
             if constexpr (AM == A_MATRIX) {
-                src = a_row[j] + static_cast<long long>(k0) * a_mul[j];
+                src = a_row[j] + pack_k<kPackI8Chunk, kAP>(k0, a_mul[j]);
             } else {
                 const ConvGeom &g = a.cv;
                 const int k = k0 + a_chunk[j] * 16;
@@ -546,7 +554,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
 #pragma unroll
         for (int j = 0; j < B_DMA; ++j) {
 #if defined(__HIP_DEVICE_COMPILE__)
-            __builtin_amdgcn_global_load_lds(b_row[j] + static_cast<long long>(k0) * b_mul[j],
+            __builtin_amdgcn_global_load_lds(b_row[j] + pack_k<kPackI8Chunk, kBP>(k0, b_mul[j]),
                                              sb + (wave * B_DMA + j) * 1024, 16, 0, 0);
 #endif
         }
@@ -564,9 +572,16 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         }
     }
 
-    // MFMA operand lanes: row r32 of a 32-row fragment, k-chunk 2 * step + h.
+    // MFMA operand lanes: row r32 of a 32-row fragment, k-chunk 2 * step + h. LDS position of
+    // (row, chunk) in a stage: plain rows keep 128 bytes per row, chunks XOR-swizzled; packed
+    // rows keep 8-row blocks of chunk-major 16-byte slots (the 16 rows one ds_read_b128 pass
+    // reads fall in two blocks whose slots sit 128 bytes apart modulo 256: no bank conflict).
     const int r32 = lane & 31;
     const int h = lane >> 5;
+    auto lds_pos = [](bool packed, int row, int c) {
+        return packed ? (row >> 3) * 1024 + ((((c ^ ((row >> 3) & 1)) << 3) + (row & 7)) << 4)
+                      : row * kSK + ((c ^ ((row >> 1) & 7)) << 4);
+    };
     constexpr int KS = kSK / 32;  // MFMA k-steps per stage
     auto compute = [&](const int8_t *sa, const int8_t *sb) {
         // All operand reads of the stage first, so their LDS latency overlaps.
@@ -577,14 +592,12 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
 #pragma unroll
             for (int i = 0; i < MF; ++i) {
                 const int row = wm * WM + 32 * i + r32;
-                fa[step][i] =
-                    *reinterpret_cast<const i32x4 *>(sa + row * kSK + ((c ^ ((row >> 1) & 7)) << 4));
+                fa[step][i] = *reinterpret_cast<const i32x4 *>(sa + lds_pos(kAP, row, c));
             }
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
                 const int row = wn * 64 + 32 * j + r32;
-                fb[step][j] =
-                    *reinterpret_cast<const i32x4 *>(sb + row * kSK + ((c ^ ((row >> 1) & 7)) << 4));
+                fb[step][j] = *reinterpret_cast<const i32x4 *>(sb + lds_pos(kBP, row, c));
             }
         }
 #pragma unroll
@@ -916,9 +929,10 @@ void igemm_run(size_t m, size_t n, const void *input, size_t group_idx, size_t m
                           (p.kernel_shape[2] - 1) * p.dilation[2] < 1024 && in_bytes < (1ull << 31);
     if (packed) {
         TQT_REQUIRE(ldb >= kfull, "ldb < k");
-        a.pb = make_pack(kPackI8NStep, n, ldb, kfull, k_idx_b);
-        launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8, PK_B>(a, geo_fast && k_idx_b % 16 == 0,
-                                                           stream, where);
+        a.pb = make_pack(kPackI8NStep, kPackI8Chunk, n, ldb, kfull, k_idx_b);
+        launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8, PK_B>(
+            a, geo_fast && kfull % kPackI8Chunk == 0 && kfull < (1u << 24) && k_idx_b % 16 == 0,
+            stream, where);
     } else {
         launch_int8<A_CONV_CL, B_NK, EPI_REQUANT_I8>(a, geo_fast && ldb % 16 == 0, stream, where);
     }
@@ -958,11 +972,12 @@ void packed_gemm_run(size_t m, size_t n, size_t k, const void *A, size_t lda, si
     a.ldc = static_cast<long long>(ldc);
     a.D = D;
     a.ldd = static_cast<long long>(ldd);
-    a.pa = make_pack(a_packed ? kPackI8MStep : 0, m, lda, k, a_packed ? k_idx_a : 0);
-    a.pb = make_pack(kPackI8NStep, n, ldb, k, k_idx_b);
-    // fast paths read 16-byte chunks: every chunk of a packed row must start 16-byte aligned
-    const bool fast = (k % 16 == 0) && aligned16(A) && aligned16(B) && (k_idx_b % 16 == 0) &&
-                      (a_packed ? k_idx_a % 16 == 0 : lda % 16 == 0);
+    a.pa = make_pack(a_packed ? kPackI8MStep : 0, kPackI8Chunk, m, lda, k,
+                     a_packed ? k_idx_a : 0);
+    a.pb = make_pack(kPackI8NStep, kPackI8Chunk, n, ldb, k, k_idx_b);
+    // fast paths: whole chunks, every 16-byte load aligned, packed k offsets within 24 bits
+    const bool fast = (k % kPackI8Chunk == 0) && k < (1u << 24) && aligned16(A) && aligned16(B) &&
+                      (k_idx_b % 16 == 0) && (a_packed ? k_idx_a % 16 == 0 : lda % 16 == 0);
     if (a_packed) {
         launch_int8<A_MATRIX, B_NK, EPI, PK_AB>(a, fast, stream, where);
     } else {

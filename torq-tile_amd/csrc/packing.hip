@@ -6,8 +6,9 @@
 // gemm_f16_i4.hip). The layout (PackDesc, pack_offset) is defined in tqt_hip_common.hpp; the
 // reference's packers are the permutations of tqt_gemm_pack_rvv.h:354-398, 542-567, 740-856.
 //
-// A packer is one GPU kernel: one thread per 16-byte chunk of the packed output gathers its
-// bytes from the source row (k-contiguous [rows, k] sources) or column ([k, n] sources).
+// A packer is one GPU kernel: one thread per 16-byte piece of a row gathers its bytes from the
+// source row (k-contiguous [rows, k] sources) or column ([k, n] sources). Chunks are multiples of
+// 16 bytes, so a piece never straddles two chunks and its bytes are contiguous in the output.
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950.h"
@@ -39,7 +40,7 @@ __global__ __launch_bounds__(256) void pack_kernel(PackSrc s, uint8_t *dst, Pack
     const long long kb0 = 16 * (idx - static_cast<long long>(r) * nchunks);
     const long long rem = d.kbytes - kb0;
     const int cw = rem < 16 ? static_cast<int>(rem) : 16;
-    uint8_t *o = dst + pack_offset(d, r, kb0);  // the chunk's cw bytes are contiguous
+    uint8_t *o = dst + pack_offset(d, r, kb0);  // the piece's cw bytes are contiguous
     const uint8_t *row = s.p + static_cast<long long>(r) * s.rs;
     if (!kFrag && s.cs == 1 && cw == 16 &&
         ((reinterpret_cast<uintptr_t>(row + kb0) | reinterpret_cast<uintptr_t>(o)) & 15) == 0) {
@@ -84,7 +85,7 @@ void pack_rows(const void *src, long long rs, long long cs, void *dst, const Pac
 // Packer argument conventions of the reference (tqt_gemm_pack_rvv.h): (rows, k, ld, ld_packed,
 // k_idx) in elements of `esize` bytes; int4 operands pass esize 0 (two elements per byte).
 void pack_nk(size_t rows, size_t k, size_t ld, size_t ld_packed, size_t k_idx, size_t step,
-             int esize, bool frag, const void *src, void *dst, void *stream, bool sync,
+             int kc, int esize, bool frag, const void *src, void *dst, void *stream, bool sync,
              const char *where)
 {
     if (esize == 0) {
@@ -93,7 +94,7 @@ void pack_nk(size_t rows, size_t k, size_t ld, size_t ld_packed, size_t k_idx, s
     }
     TQT_REQUIRE(ld >= k && ld_packed >= k, "ld < k");
     auto bytes = [esize](size_t e) { return esize == 0 ? e / 2 : e * esize; };
-    const PackDesc d = make_pack(step, rows, bytes(ld_packed), bytes(k), bytes(k_idx));
+    const PackDesc d = make_pack(step, kc, rows, bytes(ld_packed), bytes(k), bytes(k_idx));
     pack_rows(src, static_cast<long long>(bytes(ld)), 1, dst, d, frag, stream, sync, where);
 }
 
@@ -102,7 +103,7 @@ void pack_kn_i8(size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx,
                 const void *src, void *dst, void *stream, bool sync, const char *where)
 {
     TQT_REQUIRE(ldb >= n && ldb_packed >= k, "ldb < n or ldb_packed < k");
-    const PackDesc d = make_pack(step, n, ldb_packed, k, k_idx);
+    const PackDesc d = make_pack(step, kPackI8Chunk, n, ldb_packed, k, k_idx);
     pack_rows(src, 1, static_cast<long long>(ldb), dst, d, false, stream, sync, where);
 }
 
@@ -174,14 +175,14 @@ void tqt_run_a_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950_async(size_t m, size_t k,
                                                              const void *A, void *A_packed,
                                                              void *stream)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, 1, false, A, A_packed, stream, false,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, kPackI8Chunk, 1, false, A, A_packed, stream, false,
             "tqt_run_a_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950");
 }
 void tqt_run_a_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950(size_t m, size_t k, size_t lda,
                                                        size_t lda_packed, size_t k_idx,
                                                        const void *A, void *A_packed)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, 1, false, A, A_packed, nullptr, true,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, kPackI8Chunk, 1, false, A, A_packed, nullptr, true,
             "tqt_run_a_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950");
 }
 void tqt_run_b_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950_async(size_t n, size_t k, size_t ldb,
@@ -204,14 +205,14 @@ void tqt_run_bt_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950_async(size_t n, size_t k
                                                               const void *B, void *B_packed,
                                                               void *stream)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, 1, false, B, B_packed, stream, false,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed, stream, false,
             "tqt_run_bt_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950");
 }
 void tqt_run_bt_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950(size_t n, size_t k, size_t ldb,
                                                         size_t ldb_packed, size_t k_idx,
                                                         const void *B, void *B_packed)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, 1, false, B, B_packed, nullptr, true,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed, nullptr, true,
             "tqt_run_bt_pack_gemm_clamp_i32_i8p_i8p_mfma_gfx950");
 }
 
@@ -288,13 +289,13 @@ void tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed,
     void *stream)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, 1, false, B, B_packed, stream, false,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed, stream, false,
             "tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
 }
 void tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950(
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, 1, false, B, B_packed, nullptr, true,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed, nullptr, true,
             "tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
 }
 
@@ -362,13 +363,13 @@ void tqt_run_a_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950
     size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed,
     void *stream)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, 1, false, A, A_packed, stream, false,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, kPackI8Chunk, 1, false, A, A_packed, stream, false,
             "tqt_run_a_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950");
 }
 void tqt_run_a_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(
     size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, 1, false, A, A_packed, nullptr, true,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, kPackI8Chunk, 1, false, A, A_packed, nullptr, true,
             "tqt_run_a_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950");
 }
 void tqt_run_b_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950_async(
@@ -388,13 +389,13 @@ void tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx95
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed,
     void *stream)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, 1, false, B, B_packed, stream, false,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed, stream, false,
             "tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950");
 }
 void tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, 1, false, B, B_packed, nullptr, true,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed, nullptr, true,
             "tqt_run_bt_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950");
 }
 
@@ -466,26 +467,26 @@ void tqt_run_a_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950_async(
     size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed,
     void *stream)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A8MStep, 1, false, A, A_packed, stream, false,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A8MStep, kPackW4A8Chunk, 1, false, A, A_packed, stream, false,
             "tqt_run_a_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
 }
 void tqt_run_a_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950(
     size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A8MStep, 1, false, A, A_packed, nullptr, true,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A8MStep, kPackW4A8Chunk, 1, false, A, A_packed, nullptr, true,
             "tqt_run_a_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
 }
 void tqt_run_bt_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950_async(
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed,
     void *stream)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A8NStep, 0, false, B, B_packed, stream, false,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A8NStep, kPackW4A8Chunk, 0, false, B, B_packed, stream, false,
             "tqt_run_bt_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
 }
 void tqt_run_bt_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950(
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A8NStep, 0, false, B, B_packed, nullptr, true,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A8NStep, kPackW4A8Chunk, 0, false, B, B_packed, nullptr, true,
             "tqt_run_bt_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
 }
 
@@ -559,26 +560,26 @@ void tqt_run_a_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950_async(
     size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed,
     void *stream)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A16MStep, 2, false, A, A_packed, stream, false,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A16MStep, kPackW4A16Chunk, 2, false, A, A_packed, stream, false,
             "tqt_run_a_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
 }
 void tqt_run_a_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(
     size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed)
 {
-    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A16MStep, 2, false, A, A_packed, nullptr, true,
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A16MStep, kPackW4A16Chunk, 2, false, A, A_packed, nullptr, true,
             "tqt_run_a_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
 }
 void tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950_async(
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed,
     void *stream)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, 0, true, B, B_packed, stream, false,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, kPackW4A16Chunk, 0, true, B, B_packed, stream, false,
             "tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
 }
 void tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(
     size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed)
 {
-    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, 0, true, B, B_packed, nullptr, true,
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, kPackW4A16Chunk, 0, true, B, B_packed, nullptr, true,
             "tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
 }
 
@@ -631,14 +632,14 @@ void tqt_run_bt_pack_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx
     size_t n, size_t k, size_t ldw, size_t ldw_packed, size_t k_idx, const void *weight,
     void *weight_packed, void *stream)
 {
-    pack_nk(n, k, ldw, ldw_packed, k_idx, kPackI8NStep, 1, false, weight, weight_packed, stream,
+    pack_nk(n, k, ldw, ldw_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, weight, weight_packed, stream,
             false, "tqt_run_bt_pack_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
 }
 void tqt_run_bt_pack_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950(
     size_t n, size_t k, size_t ldw, size_t ldw_packed, size_t k_idx, const void *weight,
     void *weight_packed)
 {
-    pack_nk(n, k, ldw, ldw_packed, k_idx, kPackI8NStep, 1, false, weight, weight_packed, nullptr,
+    pack_nk(n, k, ldw, ldw_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, weight, weight_packed, nullptr,
             true, "tqt_run_bt_pack_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
 }
 

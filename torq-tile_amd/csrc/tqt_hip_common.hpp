@@ -153,20 +153,24 @@ __device__ __forceinline__ void column_multiplier_dev(float scale_a, const float
 // [p*step, p*step + w), w = min(step, rows - p*step), and starts at byte p*step*ld, moved back by
 // shift*(step - w) bytes when a panel after the first is narrower (shift = k_idx in bytes: the
 // reference's tail-tile rule, tqt_gemm_pack_rvv.h:314-318). Inside a panel each row is cut into
-// 16-byte chunks - one MFMA lane fragment, 16 consecutive k bytes of one row - stored chunk-major:
-// chunk c of local row r at 16*c*w + r*cw, cw = min(16, kbytes - 16*c). One k-step of a whole
-// panel is thus one contiguous block whose fragments come in the order MFMA lanes take them
-// (lane l <-> row l mod 16 or 32), and when kbytes % 16 == 0 byte kb (a multiple of 16) of row r
-// sits at row_base(r) + kb * w. A panel of w rows holds w * kbytes bytes, so the packed sizes are
-// the unpacked ones (m*k, n*k, n*k/2).
+// chunks of kc bytes stored chunk-major: chunk c of local row r at kc*c*w + r*cw,
+// cw = min(kc, kbytes - kc*c). kc is the k-extent one wave load instruction takes from a row:
+// 128 bytes for the int8 and W4A8 mainloops (8 rows x 128 bytes per instruction: one contiguous
+// KiB), 16 bytes - one MFMA lane fragment - for W4A16 (16 channels x 16 bytes per lane group).
+// One k-step of a whole panel is thus one contiguous block in the order the lanes take it. When
+// kbytes % kc == 0, byte kb of row r sits at row_base(r) + (kb - kb % kc) * w + kb % kc. A panel
+// of w rows holds w * kbytes bytes, so the packed sizes are the unpacked ones (m*k, n*k, n*k/2).
 // ---------------------------------------------------------------------------------------------
-// Panel heights (m_step / n_step) of the packed kernel types.
+// Panel heights (m_step / n_step) and chunk sizes of the packed kernel types.
 constexpr size_t kPackI8MStep = 128;   // int8 GEMMs and igemmcl (A and B panels)
 constexpr size_t kPackI8NStep = 128;
+constexpr int kPackI8Chunk = 16;
 constexpr size_t kPackW4A8MStep = 16;  // W4A8: one 16-channel weight tile per panel
 constexpr size_t kPackW4A8NStep = 16;
+constexpr int kPackW4A8Chunk = 16;
 constexpr size_t kPackW4A16MStep = 32; // W4A16: one 32-row activation group, 16 channels
 constexpr size_t kPackW4A16NStep = 16;
+constexpr int kPackW4A16Chunk = 16;
 
 // Which operands of a kernel instance are in the packed layout; plain row-major otherwise.
 enum PackMode { PK_NONE = 0, PK_A = 1, PK_B = 2, PK_AB = 3 };
@@ -178,6 +182,7 @@ struct PackDesc
     long long shift;   // k_idx in bytes (tail panels after the first start shift*(step-w) earlier)
     int step;          // rows per panel; 0 = plain row-major (row r at r * ld)
     int rows;          // rows of the operand
+    int kc;            // chunk bytes (a power of two, >= 16)
 };
 
 __host__ __device__ inline long long pack_panel_base(const PackDesc &d, int p, int w)
@@ -195,13 +200,14 @@ struct PackRow
 {
     long long base;
     long long kbytes;
-    int w, rl;
+    int w, rl, kc;
 };
 
 __host__ __device__ inline PackRow pack_row_info(const PackDesc &d, int r)
 {
     PackRow pr;
     pr.kbytes = d.kbytes;
+    pr.kc = d.kc;
     if (d.step == 0) {
         pr.base = static_cast<long long>(r) * d.ld;
         pr.w = 1;
@@ -219,10 +225,10 @@ __host__ __device__ inline PackRow pack_row_info(const PackDesc &d, int r)
 // Byte offset of byte kb (any kb < kbytes) of the row.
 __host__ __device__ inline long long pack_row_byte(const PackRow &pr, long long kb)
 {
-    const long long c = kb >> 4;
-    const long long rem = pr.kbytes - 16 * c;
-    const long long cw = rem < 16 ? rem : 16;
-    return pr.base + 16 * c * pr.w + pr.rl * cw + (kb & 15);
+    const long long c0 = kb - kb % pr.kc;  // first byte of kb's chunk
+    const long long rem = pr.kbytes - c0;
+    const long long cw = rem < pr.kc ? rem : pr.kc;
+    return pr.base + c0 * pr.w + pr.rl * cw + kb % pr.kc;
 }
 
 __host__ __device__ inline long long pack_offset(const PackDesc &d, int r, long long kb)
@@ -230,7 +236,7 @@ __host__ __device__ inline long long pack_offset(const PackDesc &d, int r, long 
     return pack_row_byte(pack_row_info(d, r), kb);
 }
 
-// For kbytes % 16 == 0: byte kb (a multiple of 16) of row r is at the returned offset + kb * mul.
+// For kbytes % kc == 0: byte kb of row r is at the returned offset + pack_k(kb, mul, kc).
 __host__ __device__ inline long long pack_row(const PackDesc &d, int r, int &mul)
 {
     if (d.step == 0) {
@@ -241,12 +247,26 @@ __host__ __device__ inline long long pack_row(const PackDesc &d, int r, int &mul
     const int left = d.rows - p * d.step;
     const int w = left < d.step ? left : d.step;
     mul = w;
-    return pack_panel_base(d, p, w) + 16ll * (r - p * d.step);
+    return pack_panel_base(d, p, w) + static_cast<long long>(d.kc) * (r - p * d.step);
 }
 
-// Host-side description of a packed operand: `rows` rows of `kbytes` bytes, panel height `step`,
-// leading dimension `ld_bytes`, k_idx `shift_bytes`.
-inline PackDesc make_pack(size_t step, size_t rows, size_t ld_bytes, size_t kbytes,
+// Offset of byte kb from the row base pack_row returned (a plain row: kb itself). For a packed
+// row kb < 2^24 and mul <= 2^7 (the launchers of the packed fast paths check kbytes < 2^24; panel
+// heights are at most 128), so one 24-bit multiply gives it.
+template <int KC, bool kPacked>
+__device__ __forceinline__ uint32_t pack_k(uint32_t kb, int mul)
+{
+    if constexpr (!kPacked) {
+        return kb;
+    } else {
+        return __umul24(kb & ~static_cast<uint32_t>(KC - 1), static_cast<uint32_t>(mul)) +
+               (kb & static_cast<uint32_t>(KC - 1));
+    }
+}
+
+// Host-side description of a packed operand: `rows` rows of `kbytes` bytes, panel height `step`
+// (0: plain row-major), chunk bytes `kc`, leading dimension `ld_bytes`, k_idx `shift_bytes`.
+inline PackDesc make_pack(size_t step, int kc, size_t rows, size_t ld_bytes, size_t kbytes,
                           size_t shift_bytes)
 {
     TQT_REQUIRE(rows < (1u << 31), "dimension exceeds 2^31-1");
@@ -256,6 +276,7 @@ inline PackDesc make_pack(size_t step, size_t rows, size_t ld_bytes, size_t kbyt
     d.shift = static_cast<long long>(shift_bytes);
     d.step = static_cast<int>(step);
     d.rows = static_cast<int>(rows);
+    d.kc = kc;
     return d;
 }
 
