@@ -7,9 +7,10 @@ Headline (BASELINE.json metric "W4A8 GEMV HBM GB/s (M=1) + W8A8 GEMM int8 TOPS (
               M=512, K=4096, N=4096), with its MFMA roofline;
   * w4a8    = W4A8 decode GEMV HBM GB/s on configs[2] at M=1 (K=4096, N=11008), with its HBM
               roofline; M=4 and M=8 are reported beside it.
-The remaining configurations (int8->int32 GEMM, W4A16, int8 implicit-GEMM conv), and the packed
+The remaining configurations (int8->int32 GEMM, W4A16, int8 implicit-GEMM conv), the packed
 siblings of W8A8, W4A8 and W4A16 on the same shapes (operands packed by the library's packers
-before timing), are timed the same way and reported under "configs".
+before timing), and the W4A8 decode step with its activation quantization on the GPU, are timed
+the same way and reported under "configs".
 
 A step is one launch of the kernel over one batch of synthetic inputs already resident in
 HBM. Each launch reads a different copy of the weights (and activations): the copies together
@@ -188,8 +189,10 @@ def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng, packed=False):
                 bytes=algo_bytes, copies=nc, inputs=(A, B, sb, bias, zp_a))
 
 
-def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m, packed=False):
-    """packed: the qai8dxp_qsi4cxp sibling on the same inputs (packed once before timing)."""
+def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m, packed=False, dynq=False):
+    """packed: the qai8dxp_qsi4cxp sibling on the same inputs (packed once before timing).
+    dynq: each step is the decode pair "quantize the f32 activations on the GPU, then the W4A8
+    GEMV" (tqt_run_quantize_qai8dx_f32_gfx950 + the W4A8 run), both on the stream."""
     n, k = W4A8["n"], W4A8["k"]
     A, Bp, sa, za, sb, bias = inputs_w4a8(rng, m, n, k)
     nc = copies_for(Bp.nbytes)
@@ -207,15 +210,22 @@ def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m, packed=False):
     p = mod.QAI8DXQSI4CXParams(dsa.data_ptr(), dza.data_ptr(), dsb.data_ptr())
     f = lib.fn("w4a8p" if packed else "w4a8", "run_async")
     s = timer.stream.cuda_stream
+    if dynq:
+        Af = rng.standard_normal((m, k), dtype=np.float32)
+        dAf = [torch.from_numpy(Af).cuda() for _ in range(nc)]
 
     def launch(i):
+        if dynq:
+            lib.quantize_async(m, k, dAf[i].data_ptr(), k, dA[i].data_ptr(), k, dsa.data_ptr(),
+                               dza.data_ptr(), s)
         f(m, n, k, dA[i].data_ptr(), k, 0, dB[i].data_ptr(), k, 0, None, n, dD.data_ptr(), n,
           dbias.data_ptr(), -math.inf, math.inf, ctypes.byref(p), s)
 
     ms = timer.run(launch, nc, warmup, steps)
     ms_stream = timer.stream_ms(launch, nc, warmup, steps) if timer.graphs else ms
-    # B n*k/2 + scale_b 4n + bias 4n + A m*k + scale_a/zp_a 8m + D 4mn
-    algo_bytes = n * k // 2 + 4 * n + 4 * n + m * k + 8 * m + 4 * m * n
+    # B n*k/2 + scale_b 4n + bias 4n + A m*k + scale_a/zp_a 8m + D 4mn (+ the f32 A the
+    # quantization reads, 4mk, when it runs in the step)
+    algo_bytes = n * k // 2 + 4 * n + 4 * n + m * k + 8 * m + 4 * m * n + (4 * m * k if dynq else 0)
     return dict(ms=ms, ms_stream=ms_stream, gbs=algo_bytes / (ms * 1e-3) / 1e9, bytes=algo_bytes,
                 ops=2.0 * m * n * k, copies=nc, inputs=(A, Bp, sa, za, sb, bias))
 
@@ -461,7 +471,7 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,w4a16p,conv,"
+                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,w4a16p,w4a8dq,conv,"
                          "clamp,copy): "
                          "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
@@ -491,6 +501,7 @@ def main():
             "w8a8p": lambda: bench_w8a8(torch, mod, lib, timer, W, K, rng, packed=True),
             "w4a8p": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True),
             "w4a16p": lambda: bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True),
+            "w4a8dq": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True),
             "conv": lambda: bench_conv(torch, mod, lib, timer, W, K, rng),
             "clamp": lambda: bench_clamp(torch, mod, lib, timer, W, K, rng),
             "copy": lambda: bench_copy(torch, timer, W, K),
@@ -511,6 +522,7 @@ def main():
         w8p = bench_w8a8(torch, mod, lib, timer, W, K, rng, packed=True)
         w4p = bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True)
         w416p = bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True)
+        w4dq = bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True)
 
     w41 = w4[1]
     traffic = None if args.no_traffic else hbm_traffic()
@@ -569,6 +581,9 @@ def main():
             "packed qai8dxp_qsi4cxp M=1 K=4096 N=11008": {
                 "us": round(w4p["ms"] * 1e3, 3), "GB/s": round(w4p["gbs"], 2),
                 "hbm_frac": round(w4p["gbs"] / HBM_PEAK_GBS, 4)},
+            "W4A8 decode step with GPU activation quantization, M=1 K=4096 N=11008": {
+                "us": round(w4dq["ms"] * 1e3, 3), "GB/s": round(w4dq["gbs"], 2),
+                "hbm_frac": round(w4dq["gbs"] / HBM_PEAK_GBS, 4)},
             "packed f16p_qsi4c2p 32x14336x4096 bl32": {
                 "us": round(w416p["ms"] * 1e3, 3), "GB/s": round(w416p["gbs"], 2),
                 "hbm_frac": round(w416p["gbs"] / HBM_PEAK_GBS, 4)},

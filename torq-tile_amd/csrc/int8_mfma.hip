@@ -400,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Streaming kernel for B = [n, k] (W8A8 and igemmcl), k % 128 == 0.
+// Streaming kernel for plain A and B = [n, k] (W8A8 and its packed siblings), k % 128 == 0.
 //
 // A workgroup of 4 wave64s (2 x 2) owns a BM x 128 output tile (BM = 64 or 128) and walks k in
 // stages of 128 bytes through a 4-deep ring of LDS stages filled by direct global->LDS loads
@@ -417,16 +417,13 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 // ---------------------------------------------------------------------------------------------
 constexpr int kSK = 128;  // k bytes per pipeline stage
 
-// Source of padding taps of the implicit convolution (global->LDS loads cannot write zeros).
-__device__ __attribute__((aligned(16))) int8_t g_zero16[16];
-
 __host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm)
 {
     // s_waitcnt immediate (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
     return (vm & 15) | (7 << 4) | ((vm >> 4) << 14);
 }
 
-template <int BM, int AM, int EPI, int PK>
+template <int BM, int EPI, int PK>
 __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int tiles_m, int tiles,
                                                                int per_xcd)
 {
@@ -474,36 +471,21 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     constexpr bool kAP = (PK & PK_A) != 0;
     constexpr bool kBP = (PK & PK_B) != 0;
     const int8_t *a_row[A_DMA];
-    int a_chunk[A_DMA], a_mul[A_DMA];
-    int a_id0[A_DMA], a_ih0[A_DMA], a_iw0[A_DMA];
+    int a_mul[A_DMA];
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) {
         const int blk = wave * A_DMA + j;
         const int r = 8 * blk + (kAP ? (lane & 7) : (lane >> 3));
-        a_chunk[j] = kAP ? ((lane >> 3) ^ (blk & 1)) : ((lane & 7) ^ ((r >> 1) & 7));
+        const int chunk = kAP ? ((lane >> 3) ^ (blk & 1)) : ((lane & 7) ^ ((r >> 1) & 7));
         const int gm = min(m0 + r, a.M - 1);
+        long long base;
         a_mul[j] = 1;  // k multiplier of a packed row (its panel width)
-        if constexpr (AM == A_MATRIX) {
-            long long base;
-            if constexpr ((PK & PK_A) != 0) {
-                base = pack_row(a.pa, gm, a_mul[j]);
-            } else {
-                base = static_cast<long long>(gm) * a.lda;
-            }
-            a_row[j] = a.A + base + pack_k<kPackI8Chunk, kAP>(a_chunk[j] * 16, a_mul[j]);
-            a_id0[j] = a_ih0[j] = a_iw0[j] = 0;
+        if constexpr (kAP) {
+            base = pack_row(a.pa, gm, a_mul[j]);
         } else {
-            const ConvGeom &g = a.cv;
-            const long long p = a.p0 + gm;
-            const long long ohw = static_cast<long long>(g.OH) * g.OW;
-            const int od = static_cast<int>(p / ohw);
-            const int oh = static_cast<int>((p / g.OW) % g.OH);
-            const int ow = static_cast<int>(p % g.OW);
-            a_id0[j] = od * g.SD - g.PD;
-            a_ih0[j] = oh * g.SH - g.PH;
-            a_iw0[j] = ow * g.SW - g.PW;
-            a_row[j] = nullptr;
+            base = static_cast<long long>(gm) * a.lda;
         }
+        a_row[j] = a.A + base + pack_k<kPackI8Chunk, kAP>(chunk * 16, a_mul[j]);
     }
     const int8_t *b_row[B_DMA];
     int b_mul[B_DMA];
@@ -515,7 +497,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         const int gn = min(n0 + r, a.N - 1);
         long long base;
         b_mul[j] = 1;
-        if constexpr ((PK & PK_B) != 0) {
+        if constexpr (kBP) {
             base = pack_row(a.pb, gn, b_mul[j]);
         } else {
             base = static_cast<long long>(gn) * a.ldb;
@@ -524,31 +506,12 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     }
 
     auto issue = [&](int st, int8_t *sa, int8_t *sb) {
-        const int k0 = st * kSK;
+        [[maybe_unused]] const int k0 = st * kSK;  // read by the device pass only
 #pragma unroll
         for (int j = 0; j < A_DMA; ++j) {
-            const int8_t *src;
-            if constexpr (AM == A_MATRIX) {
-                src = a_row[j] + pack_k<kPackI8Chunk, kAP>(k0, a_mul[j]);
-            } else {
-                const ConvGeom &g = a.cv;
-                const int k = k0 + a_chunk[j] * 16;
-                const int tap = k / g.ICg;
-                const int ic = k - tap * g.ICg;
-                const int kw = tap % g.KW;
-                const int t2 = tap / g.KW;
-                const int kh = t2 % g.KH;
-                const int kd = t2 / g.KH;
-                const int id = a_id0[j] + kd * g.DD;
-                const int ih = a_ih0[j] + kh * g.DH;
-                const int iw = a_iw0[j] + kw * g.DW;
-                const bool inb = id >= 0 && id < g.ID && ih >= 0 && ih < g.IH && iw >= 0 &&
-                                 iw < g.IW;
-                src = inb ? a.A + ((static_cast<long long>(id) * g.IH + ih) * g.IW + iw) * g.IC + ic
-                          : g_zero16;
-            }
 #if defined(__HIP_DEVICE_COMPILE__)
-            __builtin_amdgcn_global_load_lds(src, sa + (wave * A_DMA + j) * 1024, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a_row[j] + pack_k<kPackI8Chunk, kAP>(k0, a_mul[j]),
+                                             sa + (wave * A_DMA + j) * 1024, 16, 0, 0);
 #endif
         }
 #pragma unroll
@@ -780,7 +743,7 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     }
 }
 
-template <int AM, int EPI, int PK>
+template <int EPI, int PK>
 void launch_stream(const Int8Args &a, hipStream_t stream)
 {
     const long long tiles_n = (a.N + kBN - 1) / kBN;
@@ -793,11 +756,11 @@ void launch_stream(const Int8Args &a, hipStream_t stream)
     const long long per_xcd = (tiles + 7) / 8;
     TQT_REQUIRE(tiles < (1ll << 30), "grid too large");
     if (big) {
-        hipLaunchKernelGGL((int8_stream_kernel<128, AM, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
+        hipLaunchKernelGGL((int8_stream_kernel<128, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
                            stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
                            static_cast<int>(per_xcd));
     } else {
-        hipLaunchKernelGGL((int8_stream_kernel<64, AM, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
+        hipLaunchKernelGGL((int8_stream_kernel<64, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
                            stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
                            static_cast<int>(per_xcd));
     }
@@ -814,7 +777,7 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
     // kernel is faster.
     if constexpr (BMd == B_NK && AM == A_MATRIX) {
         if (fast && a.K % kSK == 0) {
-            launch_stream<AM, EPI, PK>(a, stream);
+            launch_stream<EPI, PK>(a, stream);
             check_launch(where);
             return;
         }

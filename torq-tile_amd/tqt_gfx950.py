@@ -244,6 +244,14 @@ class Lib:
                 self._fns[(kind, action)] = f
         self.dll.tqt_gfx950_target.restype = ctypes.c_char_p
         self.dll.tqt_gfx950_target.argtypes = []
+        # dynamic per-row activation quantization (include/tqt_quantize_qai8dx_gfx950.h)
+        qargs = [c_size, c_size, c_vp, c_size, c_vp, c_size, c_vp, c_vp]
+        self.quantize = self.dll.tqt_run_quantize_qai8dx_f32_gfx950
+        self.quantize.restype = None
+        self.quantize.argtypes = qargs
+        self.quantize_async = self.dll.tqt_run_quantize_qai8dx_f32_gfx950_async
+        self.quantize_async.restype = None
+        self.quantize_async.argtypes = qargs + [c_vp]
 
     def fn(self, kind, action):
         return self._fns[(kind, action)]
@@ -252,7 +260,8 @@ class Lib:
         names = [_sym(k, a) for (k, a) in self._fns]
         for kind in ("w4a16", "w4a16p"):
             names += [_sym(kind, "run"), _sym(kind, "run_async")]
-        names.append("tqt_gfx950_target")
+        names += ["tqt_gfx950_target", "tqt_run_quantize_qai8dx_f32_gfx950",
+                  "tqt_run_quantize_qai8dx_f32_gfx950_async"]
         return sorted(set(names))
 
 
