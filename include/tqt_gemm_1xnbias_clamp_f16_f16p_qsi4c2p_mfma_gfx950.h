@@ -8,6 +8,7 @@
  * 32-k blocks) of a row the 16-byte chunk c holds 4-byte slice c of each of the four blocks,
  * the operand lane group c of the f16 MFMA takes, so the kernel reads it without a shuffle.
  *
+ *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,
@@ -25,7 +26,7 @@
  * (the line of each declaration is given below). Every pointer, source and packed
  * buffers included, is device-accessible; the packers run on the GPU and, like the runs,
  * return with their output written; the _async forms (no counterpart in the reference)
- * enqueue on a hipStream_t instead.
+ * enqueue on a hipStream_t instead. Params structs and scalars stay on the host.
  */
 #ifndef TQT_GEMM_1XNBIAS_CLAMP_F16_F16P_QSI4C2P_MFMA_GFX950_H
 #define TQT_GEMM_1XNBIAS_CLAMP_F16_F16P_QSI4C2P_MFMA_GFX950_H

@@ -8,6 +8,7 @@
  * dimensions and k_idx_a/k_idx_b for the tail rule, like the packers (the reference run uses k
  * and ignores k_idx, which agrees for the packers' own lda = k, k_idx = 0 case).
  *
+ *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,
@@ -26,7 +27,7 @@
  * (the line of each declaration is given below). Every pointer, source and packed
  * buffers included, is device-accessible; the packers run on the GPU and, like the runs,
  * return with their output written; the _async forms (no counterpart in the reference)
- * enqueue on a hipStream_t instead.
+ * enqueue on a hipStream_t instead. Params structs and scalars stay on the host.
  */
 #ifndef TQT_GEMM_1XNBIAS_CLAMP_F32_QAI8DXP_QSI4CXP_MFMA_GFX950_H
 #define TQT_GEMM_1XNBIAS_CLAMP_F32_QAI8DXP_QSI4CXP_MFMA_GFX950_H

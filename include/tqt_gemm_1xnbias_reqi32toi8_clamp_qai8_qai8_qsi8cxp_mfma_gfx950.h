@@ -7,6 +7,7 @@
  * gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt (per-column multiplier from scale_a *
  * scale_b[n] / scale_d, computed on the device).
  *
+ *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,
@@ -25,7 +26,7 @@
  * (the line of each declaration is given below). Every pointer, source and packed
  * buffers included, is device-accessible; the packers run on the GPU and, like the runs,
  * return with their output written; the _async forms (no counterpart in the reference)
- * enqueue on a hipStream_t instead.
+ * enqueue on a hipStream_t instead. Params structs and scalars stay on the host.
  */
 #ifndef TQT_GEMM_1XNBIAS_REQI32TOI8_CLAMP_QAI8_QAI8_QSI8CXP_MFMA_GFX950_H
 #define TQT_GEMM_1XNBIAS_REQI32TOI8_CLAMP_QAI8_QAI8_QSI8CXP_MFMA_GFX950_H

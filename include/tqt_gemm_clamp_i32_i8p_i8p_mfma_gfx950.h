@@ -6,6 +6,7 @@
  * (optional), D int32 [m, n]. The packed run uses the [n, k] streaming mainloop whatever the
  * source orientation was.
  *
+ *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,
@@ -24,7 +25,7 @@
  * (the line of each declaration is given below). Every pointer, source and packed
  * buffers included, is device-accessible; the packers run on the GPU and, like the runs,
  * return with their output written; the _async forms (no counterpart in the reference)
- * enqueue on a hipStream_t instead.
+ * enqueue on a hipStream_t instead. Params structs and scalars stay on the host.
  */
 #ifndef TQT_GEMM_CLAMP_I32_I8P_I8P_MFMA_GFX950_H
 #define TQT_GEMM_CLAMP_I32_I8P_I8P_MFMA_GFX950_H

@@ -6,7 +6,7 @@
  *   - struct tqt_qai8_qai8_qsi8cx_params  : reference src/gemm/gemm_i8_i8/tqt_params_i8_i8.h:16-24
  *   - struct tqt_qai8dx_qsi4cx_params     : reference src/gemm/gemm_i8_i4/tqt_params_i8_i4.h:23-28
  *   - struct tqt_conv_params              : reference src/common/tqt_conv.h:20-31
- *   - float16_t                           : reference src/common/tqt_common.h:28
+ *   - float16_t, bfloat16_t               : reference src/common/tqt_common.h:27-28
  *
  * Memory contract of every tqt_run_* in this library: A, B, C, D, bias, and the arrays the
  * param structs point to (scale_a, zero_point_a, scale_b) are device-accessible pointers
@@ -31,6 +31,12 @@ extern "C" {
 #ifndef TQT_FLOAT16_T_DEFINED
 #define TQT_FLOAT16_T_DEFINED
 typedef _Float16 float16_t;
+#endif
+
+/* reference src/common/tqt_common.h:27 */
+#ifndef TQT_BFLOAT16_T_DEFINED
+#define TQT_BFLOAT16_T_DEFINED
+typedef __bf16 bfloat16_t;
 #endif
 
 /* Quantization parameters for qai8 (A) x qsi8cx (B) -> qai8 (D).

@@ -12,6 +12,7 @@
 
 #include <float.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #ifdef _OPENMP
@@ -112,6 +113,26 @@ static uint16_t round_to_f16(uint32_t sign16, uint64_t sig, int exp2)
         return (uint16_t)(sign16 | 0x7c00u);
     }
     return (uint16_t)(sign16 | (uint16_t)((e + 15) << 10) | (uint16_t)(q - 1024));
+}
+
+float tqto_bf16_to_f32(uint16_t b)
+{
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t tqto_f32_to_bf16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) {
+        return 0x7fc0u;
+    }
+    /* round to nearest even on the 16 dropped bits */
+    const uint32_t lsb = (x >> 16) & 1u;
+    return (uint16_t)((x + 0x7fffu + lsb) >> 16);
 }
 
 uint16_t tqto_f32_to_f16(float f)
@@ -435,6 +456,51 @@ void tqto_gemm_qai8dx_qsi4cxt_f32(size_t m, size_t n, size_t k, const int8_t *A,
         }
     }
     TILE_LOOP_END
+}
+
+void tqto_gemm_qai8dx_qsi4cxt_h16(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                  const uint8_t *B, size_t ldb, const uint16_t *C, size_t ldc,
+                                  uint16_t *D, size_t ldd, const uint16_t *bias, uint16_t cmin,
+                                  uint16_t cmax, const float *scale_a,
+                                  const int32_t *zero_point_a, const float *scale_b, int out_bf16)
+{
+    /* …_{f16,bf16}_qai8dx_qsi4cxt_4x1vl_rvv.cpp gemm_kernel: the f32 path of
+     * tqto_gemm_qai8dx_qsi4cxt_f32 on widened C / bias / clamps (vfwcvt / vfwcvtbf16 are exact),
+     * then tqt_store_narrow_{f16,bf16}_kernel (vfncvt.f.f.w / vfncvtbf16.f.f.w, RNE). */
+    float (*widen)(uint16_t) = out_bf16 ? tqto_bf16_to_f32 : tqto_f16_to_f32;
+    float *C32 = NULL, *bias32 = NULL;
+    float *D32 = (float *)malloc(m * n * sizeof(float));
+    if (C) {
+        C32 = (float *)malloc(m * n * sizeof(float));
+        for (size_t i = 0; i < m; ++i) {
+            for (size_t j = 0; j < n; ++j) {
+                C32[i * n + j] = widen(C[i * ldc + j]);
+            }
+        }
+    }
+    if (bias) {
+        bias32 = (float *)malloc(n * sizeof(float));
+        for (size_t j = 0; j < n; ++j) {
+            bias32[j] = widen(bias[j]);
+        }
+    }
+    tqto_gemm_qai8dx_qsi4cxt_f32(m, n, k, A, lda, B, ldb, C32, n, D32, n, bias32, widen(cmin),
+                                 widen(cmax), scale_a, zero_point_a, scale_b);
+    for (size_t i = 0; i < m; ++i) {
+        for (size_t j = 0; j < n; ++j) {
+            const float f = D32[i * n + j];
+            uint16_t h;
+            if (out_bf16) {
+                h = tqto_f32_to_bf16(f);
+            } else {
+                h = f != f ? (uint16_t)0x7e00u : tqto_f32_to_f16(f);
+            }
+            D[i * ldd + j] = h;
+        }
+    }
+    free(D32);
+    free(C32);
+    free(bias32);
 }
 
 void tqto_gemm_f16_qsi4c2t_f32acc(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,

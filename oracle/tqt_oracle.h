@@ -26,6 +26,11 @@ int tqto_get_threads(void);
 float tqto_f16_to_f32(uint16_t h);
 uint16_t tqto_f32_to_f16(float f);
 
+/* bfloat16 <-> binary32: widening is exact; narrowing rounds to nearest even and gives the
+ * canonical quiet NaN 0x7fc0 for a NaN (RISC-V vfncvtbf16.f.f.w under the default rounding). */
+float tqto_bf16_to_f32(uint16_t b);
+uint16_t tqto_f32_to_bf16(float f);
+
 /* src/gemm/gemm_i8_i8/tqt_utils_i8_i8.h:98-132 (+ integer_from_exp :16-91) */
 void tqto_quantize_multiplier(double x, int32_t *mult, int32_t *shift);
 
@@ -60,6 +65,18 @@ void tqto_gemm_qai8dx_qsi4cxt_f32(size_t m, size_t n, size_t k, const int8_t *A,
                                   float *D, size_t ldd, const float *bias, float cmin, float cmax,
                                   const float *scale_a, const int32_t *zero_point_a,
                                   const float *scale_b);
+
+/* The f16 / bf16 output siblings gemm_1xnbias_clamp_{f16,bf16}_qai8dx_qsi4cxt
+ * (…_4x1vl_rvv.cpp gemm_kernel, epilogue tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:428-628): the f32
+ * epilogue above with C and bias widened from the output type, the clamp bounds widened to f32,
+ * then one RNE narrowing (a NaN becomes the canonical quiet NaN 0x7e00 / 0x7fc0, as RISC-V
+ * conversions give). C, D, bias and the clamps are raw 16-bit patterns; out_bf16 selects bf16. */
+void tqto_gemm_qai8dx_qsi4cxt_h16(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                  const uint8_t *B, size_t ldb, const uint16_t *C, size_t ldc,
+                                  uint16_t *D, size_t ldd, const uint16_t *bias, uint16_t cmin,
+                                  uint16_t cmax, const float *scale_a,
+                                  const int32_t *zero_point_a, const float *scale_b,
+                                  int out_bf16);
 
 /* W4A16 with f32 accumulation: the reference test oracle reference_gemm_quantized_weight_mixed
  * (test/common/reference_gemm.cpp:132-179) for TA = TD = f16, evaluated without FMA

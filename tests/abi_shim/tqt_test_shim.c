@@ -30,6 +30,14 @@
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_interface.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_interface.h"
+#include "tqt_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_interface.h"
+#include "tqt_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950.h"
 
 static const struct tqt_gemm_clamp_i32_i8_i8_ukernel k_clamp = {
     tqt_get_m_step_gemm_clamp_i32_i8_i8_mfma_gfx950,
@@ -179,11 +187,68 @@ static const struct tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_ukern
     tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950,
 };
 
+static const struct tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_ukernel k_w4a8_f16 = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_ukernel k_w4a8p_f16 = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_ukernel k_w4a8_bf16 = {
+    tqt_get_m_step_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_ukernel k_w4a8p_bf16 = {
+    tqt_get_m_step_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
+};
+
 /* m_step and n_step of each kernel type read through its interface struct:
  * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl, then the packed types
  * clamp_i32_i8p_i8p, qai8_qai8_qsi8cxp, qai8_qai8p_qsi8cxp, qai8dxp_qsi4cxp, f16p_qsi4c2p,
- * igemmcl qsi8cxp. */
-void tqts_steps_via_interfaces(size_t out[22])
+ * igemmcl qsi8cxp, then the W4A8 output siblings f16 qsi4cxt, f16 qsi4cxp, bf16 qsi4cxt,
+ * bf16 qsi4cxp. */
+void tqts_steps_via_interfaces(size_t out[30])
 {
     out[0] = k_clamp.get_m_step();
     out[1] = k_clamp.get_n_step();
@@ -207,6 +272,14 @@ void tqts_steps_via_interfaces(size_t out[22])
     out[19] = k_w4a16p.get_n_step();
     out[20] = k_igemmp.get_m_step();
     out[21] = k_igemmp.get_n_step();
+    out[22] = k_w4a8_f16.get_m_step();
+    out[23] = k_w4a8_f16.get_n_step();
+    out[24] = k_w4a8p_f16.get_m_step();
+    out[25] = k_w4a8p_f16.get_n_step();
+    out[26] = k_w4a8_bf16.get_m_step();
+    out[27] = k_w4a8_bf16.get_n_step();
+    out[28] = k_w4a8p_bf16.get_m_step();
+    out[29] = k_w4a8p_bf16.get_n_step();
 }
 
 /* W4A16 run through the interface struct with _Float16 clamps given as binary16 bits. */
@@ -285,5 +358,55 @@ void tqts_run_w4a16p(size_t m, size_t n, size_t k, size_t bl, const void *A_pack
     } else {
         k_w4a16p.run_gemm(m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b,
                           ldsb, C, ldc, D, ldd, bias, cmin, cmax);
+    }
+}
+
+/* W4A8 with a 16-bit D (f16 when bf16 == 0, else bf16), the plain (qsi4cxt) or packed (qsi4cxp)
+ * type, clamp bounds given as their 16-bit patterns: through the interface struct, or
+ * stream-ordered when stream != NULL. */
+void tqts_run_w4a8h(int bf16, int packed, size_t m, size_t n, size_t k, const void *A,
+                    size_t lda, size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b,
+                    const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+                    uint16_t cmin_bits, uint16_t cmax_bits,
+                    const struct tqt_qai8dx_qsi4cx_params *params, void *stream)
+{
+    if (bf16) {
+        bfloat16_t cmin, cmax;
+        memcpy(&cmin, &cmin_bits, 2);
+        memcpy(&cmax, &cmax_bits, 2);
+        if (packed && stream) {
+            tqt_run_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950_async(
+                m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, cmin, cmax,
+                params, stream);
+        } else if (packed) {
+            k_w4a8p_bf16.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias,
+                                  cmin, cmax, params);
+        } else if (stream) {
+            tqt_run_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950_async(
+                m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, cmin, cmax,
+                params, stream);
+        } else {
+            k_w4a8_bf16.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias,
+                                 cmin, cmax, params);
+        }
+        return;
+    }
+    float16_t cmin, cmax;
+    memcpy(&cmin, &cmin_bits, 2);
+    memcpy(&cmax, &cmax_bits, 2);
+    if (packed && stream) {
+        tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950_async(
+            m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, cmin, cmax, params,
+            stream);
+    } else if (packed) {
+        k_w4a8p_f16.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, cmin,
+                             cmax, params);
+    } else if (stream) {
+        tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950_async(
+            m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, cmin, cmax, params,
+            stream);
+    } else {
+        k_w4a8_f16.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, cmin,
+                            cmax, params);
     }
 }

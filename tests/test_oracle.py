@@ -58,6 +58,58 @@ def test_f32_to_f16_rounding():
     assert np.array_equal(got, exp)
 
 
+def test_bf16_conversions():
+    """bfloat16 widening is exact for every pattern; narrowing rounds to nearest even on the 16
+    dropped bits (checked against an integer formulation of RNE and against the defining
+    property: the result is a neighbour of x and the nearer one, ties to even), NaN -> 0x7fc0."""
+    o = T.oracle()
+    bits = np.arange(65536, dtype=np.uint16)
+    got = np.array([o.tqto_bf16_to_f32(int(b)) for b in bits], np.float32)
+    exp = (bits.astype(np.uint32) << 16).view(np.float32)
+    nan = np.isnan(exp)
+    assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))
+    rng = np.random.default_rng(1)
+    u = np.concatenate([rng.integers(0, 2 ** 32, 40000, dtype=np.uint64).astype(np.uint32),
+                        np.array([0x3f808000, 0x3f818000, 0x3f80ffff, 0x7f7fffff, 0x7f800000,
+                                  0xff800000, 0x7fc00001, 0x00008000, 0x80018000], np.uint32)])
+    vals = u.view(np.float32)
+    got = np.array([o.tqto_f32_to_bf16(float(v)) for v in vals], np.uint16)
+    np.testing.assert_array_equal(got, T.bf16_bits(vals))
+    fin = np.isfinite(vals) & (np.abs(vals) < 3.38e38)
+    x = vals[fin].astype(np.float64)
+    y = T.bits_bf16_f32(got[fin]).astype(np.float64)
+    lo = T.bits_bf16_f32((u[fin] >> 16).astype(np.uint16)).astype(np.float64)  # truncation
+    step = np.abs(T.bits_bf16_f32(((u[fin] >> 16) + 1).astype(np.uint16)).astype(np.float64) - lo)
+    assert np.all(np.abs(y - x) <= step / 2 + 0.0)
+    ties = np.abs(np.abs(y - x) - step / 2) == 0
+    assert np.all((got[fin][ties] & 1) == 0)
+    assert all(o.tqto_f32_to_bf16(float("nan")) == 0x7FC0 for _ in range(1))
+
+
+def test_w4a8_h16_is_f32_epilogue_then_narrowing():
+    """The f16 / bf16 output siblings: the f32 oracle on widened C, bias and clamp bounds,
+    rounded once (f16: numpy's RNE; bf16: the integer RNE above)."""
+    m, n, k = 5, 40, 256
+    d = T.gen_w4a8(m, n, k, seed=8, with_c=True)
+    rng = np.random.default_rng(9)
+    for bf16 in (False, True):
+        if bf16:
+            C16, b16 = T.bf16_bits(d["C"]), T.bf16_bits(d["bias"])
+            w = T.bits_bf16_f32
+            cmin, cmax = int(T.bf16_bits(np.float32(-3.0))), int(T.bf16_bits(np.float32(2.5)))
+        else:
+            C16, b16 = T.f16_bits(d["C"]), T.f16_bits(d["bias"])
+            w = lambda b: T.bits_f16(b).astype(np.float32)
+            cmin, cmax = int(T.f16_bits(-3.0)), int(T.f16_bits(2.5))
+        got = T.oracle_w4a8_h16(d["A"], d["Bp"], C16, b16, cmin, cmax, d["scale_a"], d["zp_a"],
+                                d["scale_b"], bf16)
+        f32 = T.oracle_w4a8(d["A"], d["Bp"], w(C16), w(b16), float(w(np.uint16(cmin))),
+                            float(w(np.uint16(cmax))), d["scale_a"], d["zp_a"], d["scale_b"])
+        exp = T.bf16_bits(f32) if bf16 else f32.astype(np.float16).view(np.uint16)
+        np.testing.assert_array_equal(got, exp)
+    del rng
+
+
 # ------------------------------------------------------------------------------------------
 # Requantization multiplier
 # ------------------------------------------------------------------------------------------

@@ -184,12 +184,22 @@ def test_packed_sizes_equal_unpacked_sizes(lib, mod):
     assert g("w8a8p", "get_d_size")(m, n) == m * n
     assert g("w4a8p", "get_d_size")(m, n) == 4 * m * n
     assert g("w4a16p", "get_d_size")(m, n) == 2 * m * n
+    for kind in ("w4a8h", "w4a8b", "w4a8hp", "w4a8bp"):
+        assert g(kind, "get_d_size")(m, n) == 2 * m * n
+        ms = _getter(lib, sym(mod, kind, "get_m_step"), 0)()
+        ns = _getter(lib, sym(mod, kind, "get_n_step"), 0)()
+        assert (ms, ns) == (_getter(lib, sym(mod, "w4a8", "get_m_step"), 0)(),
+                            _getter(lib, sym(mod, "w4a8", "get_n_step"), 0)())
+        off = _getter(lib, sym(mod, kind, "get_d_offset"), 3)(3 * ms, 2 * ns, n)
+        assert off == 2 * (3 * ms * n + 2 * ns)
+        assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(2 * ns) == 2 * 2 * ns
 
 
 def test_packed_steps_via_interface_structs(lib, mod, shim):
-    out = (ctypes.c_size_t * 22)()
+    out = (ctypes.c_size_t * 30)()
     shim.tqts_steps_via_interfaces(out)
-    kinds = ["clamp", "w8a8", "w4a8", "w4a16", "igemmcl"] + list(PACKED)
+    kinds = (["clamp", "w8a8", "w4a8", "w4a16", "igemmcl"] + list(PACKED) +
+             ["w4a8h", "w4a8hp", "w4a8b", "w4a8bp"])
     for t, kind in enumerate(kinds):
         assert out[2 * t] == _getter(lib, sym(mod, kind, "get_m_step"), 0)()
         assert out[2 * t + 1] == _getter(lib, sym(mod, kind, "get_n_step"), 0)()

@@ -88,6 +88,8 @@ def oracle():
         "tqto_get_threads": (ctypes.c_int, []),
         "tqto_f16_to_f32": (f32, [u16]),
         "tqto_f32_to_f16": (u16, [f32]),
+        "tqto_bf16_to_f32": (f32, [u16]),
+        "tqto_f32_to_bf16": (u16, [f32]),
         "tqto_quantize_multiplier": (None, [ctypes.c_double, c_vp, c_vp]),
         "tqto_requant_one": (i8, [i32, i32, i32, i32, i8, i8]),
         "tqto_gemm_clamp_i32_i8_i8": (None, [c_size] * 3 + [c_vp, c_size, c_vp, c_size, c_vp,
@@ -100,6 +102,9 @@ def oracle():
         "tqto_gemm_qai8dx_qsi4cxt_f32": (None, [c_size] * 3 + [c_vp, c_size, c_vp, c_size, c_vp,
                                                  c_size, c_vp, c_size, c_vp, f32, f32, c_vp,
                                                  c_vp, c_vp]),
+        "tqto_gemm_qai8dx_qsi4cxt_h16": (None, [c_size] * 3 + [c_vp, c_size, c_vp, c_size, c_vp,
+                                                 c_size, c_vp, c_size, c_vp, u16, u16, c_vp,
+                                                 c_vp, c_vp, ctypes.c_int]),
         "tqto_gemm_f16_qsi4c2t_f32acc": (None, [c_size] * 4 + [c_vp, c_size, c_vp, c_size, c_vp,
                                                  c_size, c_vp, c_size, c_vp, c_size, c_vp, u16,
                                                  u16]),
@@ -213,6 +218,30 @@ def oracle_w4a8(A, Bp, C, bias, cmin, cmax, scale_a, zp_a, scale_b):
                                           ptr(bias), cmin, cmax, ptr(scale_a), ptr(zp_a),
                                           ptr(scale_b))
     return D
+
+
+def oracle_w4a8_h16(A, Bp, C16, bias16, cmin_bits, cmax_bits, scale_a, zp_a, scale_b, bf16):
+    """W4A8 with f16 (bf16=False) or bf16 C, bias, clamps and D, as 16-bit patterns."""
+    m, k = A.shape
+    n = Bp.shape[0]
+    D = np.zeros((m, n), np.uint16)
+    oracle().tqto_gemm_qai8dx_qsi4cxt_h16(m, n, k, ptr(A), k, ptr(Bp), k, ptr(C16), n, ptr(D), n,
+                                          ptr(bias16), cmin_bits, cmax_bits, ptr(scale_a),
+                                          ptr(zp_a), ptr(scale_b), 1 if bf16 else 0)
+    return D
+
+
+def bf16_bits(x):
+    """float32 values -> bfloat16 bit patterns, round to nearest even (integer arithmetic,
+    independent of the oracle's C)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return np.where(nan, np.uint16(0x7FC0), r)
+
+
+def bits_bf16_f32(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
 def oracle_w4a16(A16, Bp, S16, bl, C16, bias16, cmin_bits, cmax_bits, rvv=False):

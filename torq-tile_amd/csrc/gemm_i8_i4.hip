@@ -21,6 +21,10 @@
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -38,11 +42,11 @@ struct W4A8Args
     long long lda;
     const uint8_t *B;
     long long bstride;  // bytes between weight rows (= ldb / 2)
-    const float *C;
+    const void *C;  // f32, f16 or bf16 elements (the kernel's OUT)
     long long ldc;
-    float *D;
+    void *D;
     long long ldd;
-    const float *bias;
+    const void *bias;
     float cmin, cmax;
     const float *scale_a;
     const int32_t *zp_a;
@@ -104,7 +108,7 @@ __device__ __forceinline__ void decode_w16(const u32x4 w, i32x4 &q0, i32x4 &q1)
     q1[3] = static_cast<int32_t>((w[3] & 0xf0f0f0f0u) ^ 0x80808080u);
 }
 
-template <bool kActInLds, int PK>
+template <bool kActInLds, int PK, int OUT>
 __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 {
     __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][2 * kPairsPerBatch][1024];
@@ -139,10 +143,10 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         p_sa = a.scale_a[gm];
         p_za = a.zp_a[gm];
         if (a.bias) {
-            p_bias = a.bias[gn];
+            p_bias = load_out<OUT>(a.bias, gn);
         }
         if (a.C) {
-            p_c = a.C[static_cast<long long>(gm) * a.ldc + gn];
+            p_c = load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
         }
     }
 
@@ -298,14 +302,15 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
             rs += static_cast<uint32_t>(s_part[w][rows][ocol]);
         }
         const int gm = m0 + orow, gn = n0 + ocol;
-        a.D[static_cast<long long>(gm) * a.ldd + gn] = epilogue_f32(
-            static_cast<int32_t>(tot) >> 4, static_cast<int32_t>(rs) >> 4, p_za, p_sa, p_sb,
-            a.C ? &p_c : nullptr, a.bias ? &p_bias : nullptr, a.cmin, a.cmax);
+        store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn,
+                       epilogue_f32(static_cast<int32_t>(tot) >> 4, static_cast<int32_t>(rs) >> 4,
+                                    p_za, p_sa, p_sb, a.C ? &p_c : nullptr,
+                                    a.bias ? &p_bias : nullptr, a.cmin, a.cmax));
     }
 }
 
 // Generic path: one thread per output, any alignment, any even k.
-template <int PK>
+template <int PK, int OUT>
 __global__ __launch_bounds__(256) void w4a8_generic_kernel(W4A8Args a)
 {
     const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -330,14 +335,17 @@ __global__ __launch_bounds__(256) void w4a8_generic_kernel(W4A8Args a)
         acc += static_cast<uint32_t>(a0 * lo);
         acc += static_cast<uint32_t>(a1 * hi);
     }
-    a.D[static_cast<long long>(gm) * a.ldd + gn] = epilogue_f32(
-        static_cast<int32_t>(acc), static_cast<int32_t>(rsum), a.zp_a[gm], a.scale_a[gm],
-        a.scale_b[gn], a.C ? &a.C[static_cast<long long>(gm) * a.ldc + gn] : nullptr,
-        a.bias ? &a.bias[gn] : nullptr, a.cmin, a.cmax);
+    const float c = a.C ? load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn) : 0.f;
+    const float b = a.bias ? load_out<OUT>(a.bias, gn) : 0.f;
+    store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn,
+                   epilogue_f32(static_cast<int32_t>(acc), static_cast<int32_t>(rsum), a.zp_a[gm],
+                                a.scale_a[gm], a.scale_b[gn], a.C ? &c : nullptr,
+                                a.bias ? &b : nullptr, a.cmin, a.cmax));
 }
 
 // Shared body of the W4A8 runs. `packed`: A and B are in the packed layout (A rows of k bytes,
 // B rows of k/2 bytes; k_idx_a / k_idx_b apply the packers' tail rule).
+template <int OUT>
 void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a,
               const void *B, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
               size_t ldd, const void *bias, float clamp_min, float clamp_max,
@@ -364,11 +372,11 @@ void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_
     a.lda = static_cast<long long>(lda);
     a.B = static_cast<const uint8_t *>(B);
     a.bstride = static_cast<long long>(ldb / 2);
-    a.C = static_cast<const float *>(C);
+    a.C = C;
     a.ldc = static_cast<long long>(ldc);
-    a.D = static_cast<float *>(D);
+    a.D = D;
     a.ldd = static_cast<long long>(ldd);
-    a.bias = static_cast<const float *>(bias);
+    a.bias = bias;
     a.cmin = clamp_min;
     a.cmax = clamp_max;
     a.scale_a = params->scale_a;
@@ -398,18 +406,19 @@ void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_
         const dim3 grid(gx, static_cast<unsigned>(gy));
         if (rows_max * ppw * 16 <= 64) {  // each wave's activation slice: one chunk per lane
             if (packed) {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_AB>), grid, dim3(kWaves * 64), 0, s, a);
+                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_AB, OUT>), grid, dim3(kWaves * 64), 0,
+                                   s, a);
             } else {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_NONE>), grid, dim3(kWaves * 64), 0, s,
-                                   a);
+                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_NONE, OUT>), grid, dim3(kWaves * 64),
+                                   0, s, a);
             }
         } else {
             if (packed) {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_AB>), grid, dim3(kWaves * 64), 0, s,
-                                   a);
+                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_AB, OUT>), grid, dim3(kWaves * 64),
+                                   0, s, a);
             } else {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_NONE>), grid, dim3(kWaves * 64), 0,
-                                   s, a);
+                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_NONE, OUT>), grid, dim3(kWaves * 64),
+                                   0, s, a);
             }
         }
     } else {
@@ -417,11 +426,11 @@ void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_
         const long long blocks = (total + 255) / 256;
         TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
         if (packed) {
-            hipLaunchKernelGGL(w4a8_generic_kernel<PK_AB>, dim3(static_cast<unsigned>(blocks)),
+            hipLaunchKernelGGL((w4a8_generic_kernel<PK_AB, OUT>), dim3(static_cast<unsigned>(blocks)),
                                dim3(256), 0, s, a);
         } else {
-            hipLaunchKernelGGL(w4a8_generic_kernel<PK_NONE>, dim3(static_cast<unsigned>(blocks)),
-                               dim3(256), 0, s, a);
+            hipLaunchKernelGGL((w4a8_generic_kernel<PK_NONE, OUT>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
         }
     }
     check_launch(where);
@@ -487,8 +496,8 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950_async(
     size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
     float clamp_min, float clamp_max, const struct tqt_qai8dx_qsi4cx_params *params, void *stream)
 {
-    w4a8_run(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min, clamp_max,
-             params, false, as_stream(stream),
+    w4a8_run<OUT_F32>(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min,
+                      clamp_max, params, false, as_stream(stream),
              "tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950");
 }
 
@@ -519,8 +528,8 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950_async(
     size_t ldd, const void *bias, float clamp_min, float clamp_max,
     const struct tqt_qai8dx_qsi4cx_params *params, void *stream)
 {
-    w4a8_run(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd, bias,
-             clamp_min, clamp_max, params, true, as_stream(stream),
+    w4a8_run<OUT_F32>(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd,
+                      bias, clamp_min, clamp_max, params, true, as_stream(stream),
              "tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
 }
 
@@ -538,5 +547,79 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950(
         clamp_max, params, nullptr);
     finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
 }
+
+// =============================================================================================
+// Output-type siblings: W4A8 with f16 or bf16 D, C and bias (reference
+// …/gemm_1xnbias_clamp_{f16,bf16}_qai8dx_qsi4cxt/…_4x1vl_rvv.cpp and their packed siblings
+// …_{f16,bf16}_qai8dxp_qsi4cxp; epilogue tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:428-628: the f32
+// epilogue with C and bias widened from the output type, the clamp bounds widened to f32, one
+// round-to-nearest-even narrowing at the store). Packers and packed getters are in packing.hip.
+// =============================================================================================
+
+#define TQT_W4A8_OUT_GETTERS(T, ES)                                                               \
+    size_t tqt_get_m_step_##T##_mfma_gfx950(void) { return kW4A8MStep; }                         \
+    size_t tqt_get_n_step_##T##_mfma_gfx950(void) { return kW4A8NStep; }                         \
+    size_t tqt_get_a_offset_##T##_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda)            \
+    {                                                                                             \
+        TQT_REQUIRE(m_idx % kW4A8MStep == 0, "m_idx % m_step == 0");                             \
+        return m_idx * lda + k_idx;                                                               \
+    }                                                                                             \
+    size_t tqt_get_b_offset_##T##_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb)            \
+    {                                                                                             \
+        TQT_REQUIRE(n_idx % kW4A8NStep == 0, "n_idx % n_step == 0");                             \
+        TQT_REQUIRE(k_idx % 2 == 0, "k_idx % 2 == 0");                                           \
+        return n_idx * (ldb / 2) + k_idx / 2;                                                     \
+    }                                                                                             \
+    size_t tqt_get_c_offset_##T##_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)            \
+    {                                                                                             \
+        TQT_REQUIRE(m_idx % kW4A8MStep == 0, "m_idx % m_step == 0");                             \
+        TQT_REQUIRE(n_idx % kW4A8NStep == 0, "n_idx % n_step == 0");                             \
+        return (m_idx * ldc + n_idx) * (ES);                                                      \
+    }                                                                                             \
+    size_t tqt_get_bias_offset_##T##_mfma_gfx950(size_t n_idx)                                   \
+    {                                                                                             \
+        TQT_REQUIRE(n_idx % kW4A8NStep == 0, "n_idx % n_step == 0");                             \
+        return n_idx * (ES);                                                                      \
+    }                                                                                             \
+    size_t tqt_get_d_offset_##T##_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)            \
+    {                                                                                             \
+        TQT_REQUIRE(m_idx % kW4A8MStep == 0, "m_idx % m_step == 0");                             \
+        TQT_REQUIRE(n_idx % kW4A8NStep == 0, "n_idx % n_step == 0");                             \
+        return (m_idx * ldd + n_idx) * (ES);                                                      \
+    }                                                                                             \
+    size_t tqt_get_d_size_##T##_mfma_gfx950(size_t m, size_t n) { return m * n * (ES); }
+
+// The run pair (synchronous and stream-ordered) of a W4A8 output sibling.
+#define TQT_W4A8_OUT_RUNS(T, CT, OUT, PACKED)                                                     \
+    void tqt_run_##T##_mfma_gfx950_async(                                                         \
+        size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,   \
+        size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd,               \
+        const void *bias, CT clamp_min, CT clamp_max,                                             \
+        const struct tqt_qai8dx_qsi4cx_params *params, void *stream)                              \
+    {                                                                                             \
+        w4a8_run<OUT>(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias,            \
+                      static_cast<float>(clamp_min), static_cast<float>(clamp_max), params,       \
+                      PACKED, as_stream(stream), "tqt_run_" #T "_mfma_gfx950");                   \
+    }                                                                                             \
+    void tqt_run_##T##_mfma_gfx950(size_t m, size_t n, size_t k, const void *A, size_t lda,       \
+                                   size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b,     \
+                                   const void *C, size_t ldc, void *D, size_t ldd,                \
+                                   const void *bias, CT clamp_min, CT clamp_max,                  \
+                                   const struct tqt_qai8dx_qsi4cx_params *params)                 \
+    {                                                                                             \
+        if (!params || m == 0 || n == 0) {                                                        \
+            return;                                                                               \
+        }                                                                                         \
+        tqt_run_##T##_mfma_gfx950_async(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D,     \
+                                        ldd, bias, clamp_min, clamp_max, params, nullptr);        \
+        finish_sync(nullptr, "tqt_run_" #T "_mfma_gfx950");                                       \
+    }
+
+TQT_W4A8_OUT_GETTERS(gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt, sizeof(float16_t))
+TQT_W4A8_OUT_RUNS(gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt, float16_t, OUT_F16, false)
+TQT_W4A8_OUT_GETTERS(gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt, sizeof(bfloat16_t))
+TQT_W4A8_OUT_RUNS(gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt, bfloat16_t, OUT_BF16, false)
+TQT_W4A8_OUT_RUNS(gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp, float16_t, OUT_F16, true)
+TQT_W4A8_OUT_RUNS(gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp, bfloat16_t, OUT_BF16, true)
 
 }  // extern "C"

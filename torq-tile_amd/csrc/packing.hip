@@ -16,6 +16,8 @@
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_clamp_i32_i8p_i8p_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -642,5 +644,76 @@ void tqt_run_bt_pack_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx
     pack_nk(n, k, ldw, ldw_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, weight, weight_packed, nullptr,
             true, "tqt_run_bt_pack_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
 }
+
+// =============================================================================================
+// gemm_1xnbias_clamp_{f16,bf16}_qai8dxp_qsi4cxp (reference …_{f16,bf16}_qai8dxp_qsi4cxp_4x1vl_rvv.cpp):
+// the packed layout and packers of qai8dxp_qsi4cxp with 2-byte C, bias and D elements.
+// =============================================================================================
+#define TQT_W4A8P_OUT(T)                                                                          \
+    size_t tqt_get_m_step_##T##_mfma_gfx950(void) { return kPackW4A8MStep; }                     \
+    size_t tqt_get_n_step_##T##_mfma_gfx950(void) { return kPackW4A8NStep; }                     \
+    size_t tqt_get_a_packed_offset_##T##_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda,     \
+                                                     size_t actual_m)                            \
+    {                                                                                             \
+        TQT_REQ_M(kPackW4A8MStep);                                                                \
+        return packed_offset(m_idx, k_idx, lda, actual_m, kPackW4A8MStep, 1);                     \
+    }                                                                                             \
+    size_t tqt_get_b_packed_offset_##T##_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb,     \
+                                                     size_t actual_n)                            \
+    {                                                                                             \
+        TQT_REQ_N(kPackW4A8NStep);                                                                \
+        TQT_REQUIRE(k_idx % 2 == 0, "k_idx % 2 == 0");                                           \
+        const size_t w = actual_n < kPackW4A8NStep ? actual_n : kPackW4A8NStep;                   \
+        return n_idx * (ldb / 2) + (k_idx / 2) * w;                                               \
+    }                                                                                             \
+    size_t tqt_get_c_offset_##T##_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)            \
+    {                                                                                             \
+        TQT_REQ_M(kPackW4A8MStep);                                                                \
+        TQT_REQ_N(kPackW4A8NStep);                                                                \
+        return (m_idx * ldc + n_idx) * sizeof(uint16_t);                                          \
+    }                                                                                             \
+    size_t tqt_get_bias_offset_##T##_mfma_gfx950(size_t n_idx)                                   \
+    {                                                                                             \
+        TQT_REQ_N(kPackW4A8NStep);                                                                \
+        return n_idx * sizeof(uint16_t);                                                          \
+    }                                                                                             \
+    size_t tqt_get_d_offset_##T##_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)            \
+    {                                                                                             \
+        TQT_REQ_M(kPackW4A8MStep);                                                                \
+        TQT_REQ_N(kPackW4A8NStep);                                                                \
+        return (m_idx * ldd + n_idx) * sizeof(uint16_t);                                          \
+    }                                                                                             \
+    size_t tqt_get_d_size_##T##_mfma_gfx950(size_t m, size_t n) { return m * n * 2; }            \
+    size_t tqt_get_a_packed_size_##T##_mfma_gfx950(size_t m, size_t k) { return m * k; }         \
+    size_t tqt_get_b_packed_size_##T##_mfma_gfx950(size_t n, size_t k) { return n * k / 2; }     \
+    void tqt_run_a_pack_##T##_mfma_gfx950_async(size_t m, size_t k, size_t lda,                  \
+                                                size_t lda_packed, size_t k_idx, const void *A,   \
+                                                void *A_packed, void *stream)                     \
+    {                                                                                             \
+        pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A8MStep, kPackW4A8Chunk, 1, false, A,        \
+                A_packed, stream, false, "tqt_run_a_pack_" #T "_mfma_gfx950");                    \
+    }                                                                                             \
+    void tqt_run_a_pack_##T##_mfma_gfx950(size_t m, size_t k, size_t lda, size_t lda_packed,      \
+                                          size_t k_idx, const void *A, void *A_packed)            \
+    {                                                                                             \
+        pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A8MStep, kPackW4A8Chunk, 1, false, A,        \
+                A_packed, nullptr, true, "tqt_run_a_pack_" #T "_mfma_gfx950");                    \
+    }                                                                                             \
+    void tqt_run_bt_pack_##T##_mfma_gfx950_async(size_t n, size_t k, size_t ldb,                 \
+                                                 size_t ldb_packed, size_t k_idx, const void *B,  \
+                                                 void *B_packed, void *stream)                    \
+    {                                                                                             \
+        pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A8NStep, kPackW4A8Chunk, 0, false, B,        \
+                B_packed, stream, false, "tqt_run_bt_pack_" #T "_mfma_gfx950");                   \
+    }                                                                                             \
+    void tqt_run_bt_pack_##T##_mfma_gfx950(size_t n, size_t k, size_t ldb, size_t ldb_packed,     \
+                                           size_t k_idx, const void *B, void *B_packed)           \
+    {                                                                                             \
+        pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A8NStep, kPackW4A8Chunk, 0, false, B,        \
+                B_packed, nullptr, true, "tqt_run_bt_pack_" #T "_mfma_gfx950");                   \
+    }
+
+TQT_W4A8P_OUT(gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp)
+TQT_W4A8P_OUT(gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp)
 
 }  // extern "C"

@@ -295,6 +295,58 @@ __host__ __device__ inline long long w4a16_frag_pos(long long kb, long long kbyt
     return 64 * g + 16 * dw + 4 * blk + (kb & 3);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Output element types of the float-output kernel types (f32, f16, bf16). Loads widen exactly;
+// stores round to nearest even (the reference's vfncvt.f.f.w / vfncvtbf16.f.f.w under the
+// default rounding mode) and write the canonical quiet NaN (0x7e00, 0x7fc0) for a NaN, as those
+// RISC-V conversions do.
+// ---------------------------------------------------------------------------------------------
+enum OutType { OUT_F32 = 0, OUT_F16 = 1, OUT_BF16 = 2 };
+
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t b)
+{
+    uint32_t u = static_cast<uint32_t>(b) << 16;
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+}
+
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f)
+{
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return 0x7fc0;
+    }
+    return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <int OUT>
+__device__ __forceinline__ float load_out(const void *p, long long i)
+{
+    if constexpr (OUT == OUT_F32) {
+        return static_cast<const float *>(p)[i];
+    } else if constexpr (OUT == OUT_F16) {
+        return static_cast<float>(static_cast<const _Float16 *>(p)[i]);
+    } else {
+        return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+    }
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_out(void *p, long long i, float v)
+{
+    if constexpr (OUT == OUT_F32) {
+        static_cast<float *>(p)[i] = v;
+    } else if constexpr (OUT == OUT_F16) {
+        const _Float16 h = static_cast<_Float16>(v);
+        static_cast<uint16_t *>(p)[i] = v != v ? static_cast<uint16_t>(0x7e00)
+                                               : __builtin_bit_cast(uint16_t, h);
+    } else {
+        static_cast<uint16_t *>(p)[i] = f32_to_bf16_bits(v);
+    }
+}
+
 // One output of the requantization epilogue (reference tqt_kernel_gemm_i8_i8_4x1vl_rvv.h:
 // requantize_1xn :334-408 = vmulh, vsra by shift & 31, vadd zp, vnclip to i16 then i8;
 // clamp_i8 :231-259 = vmax then vmin).

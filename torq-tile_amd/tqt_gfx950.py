@@ -32,6 +32,11 @@ KERNELS = {
     "w4a8p": "gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp",
     "w4a16p": "gemm_1xnbias_clamp_f16_f16p_qsi4c2p",
     "igemmclp": "igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp",
+    # output-type siblings of the W4A8 types: f16 / bf16 D, C, bias and clamp bounds
+    "w4a8h": "gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt",
+    "w4a8b": "gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt",
+    "w4a8hp": "gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp",
+    "w4a8bp": "gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp",
 }
 
 
@@ -224,6 +229,14 @@ _SIGS["w4a16p"]["get_scale_b_offset"] = (c_size, [c_size] * 3)
 _SIGS["igemmclp"] = _packed_sigs(
     "igemmcl", ["run_bt_pack"], _SIGS["igemmcl"]["run"][1],
     ["get_b_packed_offset", "get_b_packed_size"])
+# f16 / bf16 clamps: the runs are reached through the test shim (tqts_run_w4a8h)
+for _kind in ("w4a8h", "w4a8b"):
+    _SIGS[_kind] = {a: v for a, v in _SIGS["w4a8"].items() if not a.startswith("run")}
+for _kind in ("w4a8hp", "w4a8bp"):
+    _SIGS[_kind] = _packed_sigs(
+        "w4a8", ["run_a_pack", "run_bt_pack"], None,
+        ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SHIM_RUNS = ("w4a16", "w4a16p", "w4a8h", "w4a8b", "w4a8hp", "w4a8bp")
 
 
 class Lib:
@@ -258,7 +271,7 @@ class Lib:
 
     def symbol_names(self):
         names = [_sym(k, a) for (k, a) in self._fns]
-        for kind in ("w4a16", "w4a16p"):
+        for kind in _SHIM_RUNS:
             names += [_sym(kind, "run"), _sym(kind, "run_async")]
         names += ["tqt_gfx950_target", "tqt_run_quantize_qai8dx_f32_gfx950",
                   "tqt_run_quantize_qai8dx_f32_gfx950_async"]
