@@ -8,7 +8,6 @@
  * 32-k blocks) of a row the 16-byte chunk c holds 4-byte slice c of each of the four blocks,
  * the operand lane group c of the f16 MFMA takes, so the kernel reads it without a shuffle.
  *
- *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,

@@ -9,7 +9,6 @@
  * reference epilogue tqt_kernel_gemm_i8_i4_4x1vl_rvv.h:428-628 does.
  * A and B are pre-packed by this type's packers (the qai8dxp_qsi4cxp layout).
  *
- *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,

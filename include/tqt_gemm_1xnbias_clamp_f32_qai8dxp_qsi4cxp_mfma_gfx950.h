@@ -8,7 +8,6 @@
  * dimensions and k_idx_a/k_idx_b for the tail rule, like the packers (the reference run uses k
  * and ignores k_idx, which agrees for the packers' own lda = k, k_idx = 0 case).
  *
- *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,

@@ -7,7 +7,6 @@
  * gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt (per-column multiplier from scale_a *
  * scale_b[n] / scale_d, computed on the device).
  *
- *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,

@@ -6,7 +6,6 @@
  * (optional), D int32 [m, n]. The packed run uses the [n, k] streaming mainloop whatever the
  * source orientation was.
  *
- *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,

@@ -6,7 +6,6 @@
  * pre-packed by run_bt_pack (rows of K = KD*KH*KW*IC/groups bytes). k, k_idx_a, C and ldc are
  * not read (the reference's "NO K-tiling"); k_idx_b applies the packers' tail rule.
  *
- *
  * Packed layout (this build's; the reference's is its own [m/MR, k, MR] / [n/vl, k, vl]):
  * rows (m of A, n of B) form panels of m_step / n_step rows. Panel p holds rows
  * [p*step, p*step + w), w = min(step, rows - p*step), and starts at element p*step*ld_packed,

@@ -67,6 +67,20 @@ void tqtr_reference_gemm_qw_mixed_f16(size_t m, size_t n, size_t k, size_t bl,
         cmax);
 }
 
+// test/common/reference_gemm.cpp:131-179, TA = float16_t, TD = float (A, scale_b as binary16
+// bits)
+void tqtr_reference_gemm_qw_mixed_f16_f32(size_t m, size_t n, size_t k, size_t bl,
+                                          const uint16_t *A, size_t lda, const uint8_t *B,
+                                          size_t ldb, const uint16_t *scale_b, size_t ldsb,
+                                          const float *C, size_t ldc, float *D, size_t ldd,
+                                          const float *bias, float cmin, float cmax)
+{
+    reference_gemm_quantized_weight_mixed<float16_t, float>(
+        m, n, k, bl, reinterpret_cast<const float16_t *>(A), lda, B, ldb,
+        reinterpret_cast<const float16_t *>(scale_b), ldsb, C, ldc, D, ldd, bias,
+        bias ? BiasMode::k1xN : BiasMode::kNone, cmin, cmax);
+}
+
 // test/common/reference_conv.cpp:17-127, T = float, channel-last
 void tqtr_reference_conv_cl_f32(size_t group_idx, const float *activation, const float *weight,
                                 const float *bias, float *output, const tqt_conv_params *params,

@@ -503,6 +503,24 @@ void tqto_gemm_qai8dx_qsi4cxt_h16(size_t m, size_t n, size_t k, const int8_t *A,
     free(bias32);
 }
 
+/* The k loop of test/common/reference_gemm.cpp:148-164 for output (i, j), starting from acc:
+ * acc += f32(A) * (f32(q - 8) * f32(scale)) in k order, each product and sum rounded. */
+static float w4a16_dot(float acc, const uint16_t *arow, const uint8_t *brow,
+                       const uint16_t *srow, size_t k, size_t bl)
+{
+    for (size_t p = 0; p < k; ++p) {
+        const float a_val = tqto_f16_to_f32(arow[p]);
+        const uint8_t byte_val = brow[p / 2];
+        const int32_t b_raw =
+            (p % 2 == 0) ? (int32_t)(byte_val & 0x0f) - 8 : (int32_t)(byte_val >> 4) - 8;
+        const float scale_val = tqto_f16_to_f32(srow[p / bl]);
+        const float b_dequant = (float)b_raw * scale_val;
+        const float prod = a_val * b_dequant;
+        acc = acc + prod;
+    }
+    return acc;
+}
+
 void tqto_gemm_f16_qsi4c2t_f32acc(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,
                                   size_t lda, const uint8_t *B, size_t ldb,
                                   const uint16_t *scale_b, size_t ldsb, const uint16_t *C,
@@ -516,26 +534,39 @@ void tqto_gemm_f16_qsi4c2t_f32acc(size_t m, size_t n, size_t k, size_t bl, const
     TILE_LOOP_BEGIN(m, n)
     for (size_t i = m0; i < m0 + mr; ++i) {
         for (size_t j = n0; j < n0 + nr; ++j) {
-            float acc = 0.0f;
-            if (C) {
-                acc = tqto_f16_to_f32(C[i * ldc + j]);
-            }
-            for (size_t p = 0; p < k; ++p) {
-                const float a_val = tqto_f16_to_f32(A[i * lda + p]);
-                const uint8_t byte_val = B[j * brow_bytes + p / 2];
-                const int32_t b_raw =
-                    (p % 2 == 0) ? (int32_t)(byte_val & 0x0f) - 8 : (int32_t)(byte_val >> 4) - 8;
-                const float scale_val = tqto_f16_to_f32(scale_b[j * ldsb + p / bl]);
-                const float b_dequant = (float)b_raw * scale_val;
-                const float prod = a_val * b_dequant;
-                acc = acc + prod;
-            }
+            float acc = C ? tqto_f16_to_f32(C[i * ldc + j]) : 0.0f;
+            acc = w4a16_dot(acc, A + i * lda, B + j * brow_bytes, scale_b + j * ldsb, k, bl);
             if (bias) {
                 acc = acc + tqto_f16_to_f32(bias[j]);
             }
             acc = (acc < cminf) ? cminf : acc; /* std::max(acc, clamp_min) */
             acc = (cmaxf < acc) ? cmaxf : acc; /* std::min(acc, clamp_max) */
             D[i * ldd + j] = tqto_f32_to_f16(acc);
+        }
+    }
+    TILE_LOOP_END
+}
+
+void tqto_gemm_f16_qsi4c2t_f32out(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,
+                                  size_t lda, const uint8_t *B, size_t ldb,
+                                  const uint16_t *scale_b, size_t ldsb, const float *C, size_t ldc,
+                                  float *D, size_t ldd, const float *bias, float cmin, float cmax)
+{
+    /* test/common/reference_gemm.cpp:132-179 (TA = float16_t, TD = float, BiasMode k1xN): the
+     * oracle the reference test holds gemm_1xnbias_clamp_f32_f16_qsi4c2t to
+     * (test/common/quantized_gemm_test_runner.h:1092-1095). */
+    const size_t brow_bytes = ldb / 2;
+    TILE_LOOP_BEGIN(m, n)
+    for (size_t i = m0; i < m0 + mr; ++i) {
+        for (size_t j = n0; j < n0 + nr; ++j) {
+            float acc = C ? C[i * ldc + j] : 0.0f;
+            acc = w4a16_dot(acc, A + i * lda, B + j * brow_bytes, scale_b + j * ldsb, k, bl);
+            if (bias) {
+                acc = acc + bias[j];
+            }
+            acc = (acc < cmin) ? cmin : acc; /* std::max(acc, clamp_min) */
+            acc = (cmax < acc) ? cmax : acc; /* std::min(acc, clamp_max) */
+            D[i * ldd + j] = acc;
         }
     }
     TILE_LOOP_END

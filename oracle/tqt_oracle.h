@@ -87,6 +87,13 @@ void tqto_gemm_f16_qsi4c2t_f32acc(size_t m, size_t n, size_t k, size_t bl, const
                                   size_t ldc, uint16_t *D, size_t ldd, const uint16_t *bias,
                                   uint16_t cmin, uint16_t cmax);
 
+/* W4A16 with f32 C, bias, clamp bounds and D (test/common/reference_gemm.cpp:132-179 with
+ * TA = float16_t, TD = float): the same k loop, no rounding to f16 anywhere. */
+void tqto_gemm_f16_qsi4c2t_f32out(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,
+                                  size_t lda, const uint8_t *B, size_t ldb,
+                                  const uint16_t *scale_b, size_t ldsb, const float *C, size_t ldc,
+                                  float *D, size_t ldd, const float *bias, float cmin, float cmax);
+
 /* W4A16 with the RVV kernel's own numerics (tqt_kernel_gemm_f16_i4_8x2vl_rvv.h:99-717):
  * f16-rounded dequantized weight, sequential f16 FMA over k, f16 bias add, f16 clamp. */
 void tqto_gemm_f16_qsi4c2t_rvv(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,

@@ -30,6 +30,10 @@
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_interface.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_f16_qsi4c2t_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_interface.h"
 #include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi4cxt_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_interface.h"
@@ -243,12 +247,42 @@ static const struct tqt_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_ukernel k_w4a8p_
     tqt_run_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950,
 };
 
+static const struct tqt_gemm_1xnbias_clamp_f32_f16_qsi4c2t_ukernel k_w4a16f = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_scale_b_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_ukernel k_w4a16fp = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_scale_b_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
+};
+
 /* m_step and n_step of each kernel type read through its interface struct:
  * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl, then the packed types
  * clamp_i32_i8p_i8p, qai8_qai8_qsi8cxp, qai8_qai8p_qsi8cxp, qai8dxp_qsi4cxp, f16p_qsi4c2p,
  * igemmcl qsi8cxp, then the W4A8 output siblings f16 qsi4cxt, f16 qsi4cxp, bf16 qsi4cxt,
- * bf16 qsi4cxp. */
-void tqts_steps_via_interfaces(size_t out[30])
+ * bf16 qsi4cxp, then the W4A16 f32-output siblings qsi4c2t, qsi4c2p. */
+void tqts_steps_via_interfaces(size_t out[34])
 {
     out[0] = k_clamp.get_m_step();
     out[1] = k_clamp.get_n_step();
@@ -280,6 +314,10 @@ void tqts_steps_via_interfaces(size_t out[30])
     out[27] = k_w4a8_bf16.get_n_step();
     out[28] = k_w4a8p_bf16.get_m_step();
     out[29] = k_w4a8p_bf16.get_n_step();
+    out[30] = k_w4a16f.get_m_step();
+    out[31] = k_w4a16f.get_n_step();
+    out[32] = k_w4a16fp.get_m_step();
+    out[33] = k_w4a16fp.get_n_step();
 }
 
 /* W4A16 run through the interface struct with _Float16 clamps given as binary16 bits. */
@@ -408,5 +446,21 @@ void tqts_run_w4a8h(int bf16, int packed, size_t m, size_t n, size_t k, const vo
     } else {
         k_w4a8_f16.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd, bias, cmin,
                             cmax, params);
+    }
+}
+
+/* W4A16 with f32 C, bias and D through the interface struct of the plain (qsi4c2t) or packed
+ * (qsi4c2p) f32-output type. */
+void tqts_run_w4a16f(int packed, size_t m, size_t n, size_t k, size_t bl, const void *A,
+                     size_t lda, size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b,
+                     const void *scale_b, size_t ldsb, const void *C, size_t ldc, void *D,
+                     size_t ldd, const void *bias, float cmin, float cmax)
+{
+    if (packed) {
+        k_w4a16fp.run_gemm(m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D,
+                           ldd, bias, cmin, cmax);
+    } else {
+        k_w4a16f.run_gemm(m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D,
+                          ldd, bias, cmin, cmax);
     }
 }

@@ -13,6 +13,7 @@ oracle/_ref/libtqt_ref.so by oracle/Makefile; nothing of them is copied here.
 Fixtures (numpy .npz, no pickles):
   ref_clamp_i32.npz    reference_gemm_i32_i8 on the reference's int8 shape list
   ref_w4a16.npz        reference_gemm_quantized_weight_mixed<f16,f16> on its W4A16 shape list
+  ref_w4a16_f32.npz    reference_gemm_quantized_weight_mixed<f16,float> on the same list
   ref_im2col.npz       tqt_im2col_cl<int8_t> on the reference's igemm shape list
   ref_qm.npz           tqt_quantize_multiplier on edge and random doubles
   ref_quant.npz        quantize_i8 / quantize_bias_i32 / fuse_zp_to_bias / quantize_fp16_to_int4
@@ -108,6 +109,43 @@ def main():
         out["w4a16_%d_clamp" % i] = np.array([cmin, cmax], np.uint16)
         out["w4a16_%d_D" % i] = D
     np.savez_compressed(os.path.join(HERE, "ref_w4a16.npz"),
+                        shapes=np.array(W4A16_SHAPES, np.int64), **out)
+
+    # --- W4A16 with f32 C / bias / clamp / D (the same runner with TD = float; its
+    # UniformRandomGenerator<float> draws C and bias, the clamp defaults to +-FLT_MAX) ---
+    out = {}
+    flt_max = float(np.finfo(np.float32).max)
+    for i, (m, n, k, bl, bias, c, clamp) in enumerate(W4A16_SHAPES):
+        A = np.zeros((m, k), np.uint16)
+        r.tqtr_fill_uniform_f16(-1.0, 1.0, 42, p(A), m, k)
+        Bsrc = np.zeros((n, k), np.uint16)
+        r.tqtr_fill_uniform_f16(-1.0, 1.0, 123, p(Bsrc), n, k)
+        Bp = np.zeros((n, k // 2), np.uint8)
+        S = np.zeros((n, k // bl), np.uint16)
+        r.tqtr_quantize_fp16_to_int4(n, k, bl, p(Bsrc), p(Bp), p(S), k // bl)
+        C = None
+        if c:
+            C = np.zeros((m, n), np.float32)
+            r.tqtr_fill_uniform_f32(-5.0, 5.0, 42, p(C), m, n)
+        bvec = None
+        if bias:
+            bvec = np.zeros(n, np.float32)
+            r.tqtr_fill_uniform_f32(-0.5, 0.5, 7, p(bvec), 1, n)
+        lo, hi = (-0.5, 0.5) if clamp else (-flt_max, flt_max)
+        D = np.zeros((m, n), np.float32)
+        r.tqtr_reference_gemm_qw_mixed_f16_f32(m, n, k, bl, p(A), k, p(Bp), k, p(S), k // bl,
+                                               p(C), n, p(D), n, p(bvec), ctypes.c_float(lo),
+                                               ctypes.c_float(hi))
+        out["w4a16f_%d_A" % i] = A
+        out["w4a16f_%d_Bp" % i] = Bp
+        out["w4a16f_%d_S" % i] = S
+        if C is not None:
+            out["w4a16f_%d_C" % i] = C
+        if bvec is not None:
+            out["w4a16f_%d_bias" % i] = bvec
+        out["w4a16f_%d_clamp" % i] = np.array([lo, hi], np.float32)
+        out["w4a16f_%d_D" % i] = D
+    np.savez_compressed(os.path.join(HERE, "ref_w4a16_f32.npz"),
                         shapes=np.array(W4A16_SHAPES, np.int64), **out)
 
     # --- implicit im2col order (src/common/tqt_conv.h:131-202) ---

@@ -221,6 +221,54 @@ def test_w4a16_f32acc_vs_reference_golden():
         np.testing.assert_array_equal(got, g[pre + "D"])
 
 
+def test_w4a16_f32out_vs_reference_golden():
+    """The f32-output W4A16 oracle reproduces reference_gemm_quantized_weight_mixed<f16, float>
+    bit for bit on the reference runner's own inputs (f32 C and bias from its generator,
+    +-FLT_MAX or +-0.5 clamps)."""
+    g = golden("ref_w4a16_f32.npz")
+    for i, (m, n, k, bl, bias, c, clamp) in enumerate(g["shapes"]):
+        pre = "w4a16f_%d_" % i
+        C = g[pre + "C"] if c else None
+        bv = g[pre + "bias"] if bias else None
+        lo, hi = (float(v) for v in g[pre + "clamp"])
+        got = T.oracle_w4a16_f32(g[pre + "A"], g[pre + "Bp"], g[pre + "S"], int(bl), C, bv, lo,
+                                 hi)
+        np.testing.assert_array_equal(got.view(np.uint32), g[pre + "D"].view(np.uint32))
+
+
+def test_w4a16_f32out_rounds_to_the_f16_oracle():
+    """With f16-valued C, bias and bounds the two W4A16 oracles share every step up to the
+    store, so the f16 one is the f32 one rounded to f16 (numpy RNE)."""
+    d = T.gen_w4a16(9, 40, 256, bl=32, seed=11, with_c=True, with_bias=True)
+    lo, hi = T.f16_bits(-3.0), T.f16_bits(2.5)
+    h = T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], 32, d["C16"], d["bias16"], int(lo), int(hi))
+    f = T.oracle_w4a16_f32(d["A16"], d["Bp"], d["S16"], 32, T.bits_f16(d["C16"]),
+                           T.bits_f16(d["bias16"]), -3.0, 2.5)
+    np.testing.assert_array_equal(h, f.astype(np.float16).view(np.uint16))
+
+
+def test_w4a16_f32out_closed_form():
+    """Independent float64 evaluation: each of the k + 2 rounded additions and k products of
+    the f32 loop moves the result by at most 2^-24 of the running magnitude, so the oracle is
+    within (2k + 4) * 2^-24 * (sum|a*w| + |C| + |bias|) of exact math; a dropped term, wrong
+    nibble order or wrong block index misses by far more."""
+    m, n, k, bl = 6, 50, 512, 16
+    d = T.gen_w4a16(m, n, k, bl=bl, seed=12, with_bias=False)
+    rng = np.random.default_rng(13)
+    C = rng.uniform(-5, 5, size=(m, n)).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, size=n).astype(np.float32)
+    got = T.oracle_w4a16_f32(d["A16"], d["Bp"], d["S16"], bl, C, bias, -np.inf, np.inf)
+    A = T.bits_f16(d["A16"]).astype(np.float64)
+    q = np.empty((n, k))
+    q[:, 0::2] = (d["Bp"] & 15) - 8.0
+    q[:, 1::2] = (d["Bp"] >> 4) - 8.0
+    W = q * np.repeat(T.bits_f16(d["S16"]).astype(np.float64), bl, axis=1)
+    exact = A @ W.T + C + bias
+    S = np.abs(A) @ np.abs(W).T + np.abs(C) + np.abs(bias)
+    assert np.all(np.abs(got - exact) <= (2 * k + 4) * 2.0 ** -24 * S)
+    assert np.abs(got - exact).max() > 0  # the f32 loop does round
+
+
 def test_w4a16_rvv_numerics_within_reference_tolerance():
     """The RVV-numerics restatement (f16 weights, f16 FMA chain) stays within the reference
     test's own tolerance (abs 1.0, cosine 0.9999) of the f32 oracle on the reference inputs."""

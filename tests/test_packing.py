@@ -40,6 +40,10 @@ REF_FUNCS = {
                "get_scale_b_offset", "get_c_offset", "get_bias_offset", "get_d_offset",
                "get_d_size", "get_a_packed_size", "get_b_packed_size", "run_a_pack",
                "run_bt_pack", "run"],
+    "w4a16fp": ["get_m_step", "get_n_step", "get_a_packed_offset", "get_b_packed_offset",
+                "get_scale_b_offset", "get_c_offset", "get_bias_offset", "get_d_offset",
+                "get_d_size", "get_a_packed_size", "get_b_packed_size", "run_a_pack",
+                "run_bt_pack", "run"],
     "igemmclp": ["get_m_step", "get_n_step", "get_b_packed_offset", "get_c_offset",
                  "get_bias_offset", "get_d_offset", "get_d_size", "get_b_packed_size",
                  "run_bt_pack", "run"],
@@ -143,6 +147,8 @@ OPERANDS = [
     ("w4a8p", "get_b_packed_offset", 0, 45, 512, "n", False),
     ("w4a16p", "get_a_packed_offset", 2, 70, 384, "m", False),
     ("w4a16p", "get_b_packed_offset", 0, 40, 384, "n", True),
+    ("w4a16fp", "get_a_packed_offset", 2, 70, 384, "m", False),
+    ("w4a16fp", "get_b_packed_offset", 0, 40, 384, "n", True),
     ("igemmclp", "get_b_packed_offset", 1, 200, 288, "n", False),
 ]
 
@@ -184,6 +190,14 @@ def test_packed_sizes_equal_unpacked_sizes(lib, mod):
     assert g("w8a8p", "get_d_size")(m, n) == m * n
     assert g("w4a8p", "get_d_size")(m, n) == 4 * m * n
     assert g("w4a16p", "get_d_size")(m, n) == 2 * m * n
+    assert g("w4a16fp", "get_a_packed_size")(m, k) == 2 * m * k
+    assert g("w4a16fp", "get_b_packed_size")(n, k) == n * k // 2
+    for kind in ("w4a16f", "w4a16fp"):
+        assert g(kind, "get_d_size")(m, n) == 4 * m * n
+        assert _getter(lib, sym(mod, kind, "get_c_offset"), 3)(32, 16, n) == 4 * (32 * n + 16)
+        assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(48) == 4 * 48
+        assert (_getter(lib, sym(mod, kind, "get_scale_b_offset"), 3)(16, 3, 128) ==
+                _getter(lib, sym(mod, "w4a16", "get_scale_b_offset"), 3)(16, 3, 128))
     for kind in ("w4a8h", "w4a8b", "w4a8hp", "w4a8bp"):
         assert g(kind, "get_d_size")(m, n) == 2 * m * n
         ms = _getter(lib, sym(mod, kind, "get_m_step"), 0)()
@@ -196,10 +210,10 @@ def test_packed_sizes_equal_unpacked_sizes(lib, mod):
 
 
 def test_packed_steps_via_interface_structs(lib, mod, shim):
-    out = (ctypes.c_size_t * 30)()
+    out = (ctypes.c_size_t * 34)()
     shim.tqts_steps_via_interfaces(out)
     kinds = (["clamp", "w8a8", "w4a8", "w4a16", "igemmcl"] + list(PACKED) +
-             ["w4a8h", "w4a8hp", "w4a8b", "w4a8bp"])
+             ["w4a8h", "w4a8hp", "w4a8b", "w4a8bp", "w4a16f", "w4a16fp"])
     for t, kind in enumerate(kinds):
         assert out[2 * t] == _getter(lib, sym(mod, kind, "get_m_step"), 0)()
         assert out[2 * t + 1] == _getter(lib, sym(mod, kind, "get_n_step"), 0)()

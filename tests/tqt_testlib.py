@@ -108,6 +108,9 @@ def oracle():
         "tqto_gemm_f16_qsi4c2t_f32acc": (None, [c_size] * 4 + [c_vp, c_size, c_vp, c_size, c_vp,
                                                  c_size, c_vp, c_size, c_vp, c_size, c_vp, u16,
                                                  u16]),
+        "tqto_gemm_f16_qsi4c2t_f32out": (None, [c_size] * 4 + [c_vp, c_size, c_vp, c_size, c_vp,
+                                                 c_size, c_vp, c_size, c_vp, c_size, c_vp,
+                                                 ctypes.c_float, ctypes.c_float]),
         "tqto_gemm_f16_qsi4c2t_rvv": (None, [c_size] * 4 + [c_vp, c_size, c_vp, c_size, c_vp,
                                               c_size, c_vp, c_size, c_vp, c_size, c_vp, u16,
                                               u16]),
@@ -158,6 +161,9 @@ def ref():
         "tqtr_reference_gemm_qw_mixed_f16": (None, [c_size] * 4 + [c_vp, c_size, c_vp, c_size,
                                                      c_vp, c_size, c_vp, c_size, c_vp, c_size,
                                                      c_vp, u16, u16]),
+        "tqtr_reference_gemm_qw_mixed_f16_f32": (None, [c_size] * 4 + [
+            c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp, f32,
+            f32]),
         "tqtr_reference_conv_cl_f32": (None, [c_size, c_vp, c_vp, c_vp, c_vp,
                                                ctypes.POINTER(ConvParamsC), f32, f32]),
         "tqtr_im2col_cl_i8": (None, [c_size, c_vp, c_vp, ctypes.POINTER(ConvParamsC)]),
@@ -251,6 +257,19 @@ def oracle_w4a16(A16, Bp, S16, bl, C16, bias16, cmin_bits, cmax_bits, rvv=False)
     f = oracle().tqto_gemm_f16_qsi4c2t_rvv if rvv else oracle().tqto_gemm_f16_qsi4c2t_f32acc
     f(m, n, k, bl, ptr(A16), k, ptr(Bp), k, ptr(S16), k // bl, ptr(C16), n, ptr(D), n,
       ptr(bias16), cmin_bits, cmax_bits)
+    return D
+
+
+def oracle_w4a16_f32(A16, Bp, S16, bl, C, bias, cmin, cmax):
+    """W4A16 with f32 C, bias, clamp bounds and D (the f32-output type's oracle)."""
+    m, k = A16.shape
+    n = Bp.shape[0]
+    D = np.zeros((m, n), np.float32)
+    C = None if C is None else np.ascontiguousarray(C, np.float32)
+    bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    oracle().tqto_gemm_f16_qsi4c2t_f32out(m, n, k, bl, ptr(A16), k, ptr(Bp), k, ptr(S16), k // bl,
+                                          ptr(C), n, ptr(D), n, ptr(bias), float(cmin),
+                                          float(cmax))
     return D
 
 
@@ -366,7 +385,7 @@ def gen_igemmcl(ID, IH, IW, IC, OC, KH, KW, stride=(1, 1), pad=(0, 0), dil=(1, 1
 
 # chunk bytes per packed kernel type (one MFMA lane fragment for every type)
 PACK_CHUNK = {"clampp": 16, "w8a8pb": 16, "w8a8p": 16, "igemmclp": 16, "w4a8p": 16,
-              "w4a16p": 16}
+              "w4a16p": 16, "w4a16fp": 16}
 
 
 def frag_perm(kbytes):

@@ -14,12 +14,16 @@
 //   * v_mfma_f32_16x16x32_f16 contracts one scale block (all products exact in f32), and the
 //     block's f32 partial is scaled by the f32 value of its f16 scale and accumulated;
 //   * the eight waves' f32 partials are summed through LDS; C, bias and the clamp are applied
-//     in f32 and the result is rounded once to f16.
+//     in f32 and the result is stored once: rounded to f16 for the f16 types, as is for the
+//     f32-output types (gemm_1xnbias_clamp_f32_f16_qsi4c2t and its packed sibling, whose C and
+//     bias are f32 too).
 // A generic one-thread-per-output kernel covers every other shape with the reference test
 // oracle's exact operation order (reference test/common/reference_gemm.cpp:132-179).
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -41,11 +45,11 @@ struct W4A16Args
     long long bstride;  // bytes between weight rows
     const _Float16 *scale_b;
     long long ldsb;
-    const _Float16 *C;
+    const void *C;  // f16 or f32 (the output type)
     long long ldc;
-    _Float16 *D;
+    void *D;
     long long ldd;
-    const _Float16 *bias;
+    const void *bias;
     float cmin, cmax;
     int bl;
     PackDesc pa, pb;  // packed A / B of the p-variant (read when the kernel's PK bit is set)
@@ -124,7 +128,7 @@ __device__ __forceinline__ f16x8 permute_a(u32x4 v)
     return __builtin_bit_cast(f16x8, o);
 }
 
-template <int PK>
+template <int PK, int OUT>
 __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
 {
     __shared__ float s_part[2][kWaves][kMRows][kNTile];
@@ -246,14 +250,14 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
                     v += s_part[buf][w][orow][ocol];
                 }
                 if (a.C) {
-                    v += static_cast<float>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+                    v += load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
                 }
                 if (a.bias) {
-                    v += static_cast<float>(a.bias[gn]);
+                    v += load_out<OUT>(a.bias, gn);
                 }
                 v = fmaxf(v, a.cmin);
                 v = fminf(v, a.cmax);
-                a.D[static_cast<long long>(gm) * a.ldd + gn] = static_cast<_Float16>(v);
+                store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn, v);
             }
         }
         buf ^= 1;
@@ -296,7 +300,7 @@ __device__ __forceinline__ f16x8 unpack_q8_sgpr(uint32_t x, uint32_t magic)
     return out;
 }
 
-template <int K, int PK>
+template <int K, int PK, int OUT>
 __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
 {
     constexpr int BPW = K / 256;  // 32-k blocks per wave (8, 12 or 16)
@@ -416,14 +420,14 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
                 v += s_part[(w * kMRows + orow) * kNTile + ocol];
             }
             if (a.C) {
-                v += static_cast<float>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+                v += load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
             }
             if (a.bias) {
-                v += static_cast<float>(a.bias[gn]);
+                v += load_out<OUT>(a.bias, gn);
             }
             v = fmaxf(v, a.cmin);
             v = fminf(v, a.cmax);
-            a.D[static_cast<long long>(gm) * a.ldd + gn] = static_cast<_Float16>(v);
+            store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn, v);
         }
         __syncthreads();  // s_part is rewritten by the next tile
     };
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
 
 // Generic path: the reference test oracle's operation order, one thread per output
 // (acc = C; acc += a * (f32(q - 8) * f32(s)) in k order without FMA; acc += bias; clamp).
-template <int PK>
+template <int PK, int OUT>
 __global__ __launch_bounds__(256) void w4a16_generic_kernel(W4A16Args a)
 {
     const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -452,7 +456,7 @@ __global__ __launch_bounds__(256) void w4a16_generic_kernel(W4A16Args a)
     const int gn = static_cast<int>(idx - static_cast<long long>(gm) * a.N);
     float acc = 0.f;
     if (a.C) {
-        acc = static_cast<float>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+        acc = load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
     }
     const _Float16 *arow = a.A + static_cast<long long>(gm) * a.lda;
     const uint8_t *brow = a.B + static_cast<long long>(gn) * a.bstride;
@@ -473,11 +477,11 @@ __global__ __launch_bounds__(256) void w4a16_generic_kernel(W4A16Args a)
         acc = __fadd_rn(acc, __fmul_rn(static_cast<float>(av), bd));
     }
     if (a.bias) {
-        acc = __fadd_rn(acc, static_cast<float>(a.bias[gn]));
+        acc = __fadd_rn(acc, load_out<OUT>(a.bias, gn));
     }
     acc = (acc < a.cmin) ? a.cmin : acc;
     acc = (a.cmax < acc) ? a.cmax : acc;
-    a.D[static_cast<long long>(gm) * a.ldd + gn] = static_cast<_Float16>(acc);
+    store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn, acc);
 }
 
 int device_cu_count()
@@ -489,13 +493,14 @@ int device_cu_count()
     return cus > 0 ? cus : 1;
 }
 
-// Shared body of the W4A16 runs. `packed`: A (f16 rows) and B (int4 rows, fragment-ordered)
-// are in the packed layout; k_idx_a / k_idx_b apply the packers' tail rule.
+// Shared body of the W4A16 runs. OUT: OUT_F16 (C, bias, D f16) or OUT_F32 (C, bias, D f32);
+// the clamp bounds arrive widened to f32. `packed`: A (f16 rows) and B (int4 rows,
+// fragment-ordered) are in the packed layout; k_idx_a / k_idx_b apply the packers' tail rule.
+template <int OUT>
 void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda,
                size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b, const void *scale_b,
                size_t ldsb, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
-               float16_t clamp_min, float16_t clamp_max, bool packed, hipStream_t s,
-               const char *where)
+               float clamp_min, float clamp_max, bool packed, hipStream_t s, const char *where)
 {
     if (m == 0 || n == 0) {
         return;
@@ -517,13 +522,13 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
     a.bstride = static_cast<long long>(ldb / 2);
     a.scale_b = static_cast<const _Float16 *>(scale_b);
     a.ldsb = static_cast<long long>(ldsb);
-    a.C = static_cast<const _Float16 *>(C);
+    a.C = C;
     a.ldc = static_cast<long long>(ldc);
-    a.D = static_cast<_Float16 *>(D);
+    a.D = D;
     a.ldd = static_cast<long long>(ldd);
-    a.bias = static_cast<const _Float16 *>(bias);
-    a.cmin = static_cast<float>(clamp_min);
-    a.cmax = static_cast<float>(clamp_max);
+    a.bias = bias;
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
     a.bl = static_cast<int>(bl);
     bool layout_fast;
     if (packed) {
@@ -553,19 +558,19 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
         const int nw = static_cast<int>(nwg);
         if (packed) {
             if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_AB>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_AB, OUT>), grid, dim3(512), 0, s, a, nw);
             } else if (k == 3072) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_AB>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_AB, OUT>), grid, dim3(512), 0, s, a, nw);
             } else {
-                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_AB>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_AB, OUT>), grid, dim3(512), 0, s, a, nw);
             }
         } else {
             if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_NONE>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_NONE, OUT>), grid, dim3(512), 0, s, a, nw);
             } else if (k == 3072) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_NONE>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_NONE, OUT>), grid, dim3(512), 0, s, a, nw);
             } else {
-                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_NONE>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_NONE, OUT>), grid, dim3(512), 0, s, a, nw);
             }
         }
     } else if (fast) {
@@ -575,9 +580,9 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
         TQT_REQUIRE(gy < 65536, "m too large");
         const dim3 grid(gx, static_cast<unsigned>(gy));
         if (packed) {
-            hipLaunchKernelGGL(w4a16_mfma_kernel<PK_AB>, grid, dim3(512), 0, s, a);
+            hipLaunchKernelGGL((w4a16_mfma_kernel<PK_AB, OUT>), grid, dim3(512), 0, s, a);
         } else {
-            hipLaunchKernelGGL(w4a16_mfma_kernel<PK_NONE>, grid, dim3(512), 0, s, a);
+            hipLaunchKernelGGL((w4a16_mfma_kernel<PK_NONE, OUT>), grid, dim3(512), 0, s, a);
         }
     } else {
         const long long total = static_cast<long long>(m) * static_cast<long long>(n);
@@ -585,9 +590,9 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
         TQT_REQUIRE(blocks < (1ll << 31), "grid too large");
         const dim3 grid(static_cast<unsigned>(blocks));
         if (packed) {
-            hipLaunchKernelGGL(w4a16_generic_kernel<PK_AB>, grid, dim3(256), 0, s, a);
+            hipLaunchKernelGGL((w4a16_generic_kernel<PK_AB, OUT>), grid, dim3(256), 0, s, a);
         } else {
-            hipLaunchKernelGGL(w4a16_generic_kernel<PK_NONE>, grid, dim3(256), 0, s, a);
+            hipLaunchKernelGGL((w4a16_generic_kernel<PK_NONE, OUT>), grid, dim3(256), 0, s, a);
         }
     }
     check_launch(where);
@@ -664,8 +669,9 @@ void tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950_async(
     size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min, float16_t clamp_max,
     void *stream)
 {
-    w4a16_run(m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd, bias,
-              clamp_min, clamp_max, false, as_stream(stream),
+    w4a16_run<OUT_F16>(m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D,
+                       ldd, bias, static_cast<float>(clamp_min), static_cast<float>(clamp_max),
+                       false, as_stream(stream),
               "tqt_run_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950");
 }
 
@@ -691,8 +697,9 @@ void tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950_async(
     const void *C, size_t ldc, void *D, size_t ldd, const void *bias, float16_t clamp_min,
     float16_t clamp_max, void *stream)
 {
-    w4a16_run(m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb, C, ldc,
-              D, ldd, bias, clamp_min, clamp_max, true, as_stream(stream),
+    w4a16_run<OUT_F16>(m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb,
+                       C, ldc, D, ldd, bias, static_cast<float>(clamp_min),
+                       static_cast<float>(clamp_max), true, as_stream(stream),
               "tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
 }
 
@@ -709,6 +716,112 @@ void tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(
         m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd,
         bias, clamp_min, clamp_max, nullptr);
     finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
+}
+
+// gemm_1xnbias_clamp_f32_f16_qsi4c2t (reference …f32_f16_qsi4c2t_8x2vl_rvv.cpp): the W4A16
+// kernels with f32 C, bias, clamp bounds and D. The result is the f32 value of the reference
+// test's oracle for this type (reference_gemm_quantized_weight_mixed<float16_t, float>), never
+// rounded to f16.
+size_t tqt_get_m_step_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(void)
+{
+    return kW4A16MStep;
+}
+size_t tqt_get_n_step_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(void)
+{
+    return kW4A16NStep;
+}
+size_t tqt_get_a_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(size_t m_idx, size_t k_idx,
+                                                                       size_t lda, size_t bl)
+{
+    return tqt_get_a_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(m_idx, k_idx, lda, bl);
+}
+size_t tqt_get_b_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(size_t n_idx, size_t k_idx,
+                                                                       size_t ldb, size_t bl)
+{
+    return tqt_get_b_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(n_idx, k_idx, ldb, bl);
+}
+size_t tqt_get_scale_b_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(size_t n_idx,
+                                                                             size_t b_idx,
+                                                                             size_t ldsb)
+{
+    return tqt_get_scale_b_offset_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(n_idx, b_idx,
+                                                                                 ldsb);
+}
+size_t tqt_get_c_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(size_t m_idx, size_t n_idx,
+                                                                       size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kW4A16MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(float);
+}
+size_t tqt_get_bias_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(size_t n_idx)
+{
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    return n_idx * sizeof(float);
+}
+size_t tqt_get_d_offset_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(size_t m_idx, size_t n_idx,
+                                                                       size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kW4A16MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kW4A16NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(float);
+}
+size_t tqt_get_d_size_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(float);
+}
+
+void tqt_run_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda, size_t k_idx_a,
+    const void *B, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb, const void *C,
+    size_t ldc, void *D, size_t ldd, const void *bias, float clamp_min, float clamp_max,
+    void *stream)
+{
+    w4a16_run<OUT_F32>(m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D,
+                       ldd, bias, clamp_min, clamp_max, false, as_stream(stream),
+                       "tqt_run_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950(
+    size_t m, size_t n, size_t k, size_t bl, const void *A, size_t lda, size_t k_idx_a,
+    const void *B, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb, const void *C,
+    size_t ldc, void *D, size_t ldd, const void *bias, float clamp_min, float clamp_max)
+{
+    if (m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950_async(
+        m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd, bias,
+        clamp_min, clamp_max, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950");
+}
+
+// gemm_1xnbias_clamp_f32_f16p_qsi4c2p (reference …f32_f16p_qsi4c2p_8x2vl_rvv.cpp; geometry
+// getters and packers in packing.hip).
+void tqt_run_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, size_t bl, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb,
+    const void *C, size_t ldc, void *D, size_t ldd, const void *bias, float clamp_min,
+    float clamp_max, void *stream)
+{
+    w4a16_run<OUT_F32>(m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb,
+                       C, ldc, D, ldd, bias, clamp_min, clamp_max, true, as_stream(stream),
+                       "tqt_run_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(
+    size_t m, size_t n, size_t k, size_t bl, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *scale_b, size_t ldsb,
+    const void *C, size_t ldc, void *D, size_t ldd, const void *bias, float clamp_min,
+    float clamp_max)
+{
+    if (m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950_async(
+        m, n, k, bl, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, scale_b, ldsb, C, ldc, D, ldd,
+        bias, clamp_min, clamp_max, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950");
 }
 
 }  // extern "C"

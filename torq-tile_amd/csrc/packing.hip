@@ -1,7 +1,9 @@
 // Packers and geometry getters of the packed (p) kernel types on gfx950:
 //   gemm_clamp_i32_i8p_i8p, gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp,
 //   gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp, gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp,
-//   gemm_1xnbias_clamp_f16_f16p_qsi4c2p, igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp.
+//   gemm_1xnbias_clamp_f16_f16p_qsi4c2p, igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp,
+//   and the output-type siblings gemm_1xnbias_clamp_{f16,bf16}_qai8dxp_qsi4cxp and
+//   gemm_1xnbias_clamp_f32_f16p_qsi4c2p (same layouts as the types they share a mainloop with).
 // Their run functions live beside the mainloops they share (int8_mfma.hip, gemm_i8_i4.hip,
 // gemm_f16_i4.hip). The layout (PackDesc, pack_offset) is defined in tqt_hip_common.hpp; the
 // reference's packers are the permutations of tqt_gemm_pack_rvv.h:354-398, 542-567, 740-856.
@@ -11,6 +13,7 @@
 // 16 bytes, so a piece never straddles two chunks and its bytes are contiguous in the output.
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
@@ -583,6 +586,99 @@ void tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(
 {
     pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, kPackW4A16Chunk, 0, true, B, B_packed, nullptr, true,
             "tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
+}
+
+// =============================================================================================
+// gemm_1xnbias_clamp_f32_f16p_qsi4c2p (reference …f32_f16p_qsi4c2p_8x2vl_rvv.cpp): the packed
+// layout and packers of the f16 type; C, bias and D are f32.
+// =============================================================================================
+size_t tqt_get_m_step_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(void)
+{
+    return kPackW4A16MStep;
+}
+size_t tqt_get_n_step_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(void)
+{
+    return kPackW4A16NStep;
+}
+size_t tqt_get_a_packed_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t m_idx,
+                                                                               size_t k_idx,
+                                                                               size_t lda,
+                                                                               size_t actual_m)
+{
+    return tqt_get_a_packed_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(m_idx, k_idx,
+                                                                                   lda, actual_m);
+}
+size_t tqt_get_b_packed_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t n_idx,
+                                                                               size_t k_idx,
+                                                                               size_t ldb,
+                                                                               size_t actual_n)
+{
+    return tqt_get_b_packed_offset_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(n_idx, k_idx,
+                                                                                   ldb, actual_n);
+}
+size_t tqt_get_scale_b_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t n_idx,
+                                                                              size_t b_idx,
+                                                                              size_t ldsb)
+{
+    TQT_REQ_N(kPackW4A16NStep);
+    return (n_idx * ldsb + b_idx) * sizeof(uint16_t);
+}
+size_t tqt_get_c_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t m_idx, size_t n_idx,
+                                                                        size_t ldc)
+{
+    TQT_REQ_M(kPackW4A16MStep);
+    TQT_REQ_N(kPackW4A16NStep);
+    return (m_idx * ldc + n_idx) * sizeof(float);
+}
+size_t tqt_get_bias_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t n_idx)
+{
+    TQT_REQ_N(kPackW4A16NStep);
+    return n_idx * sizeof(float);
+}
+size_t tqt_get_d_offset_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t m_idx, size_t n_idx,
+                                                                        size_t ldd)
+{
+    TQT_REQ_M(kPackW4A16MStep);
+    TQT_REQ_N(kPackW4A16NStep);
+    return (m_idx * ldd + n_idx) * sizeof(float);
+}
+size_t tqt_get_d_size_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(float);
+}
+size_t tqt_get_a_packed_size_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t m, size_t k)
+{
+    return m * k * sizeof(uint16_t);
+}
+size_t tqt_get_b_packed_size_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(size_t n, size_t k)
+{
+    return n * k / 2;
+}
+void tqt_run_a_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950_async(
+    size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed,
+    void *stream)
+{
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A16MStep, kPackW4A16Chunk, 2, false, A, A_packed, stream, false,
+            "tqt_run_a_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950");
+}
+void tqt_run_a_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(
+    size_t m, size_t k, size_t lda, size_t lda_packed, size_t k_idx, const void *A, void *A_packed)
+{
+    pack_nk(m, k, lda, lda_packed, k_idx, kPackW4A16MStep, kPackW4A16Chunk, 2, false, A, A_packed, nullptr, true,
+            "tqt_run_a_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950");
+}
+void tqt_run_bt_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950_async(
+    size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed,
+    void *stream)
+{
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, kPackW4A16Chunk, 0, true, B, B_packed, stream, false,
+            "tqt_run_bt_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950");
+}
+void tqt_run_bt_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950(
+    size_t n, size_t k, size_t ldb, size_t ldb_packed, size_t k_idx, const void *B, void *B_packed)
+{
+    pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, kPackW4A16Chunk, 0, true, B, B_packed, nullptr, true,
+            "tqt_run_bt_pack_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950");
 }
 
 // =============================================================================================

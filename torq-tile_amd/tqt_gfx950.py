@@ -37,6 +37,9 @@ KERNELS = {
     "w4a8b": "gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt",
     "w4a8hp": "gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp",
     "w4a8bp": "gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp",
+    # f32-output siblings of the W4A16 types: f32 C, bias, clamp bounds and D
+    "w4a16f": "gemm_1xnbias_clamp_f32_f16_qsi4c2t",
+    "w4a16fp": "gemm_1xnbias_clamp_f32_f16p_qsi4c2p",
 }
 
 
@@ -236,6 +239,14 @@ for _kind in ("w4a8hp", "w4a8bp"):
     _SIGS[_kind] = _packed_sigs(
         "w4a8", ["run_a_pack", "run_bt_pack"], None,
         ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_W4A16F_RUN = ([c_size] * 4 + [c_vp, c_size, c_size] * 2 +
+               [c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp, ctypes.c_float, ctypes.c_float])
+_SIGS["w4a16f"] = dict(_SIGS["w4a16"], run=(None, _W4A16F_RUN),
+                       run_async=(None, _W4A16F_RUN + [c_vp]))
+_SIGS["w4a16fp"] = _packed_sigs(
+    "w4a16", ["run_a_pack", "run_bt_pack"], _W4A16F_RUN,
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SIGS["w4a16fp"]["get_scale_b_offset"] = (c_size, [c_size] * 3)
 _SHIM_RUNS = ("w4a16", "w4a16p", "w4a8h", "w4a8b", "w4a8hp", "w4a8bp")
 
 
