@@ -5,6 +5,7 @@
  * built against the reference headers passes the same bytes:
  *   - struct tqt_qai8_qai8_qsi8cx_params  : reference src/gemm/gemm_i8_i8/tqt_params_i8_i8.h:16-24
  *   - struct tqt_qai8dx_qsi4cx_params     : reference src/gemm/gemm_i8_i4/tqt_params_i8_i4.h:23-28
+ *   - struct tqt_qai8dxp_qsi8cxp_params   : reference src/gemm/gemm_i8_i8/tqt_params_i8_i8.h:45-50
  *   - struct tqt_conv_params              : reference src/common/tqt_conv.h:20-31
  *   - float16_t, bfloat16_t               : reference src/common/tqt_common.h:27-28
  *
@@ -59,6 +60,16 @@ struct tqt_qai8dx_qsi4cx_params
     const float *scale_a;
     const int32_t *zero_point_a;
     const float *scale_b;
+};
+
+/* Quantization parameters for qai8dx (A, per-row asymmetric int8) x qsi8cx (B, per-channel
+ * symmetric int8) -> f32 / f16 D, plain and packed. scale_a/zero_point_a have m entries,
+ * scale_b has n entries. */
+struct tqt_qai8dxp_qsi8cxp_params
+{
+    float *scale_a;
+    int32_t *zero_point_a;
+    float *scale_b;
 };
 
 /* 3D convolution geometry (1D/2D set the higher dims to 1). The batch of an NDHWC input

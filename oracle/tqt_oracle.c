@@ -591,6 +591,132 @@ static uint16_t f16_add(uint16_t a, uint16_t b)
     return f64_to_f16((double)tqto_f16_to_f32(a) + (double)tqto_f16_to_f32(b));
 }
 
+uint16_t tqto_f16_add(uint16_t a, uint16_t b)
+{
+    return f16_add(a, b);
+}
+
+/* ------------------------------------------------------------------------------------------
+ * W8A8 with dynamic per-row activation quantization (qai8dx x qsi8cx -> f32 / f16):
+ * src/gemm/gemm_i8_i8/tqt_kernel_gemm_qai8dx_qsi8cx_4x1vl_rvv.h
+ * ---------------------------------------------------------------------------------------- */
+
+/* RISC-V vfmax / vfmin (IEEE 754-2019 maximumNumber / minimumNumber): a NaN operand yields the
+ * other one (the canonical NaN 0x7fc00000 if both are NaN), and -0 orders below +0. */
+static float canonical_nan_f32(void)
+{
+    const uint32_t u = 0x7fc00000u;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static float rv_fmax(float a, float b)
+{
+    if (a != a) {
+        return b != b ? canonical_nan_f32() : b;
+    }
+    if (b != b) {
+        return a;
+    }
+    if (a == b) {
+        return signbit(a) ? b : a;
+    }
+    return a > b ? a : b;
+}
+
+static float rv_fmin(float a, float b)
+{
+    if (a != a) {
+        return b != b ? canonical_nan_f32() : b;
+    }
+    if (b != b) {
+        return a;
+    }
+    if (a == b) {
+        return signbit(a) ? a : b;
+    }
+    return a < b ? a : b;
+}
+
+/* The k loop (vwmacc_zp :95-140): each A byte is loaded, zero_point_a is subtracted in a
+ * scalar register, and vwmacc.vx at SEW=16 uses the low 16 bits of that difference, so
+ * acc = sum_k int16(q_a - zp_a) * q_b, accumulated in int32 with wrap-around. */
+static int32_t dyn_acc(const int8_t *arow, const int8_t *brow, size_t k, int32_t zp)
+{
+    uint32_t acc = 0;
+    for (size_t p = 0; p < k; ++p) {
+        const uint32_t d = (uint32_t)((int32_t)arow[p]) - (uint32_t)zp;
+        const int32_t a16 = (int32_t)(int16_t)(uint16_t)(d & 0xffffu);
+        acc += (uint32_t)(a16 * (int32_t)brow[p]);
+    }
+    return (int32_t)acc;
+}
+
+void tqto_gemm_qai8dx_qsi8cxt_f32(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                  const int8_t *B, size_t ldb, float *D, size_t ldd,
+                                  const float *bias, float cmin, float cmax,
+                                  const float *scale_a, const int32_t *zero_point_a,
+                                  const float *scale_b)
+{
+    /* dequant_fp32 :145-215: vfcvt.f.x (RNE), sigma = scale_b * scale_a, f * sigma, + bias
+     * (a zero vector when bias is NULL), vfmax cmin, vfmin cmax. */
+    TILE_LOOP_BEGIN(m, n)
+    for (size_t i = m0; i < m0 + mr; ++i) {
+        for (size_t j = n0; j < n0 + nr; ++j) {
+            const int32_t acc = dyn_acc(A + i * lda, B + j * ldb, k, zero_point_a[i]);
+            const float sigma = scale_b[j] * scale_a[i];
+            float f = (float)acc * sigma;
+            f = f + (bias ? bias[j] : 0.0f);
+            f = rv_fmax(f, cmin);
+            f = rv_fmin(f, cmax);
+            D[i * ldd + j] = f;
+        }
+    }
+    TILE_LOOP_END
+}
+
+/* -0 orders below +0 and a NaN operand yields the other, on binary16 patterns. */
+static uint16_t rv_hmax(uint16_t a, uint16_t b)
+{
+    return tqto_f32_to_f16(rv_fmax(tqto_f16_to_f32(a), tqto_f16_to_f32(b)));
+}
+
+static uint16_t rv_hmin(uint16_t a, uint16_t b)
+{
+    return tqto_f32_to_f16(rv_fmin(tqto_f16_to_f32(a), tqto_f16_to_f32(b)));
+}
+
+static uint16_t canon_f16(uint16_t h)
+{
+    return ((h & 0x7fffu) > 0x7c00u) ? (uint16_t)0x7e00u : h;
+}
+
+void tqto_gemm_qai8dx_qsi8cxt_f16(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                  const int8_t *B, size_t ldb, uint16_t *D, size_t ldd,
+                                  const uint16_t *bias, uint16_t cmin, uint16_t cmax,
+                                  const float *scale_a, const int32_t *zero_point_a,
+                                  const float *scale_b)
+{
+    /* dequant_fp16 :217-330: the f32 product f32(acc) * sigma is narrowed to f16 (vfncvt.f.f.w,
+     * RNE), the f16 bias (or a zero vector) is added in f16 (one rounding), then vfmax / vfmin
+     * with the f16 bounds. RISC-V arithmetic returns the canonical NaN 0x7e00. */
+    TILE_LOOP_BEGIN(m, n)
+    for (size_t i = m0; i < m0 + mr; ++i) {
+        for (size_t j = n0; j < n0 + nr; ++j) {
+            const int32_t acc = dyn_acc(A + i * lda, B + j * ldb, k, zero_point_a[i]);
+            const float sigma = scale_b[j] * scale_a[i];
+            const float f = (float)acc * sigma;
+            uint16_t h = canon_f16(tqto_f32_to_f16(f));
+            h = canon_f16(f16_add(h, bias ? bias[j] : (uint16_t)0));
+            h = canon_f16(rv_hmax(h, cmin));
+            h = canon_f16(rv_hmin(h, cmax));
+            D[i * ldd + j] = h;
+        }
+    }
+    TILE_LOOP_END
+}
+
 void tqto_gemm_f16_qsi4c2t_rvv(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,
                                size_t lda, const uint8_t *B, size_t ldb, const uint16_t *scale_b,
                                size_t ldsb, const uint16_t *C, size_t ldc, uint16_t *D,

@@ -94,6 +94,24 @@ void tqto_gemm_f16_qsi4c2t_f32out(size_t m, size_t n, size_t k, size_t bl, const
                                   const uint16_t *scale_b, size_t ldsb, const float *C, size_t ldc,
                                   float *D, size_t ldd, const float *bias, float cmin, float cmax);
 
+/* binary16 addition rounded once (nearest even), on bit patterns. */
+uint16_t tqto_f16_add(uint16_t a, uint16_t b);
+
+/* W8A8 with per-row dynamically quantized A (scale_a[m], zero_point_a[m]) and per-channel
+ * symmetric B [n, k] (scale_b[n]), f32 or f16 D (tqt_kernel_gemm_qai8dx_qsi8cx_4x1vl_rvv.h:
+ * vwmacc_zp :95-140, dequant_fp32 :145-215, dequant_fp16 :217-330). C is not an input (the
+ * reference ignores it). */
+void tqto_gemm_qai8dx_qsi8cxt_f32(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                  const int8_t *B, size_t ldb, float *D, size_t ldd,
+                                  const float *bias, float cmin, float cmax,
+                                  const float *scale_a, const int32_t *zero_point_a,
+                                  const float *scale_b);
+void tqto_gemm_qai8dx_qsi8cxt_f16(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                                  const int8_t *B, size_t ldb, uint16_t *D, size_t ldd,
+                                  const uint16_t *bias, uint16_t cmin, uint16_t cmax,
+                                  const float *scale_a, const int32_t *zero_point_a,
+                                  const float *scale_b);
+
 /* W4A16 with the RVV kernel's own numerics (tqt_kernel_gemm_f16_i4_8x2vl_rvv.h:99-717):
  * f16-rounded dequantized weight, sequential f16 FMA over k, f16 bias add, f16 clamp. */
 void tqto_gemm_f16_qsi4c2t_rvv(size_t m, size_t n, size_t k, size_t bl, const uint16_t *A,

@@ -30,6 +30,14 @@
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_interface.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_interface.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_f16_qsi4c2t_interface.h"
 #include "tqt_gemm_1xnbias_clamp_f32_f16_qsi4c2t_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_interface.h"
@@ -277,12 +285,71 @@ static const struct tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_ukernel k_w4a16fp = 
     tqt_run_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950,
 };
 
+static const struct tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_ukernel k_w8dyn = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_ukernel k_w8dynp = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_b_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_ukernel k_w8dynh = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_a_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_b_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950,
+};
+
+static const struct tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_ukernel k_w8dynhp = {
+    tqt_get_m_step_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_n_step_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_c_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_bias_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_d_offset_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_d_size_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_a_pack_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_b_pack_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_bt_pack_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+    tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
+};
+
 /* m_step and n_step of each kernel type read through its interface struct:
  * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl, then the packed types
  * clamp_i32_i8p_i8p, qai8_qai8_qsi8cxp, qai8_qai8p_qsi8cxp, qai8dxp_qsi4cxp, f16p_qsi4c2p,
  * igemmcl qsi8cxp, then the W4A8 output siblings f16 qsi4cxt, f16 qsi4cxp, bf16 qsi4cxt,
- * bf16 qsi4cxp, then the W4A16 f32-output siblings qsi4c2t, qsi4c2p. */
-void tqts_steps_via_interfaces(size_t out[34])
+ * bf16 qsi4cxp, then the W4A16 f32-output siblings qsi4c2t, qsi4c2p, then the qai8dx x qsi8cx
+ * types f32 qsi8cxt, f32 qsi8cxp, f16 qsi8cxt, f16 qsi8cxp. */
+void tqts_steps_via_interfaces(size_t out[42])
 {
     out[0] = k_clamp.get_m_step();
     out[1] = k_clamp.get_n_step();
@@ -318,6 +385,14 @@ void tqts_steps_via_interfaces(size_t out[34])
     out[31] = k_w4a16f.get_n_step();
     out[32] = k_w4a16fp.get_m_step();
     out[33] = k_w4a16fp.get_n_step();
+    out[34] = k_w8dyn.get_m_step();
+    out[35] = k_w8dyn.get_n_step();
+    out[36] = k_w8dynp.get_m_step();
+    out[37] = k_w8dynp.get_n_step();
+    out[38] = k_w8dynh.get_m_step();
+    out[39] = k_w8dynh.get_n_step();
+    out[40] = k_w8dynhp.get_m_step();
+    out[41] = k_w8dynhp.get_n_step();
 }
 
 /* W4A16 run through the interface struct with _Float16 clamps given as binary16 bits. */
@@ -462,5 +537,55 @@ void tqts_run_w4a16f(int packed, size_t m, size_t n, size_t k, size_t bl, const 
     } else {
         k_w4a16f.run_gemm(m, n, k, bl, A, lda, k_idx_a, B, ldb, k_idx_b, scale_b, ldsb, C, ldc, D,
                           ldd, bias, cmin, cmax);
+    }
+}
+
+/* qai8dx x qsi8cx with f32 D (clamp bounds as floats) or f16 D (bounds as binary16 bits),
+ * plain or packed, through the interface struct; stream-ordered when stream != NULL. */
+void tqts_run_w8dyn(int f16, int packed, size_t m, size_t n, size_t k, const void *A, size_t lda,
+                    size_t k_idx_a, const void *B, size_t ldb, size_t k_idx_b, void *D,
+                    size_t ldd, const void *bias, float cmin, float cmax, uint16_t cmin_bits,
+                    uint16_t cmax_bits, const struct tqt_qai8dxp_qsi8cxp_params *params,
+                    void *stream)
+{
+    if (!f16) {
+        if (stream) {
+            if (packed) {
+                tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950_async(
+                    m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, cmin, cmax,
+                    params, stream);
+            } else {
+                tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950_async(
+                    m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, cmin, cmax,
+                    params, stream);
+            }
+        } else if (packed) {
+            k_w8dynp.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias,
+                              cmin, cmax, params);
+        } else {
+            k_w8dyn.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, cmin,
+                             cmax, params);
+        }
+        return;
+    }
+    float16_t hmin, hmax;
+    memcpy(&hmin, &cmin_bits, 2);
+    memcpy(&hmax, &cmax_bits, 2);
+    if (stream) {
+        if (packed) {
+            tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950_async(
+                m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, hmin, hmax,
+                params, stream);
+        } else {
+            tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950_async(
+                m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, hmin, hmax,
+                params, stream);
+        }
+    } else if (packed) {
+        k_w8dynhp.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, hmin,
+                           hmax, params);
+    } else {
+        k_w8dynh.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, hmin,
+                          hmax, params);
     }
 }

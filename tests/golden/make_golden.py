@@ -14,6 +14,10 @@ Fixtures (numpy .npz, no pickles):
   ref_clamp_i32.npz    reference_gemm_i32_i8 on the reference's int8 shape list
   ref_w4a16.npz        reference_gemm_quantized_weight_mixed<f16,f16> on its W4A16 shape list
   ref_w4a16_f32.npz    reference_gemm_quantized_weight_mixed<f16,float> on the same list
+  ref_w8a8dyn.npz      the qai8dx x qsi8cx runner's inputs on the reference's int8 shape list
+                       (A, B from its generator; per-row / per-channel quantization restated
+                       below, quantize_i8 from the reference) with reference_gemm<float,float>
+                       of the unquantized f32 operands, the value its test compares against
   ref_im2col.npz       tqt_im2col_cl<int8_t> on the reference's igemm shape list
   ref_qm.npz           tqt_quantize_multiplier on edge and random doubles
   ref_quant.npz        quantize_i8 / quantize_bias_i32 / fuse_zp_to_bias / quantize_fp16_to_int4
@@ -43,6 +47,30 @@ CONV_SHAPES = [  # IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, DH, DW
     (3, 16, 8, 8, 3, 3, 2, 2, 1, 1, 1, 1), (8, 16, 7, 11, 3, 5, 1, 1, 0, 0, 1, 1),
     (64, 128, 4, 4, 1, 1, 1, 1, 0, 0, 1, 1), (3, 32, 16, 16, 3, 3, 1, 1, 1, 1, 1, 1),
     (3, 8, 6, 6, 3, 3, 1, 1, 0, 0, 1, 1), (64, 32, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1)]
+
+
+def asym_quant_params_i8(x):
+    """test/common/quantized_gemm_test_runner.h:37-67 compute_asym_quant_params_i8 (float32
+    arithmetic; that header needs gtest, so it cannot be compiled here)."""
+    f32 = np.float32
+    fmax = max(f32(x.max()), f32(0.0))
+    fmin = min(f32(x.min()), f32(0.0))
+    scale = f32(f32(fmax - fmin) / f32(255.0))
+    if scale == 0:
+        return f32(1.0), 0
+    zp = int(np.rint(f32(f32(-128.0) - f32(fmin / scale))))
+    if zp == -128:
+        zp = -127
+    return scale, zp
+
+
+def sym_quant_params_i8(x):
+    """test/common/quantized_gemm_test_runner.h:69-85 compute_sym_quant_params_i8."""
+    f32 = np.float32
+    fmax, fmin = f32(x.max()), f32(x.min())
+    amax = abs(fmax) if abs(fmax) >= abs(fmin) else abs(fmin)
+    scale = f32(f32(f32(2.0) * amax) / f32(255.0))
+    return f32(1.0) if scale == 0 else scale
 
 
 def main():
@@ -110,6 +138,35 @@ def main():
         out["w4a16_%d_D" % i] = D
     np.savez_compressed(os.path.join(HERE, "ref_w4a16.npz"),
                         shapes=np.array(W4A16_SHAPES, np.int64), **out)
+
+    # --- W8A8 with dynamic A quantization, f32 / f16 D
+    # (test/common/quantized_gemm_test_runner.h:1325-1425) ---
+    out = {}
+    for i, (m, n, k, _c) in enumerate(INT8_SHAPES):
+        AB = np.zeros(m * k + n * k, np.float32)
+        r.tqtr_fill_uniform_f32(-1.0, 1.0, 42, p(AB), 1, AB.size)
+        Af = AB[:m * k].reshape(m, k).copy()
+        Bf = AB[m * k:].reshape(n, k).copy()
+        bias = np.zeros(n, np.float32)
+        r.tqtr_fill_uniform_f32(-10.0, 10.0, 123, p(bias), 1, n)
+        sa = np.zeros(m, np.float32)
+        za = np.zeros(m, np.int32)
+        for row in range(m):
+            sa[row], za[row] = asym_quant_params_i8(Af[row])
+        sb = np.array([sym_quant_params_i8(Bf[ch]) for ch in range(n)], np.float32)
+        Aq = np.array([[r.tqtr_quantize_i8(float(v), float(sa[row]), int(za[row]))
+                        for v in Af[row]] for row in range(m)], np.int8)
+        Bq = np.array([[r.tqtr_quantize_i8(float(v), float(sb[ch]), 0) for v in Bf[ch]]
+                       for ch in range(n)], np.int8)
+        D = np.zeros((m, n), np.float32)
+        flt_max = float(np.finfo(np.float32).max)
+        r.tqtr_reference_gemm_f32(m, n, k, p(Af), k, p(Bf), k, 1, None, n, p(D), n, p(bias),
+                                  -flt_max, flt_max)
+        for key, v in (("A", Aq), ("B", Bq), ("scale_a", sa), ("zp_a", za), ("scale_b", sb),
+                       ("bias", bias), ("Dref", D)):
+            out["w8a8dyn_%d_%s" % (i, key)] = v
+    np.savez_compressed(os.path.join(HERE, "ref_w8a8dyn.npz"),
+                        shapes=np.array(INT8_SHAPES, np.int64), **out)
 
     # --- W4A16 with f32 C / bias / clamp / D (the same runner with TD = float; its
     # UniformRandomGenerator<float> draws C and bias, the clamp defaults to +-FLT_MAX) ---

@@ -269,6 +269,105 @@ def test_w4a16_f32out_closed_form():
     assert np.abs(got - exact).max() > 0  # the f32 loop does round
 
 
+def test_f16_add_is_correctly_rounded():
+    """binary16 addition: the exact float64 sum rounded once by numpy's float64 -> float16
+    conversion, over random normal, subnormal, huge and special patterns."""
+    o = T.oracle()
+    rng = np.random.default_rng(31)
+    a = rng.integers(0, 65536, 6000).astype(np.uint16)
+    b = rng.integers(0, 65536, 6000).astype(np.uint16)
+    b[:2000] = (a[:2000] ^ rng.integers(0, 64, 2000).astype(np.uint16))  # close magnitudes
+    got = np.array([o.tqto_f16_add(int(x), int(y)) for x, y in zip(a, b)], np.uint16)
+    with np.errstate(all="ignore"):
+        exp = (T.bits_f16(a).astype(np.float64) + T.bits_f16(b).astype(np.float64))
+        exp = exp.astype(np.float16).view(np.uint16)
+    nan = np.isnan(T.bits_f16(exp))
+    assert np.array_equal(got[~nan], exp[~nan])
+    assert np.all(np.isnan(T.bits_f16(got[nan])))
+
+
+def _dyn_golden():
+    g = golden("ref_w8a8dyn.npz")
+    for i, (m, n, k, _c) in enumerate(g["shapes"]):
+        pre = "w8a8dyn_%d_" % i
+        yield {key: g[pre + key] for key in ("A", "B", "scale_a", "zp_a", "scale_b", "bias",
+                                             "Dref")}
+
+
+def test_w8a8dyn_within_reference_tolerance():
+    """The dynamic-quantization oracle, on the reference runner's own inputs, passes the
+    reference test's own check against reference_gemm<float> of the unquantized operands
+    (quantized_gemm_test_runner.h:1414-1423: abs 1.5 / cosine 0.998 for f32, 2.5 / 0.997 for
+    f16, bounds +-FLT_MAX converted to the output type)."""
+    for d in _dyn_golden():
+        ref = d["Dref"].astype(np.float64)
+        for f16 in (False, True):
+            if f16:
+                got = T.oracle_w8a8dyn(d["A"], d["B"], T.f16_bits(d["bias"]), 0xFC00, 0x7C00,
+                                       d["scale_a"], d["zp_a"], d["scale_b"], f16=True)
+                got = T.bits_f16(got).astype(np.float64)
+                tol, cos_min = 2.5, 0.997
+            else:
+                fm = float(np.finfo(np.float32).max)
+                got = T.oracle_w8a8dyn(d["A"], d["B"], d["bias"], -fm, fm, d["scale_a"],
+                                       d["zp_a"], d["scale_b"]).astype(np.float64)
+                tol, cos_min = 1.5, 0.998
+            assert np.abs(got - ref).max() <= tol
+            cos = (got * ref).sum() / (np.linalg.norm(got) * np.linalg.norm(ref) + 1e-30)
+            assert cos >= cos_min
+
+
+def test_w8a8dyn_closed_form():
+    """Independent evaluation: the int32 accumulator from an int64 matrix product of
+    (A - zp_a) and B, then the f32 epilogue steps in numpy float32 (each rounded: f32(acc),
+    sigma = sb * sa, product, + bias, clamp); and the f16 output as numpy's f16 rounding of that
+    product, an exactly rounded f16 bias add, and the f16 clamp."""
+    d = T.gen_w8a8dyn(7, 45, 300, seed=3)
+    A64 = d["A"].astype(np.int64) - d["zp_a"].astype(np.int64)[:, None]
+    acc = (A64 @ d["B"].astype(np.int64).T).astype(np.int32)
+    sigma = d["scale_b"][None, :] * d["scale_a"][:, None]
+    prod = acc.astype(np.float32) * sigma
+    f = np.minimum(np.maximum(prod + d["bias"][None, :], np.float32(-40.0)), np.float32(35.0))
+    got = T.oracle_w8a8dyn(d["A"], d["B"], d["bias"], -40.0, 35.0, d["scale_a"], d["zp_a"],
+                           d["scale_b"])
+    np.testing.assert_array_equal(got.view(np.uint32), f.view(np.uint32))
+    b16 = T.f16_bits(d["bias"])
+    h = prod.astype(np.float16).astype(np.float64) + T.bits_f16(b16).astype(np.float64)[None, :]
+    h = np.minimum(np.maximum(h.astype(np.float16), np.float16(-40.0)), np.float16(35.0))
+    got16 = T.oracle_w8a8dyn(d["A"], d["B"], b16, int(T.f16_bits(-40.0)),
+                             int(T.f16_bits(35.0)), d["scale_a"], d["zp_a"], d["scale_b"],
+                             f16=True)
+    np.testing.assert_array_equal(got16, h.view(np.uint16))
+
+
+def test_w8a8dyn_zero_point_shift_invariance():
+    """Moving a row's int8 values and its zero point by the same c leaves every output bit
+    unchanged (the correction enters as q_a - zp_a); a sign error in the correction fails."""
+    d = T.gen_w8a8dyn(5, 30, 200, seed=4, zp_range=(-20, 20))
+    A = np.clip(d["A"], -100, 100).astype(np.int8)
+    base = T.oracle_w8a8dyn(A, d["B"], d["bias"], -np.inf, np.inf, d["scale_a"], d["zp_a"],
+                            d["scale_b"])
+    for c in (-27, 13):
+        got = T.oracle_w8a8dyn((A.astype(np.int32) + c).astype(np.int8), d["B"], d["bias"],
+                               -np.inf, np.inf, d["scale_a"], d["zp_a"] + c, d["scale_b"])
+        np.testing.assert_array_equal(got.view(np.uint32), base.view(np.uint32))
+
+
+def test_w8a8dyn_sixteen_bit_difference_and_signed_zero():
+    """Hand-worked cases of the RVV steps: q_a - zp_a is used modulo 2^16 (vwmacc.vx at SEW 16),
+    a NULL bias still adds +0 (so a -0 product becomes +0), and vfmax orders -0 below +0."""
+    A = np.array([[5, -3]], np.int8)
+    B = np.array([[2, 1]], np.int8)
+    # zp = 40000: int16(5 - 40000) = 25541, int16(-3 - 40000) = 25533 -> 2*25541 + 25533 = 76615
+    got = T.oracle_w8a8dyn(A, B, None, -np.inf, np.inf, [1.0], [40000], [1.0])
+    assert got[0, 0] == np.float32(76615.0)
+    Z = np.zeros((1, 2), np.int8)
+    neg = T.oracle_w8a8dyn(Z, B, None, -np.inf, np.inf, [1.0], [0], [-1.0])
+    assert neg.view(np.uint32)[0, 0] == 0  # -0 product + 0 = +0
+    both = T.oracle_w8a8dyn(Z, B, np.array([-0.0], np.float32), 0.0, np.inf, [1.0], [0], [-1.0])
+    assert both.view(np.uint32)[0, 0] == 0  # -0 + -0 = -0, then vfmax(-0, +0) = +0
+
+
 def test_w4a16_rvv_numerics_within_reference_tolerance():
     """The RVV-numerics restatement (f16 weights, f16 FMA chain) stays within the reference
     test's own tolerance (abs 1.0, cosine 0.9999) of the f32 oracle on the reference inputs."""

@@ -44,6 +44,14 @@ REF_FUNCS = {
                 "get_scale_b_offset", "get_c_offset", "get_bias_offset", "get_d_offset",
                 "get_d_size", "get_a_packed_size", "get_b_packed_size", "run_a_pack",
                 "run_bt_pack", "run"],
+    "w8dynp": ["get_m_step", "get_n_step", "get_a_packed_offset", "get_b_packed_offset",
+               "get_c_offset", "get_bias_offset", "get_d_offset", "get_d_size",
+               "get_a_packed_size", "get_b_packed_size", "run_a_pack", "run_b_pack",
+               "run_bt_pack", "run"],
+    "w8dynhp": ["get_m_step", "get_n_step", "get_a_packed_offset", "get_b_packed_offset",
+                "get_c_offset", "get_bias_offset", "get_d_offset", "get_d_size",
+                "get_a_packed_size", "get_b_packed_size", "run_a_pack", "run_b_pack",
+                "run_bt_pack", "run"],
     "igemmclp": ["get_m_step", "get_n_step", "get_b_packed_offset", "get_c_offset",
                  "get_bias_offset", "get_d_offset", "get_d_size", "get_b_packed_size",
                  "run_bt_pack", "run"],
@@ -149,6 +157,8 @@ OPERANDS = [
     ("w4a16p", "get_b_packed_offset", 0, 40, 384, "n", True),
     ("w4a16fp", "get_a_packed_offset", 2, 70, 384, "m", False),
     ("w4a16fp", "get_b_packed_offset", 0, 40, 384, "n", True),
+    ("w8dynp", "get_a_packed_offset", 1, 257, 320, "m", False),
+    ("w8dynhp", "get_b_packed_offset", 1, 129, 256, "n", False),
     ("igemmclp", "get_b_packed_offset", 1, 200, 288, "n", False),
 ]
 
@@ -198,6 +208,13 @@ def test_packed_sizes_equal_unpacked_sizes(lib, mod):
         assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(48) == 4 * 48
         assert (_getter(lib, sym(mod, kind, "get_scale_b_offset"), 3)(16, 3, 128) ==
                 _getter(lib, sym(mod, "w4a16", "get_scale_b_offset"), 3)(16, 3, 128))
+    for kind in ("w8dynp", "w8dynhp"):
+        assert g(kind, "get_a_packed_size")(m, k) == m * k
+        assert g(kind, "get_b_packed_size")(n, k) == n * k
+    for kind, es in (("w8dyn", 4), ("w8dynp", 4), ("w8dynh", 2), ("w8dynhp", 2)):
+        assert g(kind, "get_d_size")(m, n) == es * m * n
+        assert _getter(lib, sym(mod, kind, "get_d_offset"), 3)(128, 128, n) == es * (128 * n + 128)
+        assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(256) == es * 256
     for kind in ("w4a8h", "w4a8b", "w4a8hp", "w4a8bp"):
         assert g(kind, "get_d_size")(m, n) == 2 * m * n
         ms = _getter(lib, sym(mod, kind, "get_m_step"), 0)()
@@ -210,10 +227,11 @@ def test_packed_sizes_equal_unpacked_sizes(lib, mod):
 
 
 def test_packed_steps_via_interface_structs(lib, mod, shim):
-    out = (ctypes.c_size_t * 34)()
+    out = (ctypes.c_size_t * 42)()
     shim.tqts_steps_via_interfaces(out)
     kinds = (["clamp", "w8a8", "w4a8", "w4a16", "igemmcl"] + list(PACKED) +
-             ["w4a8h", "w4a8hp", "w4a8b", "w4a8bp", "w4a16f", "w4a16fp"])
+             ["w4a8h", "w4a8hp", "w4a8b", "w4a8bp", "w4a16f", "w4a16fp", "w8dyn", "w8dynp",
+              "w8dynh", "w8dynhp"])
     for t, kind in enumerate(kinds):
         assert out[2 * t] == _getter(lib, sym(mod, kind, "get_m_step"), 0)()
         assert out[2 * t + 1] == _getter(lib, sym(mod, kind, "get_n_step"), 0)()

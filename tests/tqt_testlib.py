@@ -111,6 +111,12 @@ def oracle():
         "tqto_gemm_f16_qsi4c2t_f32out": (None, [c_size] * 4 + [c_vp, c_size, c_vp, c_size, c_vp,
                                                  c_size, c_vp, c_size, c_vp, c_size, c_vp,
                                                  ctypes.c_float, ctypes.c_float]),
+        "tqto_f16_add": (u16, [u16, u16]),
+        "tqto_gemm_qai8dx_qsi8cxt_f32": (None, [c_size] * 3 + [
+            c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp, ctypes.c_float, ctypes.c_float,
+            c_vp, c_vp, c_vp]),
+        "tqto_gemm_qai8dx_qsi8cxt_f16": (None, [c_size] * 3 + [
+            c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp, u16, u16, c_vp, c_vp, c_vp]),
         "tqto_gemm_f16_qsi4c2t_rvv": (None, [c_size] * 4 + [c_vp, c_size, c_vp, c_size, c_vp,
                                               c_size, c_vp, c_size, c_vp, c_size, c_vp, u16,
                                               u16]),
@@ -273,6 +279,42 @@ def oracle_w4a16_f32(A16, Bp, S16, bl, C, bias, cmin, cmax):
     return D
 
 
+def oracle_w8a8dyn(A, B, bias, cmin, cmax, scale_a, zp_a, scale_b, f16=False):
+    """W8A8 with dynamic per-row A quantization: f32 D, or f16 D (bias, cmin, cmax then given as
+    binary16 patterns)."""
+    m, k = A.shape
+    n = B.shape[0]
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    sa = np.ascontiguousarray(scale_a, np.float32)
+    za = np.ascontiguousarray(zp_a, np.int32)
+    sb = np.ascontiguousarray(scale_b, np.float32)
+    if f16:
+        D = np.zeros((m, n), np.uint16)
+        b = None if bias is None else np.ascontiguousarray(bias, np.uint16)
+        oracle().tqto_gemm_qai8dx_qsi8cxt_f16(m, n, k, ptr(A), k, ptr(B), k, ptr(D), n, ptr(b),
+                                              int(cmin), int(cmax), ptr(sa), ptr(za), ptr(sb))
+    else:
+        D = np.zeros((m, n), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        oracle().tqto_gemm_qai8dx_qsi8cxt_f32(m, n, k, ptr(A), k, ptr(B), k, ptr(D), n, ptr(b),
+                                              float(cmin), float(cmax), ptr(sa), ptr(za), ptr(sb))
+    return D
+
+
+def gen_w8a8dyn(m, n, k, seed=42, zp_range=(-128, 127)):
+    """Random qai8dx x qsi8cx operands: int8 A and B, per-row scale / zero point, per-channel
+    scale, f32 bias."""
+    rng = np.random.default_rng(seed)
+    return dict(
+        A=rng.integers(-128, 128, size=(m, k), dtype=np.int64).astype(np.int8),
+        B=rng.integers(-127, 128, size=(n, k), dtype=np.int64).astype(np.int8),
+        scale_a=rng.uniform(0.002, 0.02, size=m).astype(np.float32),
+        zp_a=rng.integers(zp_range[0], zp_range[1] + 1, size=m).astype(np.int32),
+        scale_b=rng.uniform(0.001, 0.01, size=n).astype(np.float32),
+        bias=rng.uniform(-10, 10, size=n).astype(np.float32))
+
+
 def oracle_igemmcl(inp, W, bias, cmin, cmax, conv, scale_a, scale_b, qcb, scale_d, zp_d,
                    m=None, m_idx=0, group_idx=0, D=None):
     n = W.shape[0]
@@ -385,7 +427,7 @@ def gen_igemmcl(ID, IH, IW, IC, OC, KH, KW, stride=(1, 1), pad=(0, 0), dil=(1, 1
 
 # chunk bytes per packed kernel type (one MFMA lane fragment for every type)
 PACK_CHUNK = {"clampp": 16, "w8a8pb": 16, "w8a8p": 16, "igemmclp": 16, "w4a8p": 16,
-              "w4a16p": 16, "w4a16fp": 16}
+              "w4a16p": 16, "w4a16fp": 16, "w8dynp": 16, "w8dynhp": 16}
 
 
 def frag_perm(kbytes):

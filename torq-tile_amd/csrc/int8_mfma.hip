@@ -1,7 +1,10 @@
-// int8 x int8 -> int32 contraction on gfx950 int8 MFMA, shared by three kernel types:
+// int8 x int8 -> int32 contraction on gfx950 int8 MFMA, shared by these kernel types:
 //   gemm_clamp_i32_i8_i8                                (B is [k, n] row-major, int32 out)
 //   gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt     (B is [n, k], requantized int8 out)
 //   igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt  (A gathered from an NDHWC image)
+//   gemm_1xnbias_clamp_{f32,f16}_qai8dx_qsi8cxt         (per-row dynamically quantized A,
+//                                                        f32 / f16 out)
+// and their packed siblings.
 //
 // Three kernels, chosen per call:
 //   * int8_stream_kernel (plain A, B = [n, k], k % 128 == 0: W8A8 at its config): a 4-deep
@@ -22,6 +25,10 @@
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_clamp_i32_i8p_i8p_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -34,7 +41,18 @@ constexpr int kConvMaxChunks = 1024;  // fast implicit convolution: k <= 16384
 
 enum AMode { A_MATRIX = 0, A_CONV_CL = 1 };
 enum BMode { B_NK = 0, B_KN = 1 };
-enum EpiMode { EPI_CLAMP_I32 = 0, EPI_REQUANT_I8 = 1 };
+enum EpiMode { EPI_CLAMP_I32 = 0, EPI_REQUANT_I8 = 1, EPI_DYN_F32 = 2, EPI_DYN_F16 = 3 };
+
+__host__ __device__ constexpr bool is_dyn(int epi)
+{
+    return epi == EPI_DYN_F32 || epi == EPI_DYN_F16;
+}
+
+// Zero points for which q_a - zp fits 16 bits for every int8 q_a: there the reference's
+// sum of int16(q_a - zp) * q_b equals sum q_a * q_b - zp * sum q_b (mod 2^32), which the MFMA
+// kernels compute. Any other zero point takes an exact per-output loop.
+constexpr int32_t kDynZpMin = -32640;
+constexpr int32_t kDynZpMax = 32640;
 
 struct ConvGeom
 {
@@ -70,7 +88,81 @@ struct Int8Args
     int32_t zp_d;
     ConvGeom cv;
     PackDesc pa, pb;  // packed A / B of the p-variants (read when the kernel's PK bit is set)
+    // qai8dx x qsi8cx: per-row scale / zero point of A (scale_b above is per channel), an f32
+    // or f16 bias, and the clamp bounds widened to f32
+    const float *dyn_sa;
+    const int32_t *dyn_za;
+    const void *fbias;
+    float fcmin, fcmax;
 };
+
+// The reference's accumulator of one output, sum_k int16(q_a - zp) * q_b in wrapping int32
+// (tqt_kernel_gemm_qai8dx_qsi8cx_4x1vl_rvv.h:95-140: vwmacc.vx at SEW 16 takes the low 16 bits
+// of the scalar q_a - zp), summed directly.
+template <int PK>
+__device__ uint32_t dyn_exact_acc(const Int8Args &a, int gm, int gn, int32_t zp)
+{
+    const PackRow ra = pack_row_info(a.pa, gm);
+    const PackRow rb = pack_row_info(a.pb, gn);
+    uint32_t acc = 0;
+    for (int k = 0; k < a.K; ++k) {
+        const int32_t av = (PK & PK_A) ? a.A[pack_row_byte(ra, k)]
+                                       : a.A[static_cast<long long>(gm) * a.lda + k];
+        const int32_t bv = (PK & PK_B) ? a.B[pack_row_byte(rb, k)]
+                                       : a.B[static_cast<long long>(gn) * a.ldb + k];
+        const uint32_t d = static_cast<uint32_t>(av) - static_cast<uint32_t>(zp);
+        const int32_t a16 = static_cast<int16_t>(static_cast<uint16_t>(d & 0xffffu));
+        acc += static_cast<uint32_t>(a16 * bv);
+    }
+    return acc;
+}
+
+// Epilogue of the qai8dx x qsi8cx types for one output from its accumulator x
+// (tqt_kernel_gemm_qai8dx_qsi8cx_4x1vl_rvv.h): f32 D (dequant_fp32 :145-215): f32(x) * (sb * sa),
+// + bias (+0 without one), vfmax, vfmin; f16 D (dequant_fp16 :217-330): the same f32 product
+// rounded to f16, + the f16 bias in f16, then the bounds. Every step rounds once (the library is
+// built without contraction).
+template <int EPI>
+__device__ __forceinline__ void dyn_finish(const Int8Args &a, int gm, int gn, long long drow,
+                                           uint32_t x)
+{
+    const float sigma = __fmul_rn(a.scale_b[gn], a.dyn_sa[gm]);
+    const float f = __fmul_rn(static_cast<float>(static_cast<int32_t>(x)), sigma);
+    if constexpr (EPI == EPI_DYN_F32) {
+        float v = __fadd_rn(f, a.fbias ? static_cast<const float *>(a.fbias)[gn] : 0.0f);
+        v = rv_fmaxf(v, a.fcmin);
+        v = rv_fminf(v, a.fcmax);
+        static_cast<float *>(a.D)[drow * a.ldd + gn] = v;
+    } else {
+        // The product must be rounded to f32 before the f16 conversion (vfmul then vfncvt):
+        // without this register barrier the compiler folds both into one v_fma_mixlo_f16, which
+        // rounds the exact product to f16 once.
+        float fr = f;
+        asm volatile("" : "+v"(fr));
+        const _Float16 h = static_cast<_Float16>(fr);
+        const _Float16 b = a.fbias ? static_cast<const _Float16 *>(a.fbias)[gn]
+                                   : static_cast<_Float16>(0.0f);
+        const _Float16 hs = h + b;  // one binary16 rounding
+        float v = rv_fmaxf(static_cast<float>(hs), a.fcmin);  // exact on binary16 values
+        v = rv_fminf(v, a.fcmax);
+        store_out<OUT_F16>(a.D, drow * a.ldd + gn, v);
+    }
+}
+
+__device__ __forceinline__ bool dyn_zp_in_range(int32_t zp)
+{
+    return zp >= kDynZpMin && zp <= kDynZpMax;
+}
+
+// MFMA-kernel epilogue of the qai8dx x qsi8cx types for a zero point in range: acc = sum q_a *
+// q_b, rs = sum q_b of the column.
+template <int EPI>
+__device__ __forceinline__ void dyn_store(const Int8Args &a, int gm, int gn, long long drow,
+                                          int32_t acc, int32_t rs)
+{
+    const uint32_t zp = static_cast<uint32_t>(a.dyn_za[gm]);
+    dyn_finish<EPI>(a, gm, gn, drow, static_cast<uint32_t>(acc) - zp * static_cast<uint32_t>(rs));
+}
 
 // LDS tile of R rows x 64 bytes. The 16-byte column chunk of row r is XOR-swizzled with
 // (r >> 2) & 3 so that the 16 rows read by one 16-lane group of ds_read_b128 hit distinct
@@ -297,6 +389,8 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             acc[i][j] = i32x4{0, 0, 0, 0};
         }
     }
+    // qai8dx x qsi8cx: this lane's share of sum_k q_b for its column (16 of every 64 k)
+    [[maybe_unused]] int32_t rs[NT] = {};
 
     const int nk = (a.K + kBK - 1) / kBK;
     const int frag_row = lane & 15;
@@ -319,6 +413,15 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 #pragma unroll
             for (int j = 0; j < NT; ++j) {
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if constexpr (is_dyn(EPI)) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    rs[j] = __builtin_amdgcn_sdot4(fb[j][q], 0x01010101, rs[j], false);
+                }
             }
         }
     };
@@ -362,6 +465,53 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
         if (kt0 + u < nk) {
             step(kt0 + u, ps[(u + 1) % PF]);
         }
+    }
+
+    if constexpr (is_dyn(EPI)) {
+        // the four lanes of a column (lane % 16) each summed one 16-byte chunk of every k-step
+        int32_t rsum[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int32_t t = rs[j] + __shfl_xor(rs[j], 16);
+            rsum[j] = t + __shfl_xor(t, 32);
+        }
+        bool in_range = true;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
+                in_range = in_range && (gm >= a.M || dyn_zp_in_range(a.dyn_za[gm]));
+            }
+        }
+        if (in_range) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
+                        if (gm < a.M && gn < a.N) {
+                            dyn_store<EPI>(a, gm, gn, a.d_row0 + gm, acc[i][j][r], rsum[j]);
+                        }
+                    }
+                }
+            }
+        } else {
+            // a zero point beyond 16 bits: this lane's outputs summed term by term
+            for (int e = 0; e < MT * NT * 4; ++e) {
+                const int i = e / (NT * 4), j = (e / 4) % NT, r = e % 4;
+                const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
+                const int gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
+                if (gm < a.M && gn < a.N) {
+                    dyn_finish<EPI>(a, gm, gn, a.d_row0 + gm,
+                                    dyn_exact_acc<PK>(a, gm, gn, a.dyn_za[gm]));
+                }
+            }
+        }
+        return;
     }
 
     // Epilogue: lane holds D[4 * (lane / 16) + r][lane % 16] of every 16x16 sub-tile.
@@ -534,6 +684,8 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
             }
         }
     }
+    // qai8dx x qsi8cx: this lane's share of sum_k q_b for its column (half of every 32 k)
+    [[maybe_unused]] int32_t rs[NF] = {};
 
     // MFMA operand lanes: row r32 of a 32-row fragment, k-chunk 2 * step + h. LDS position of
     // (row, chunk) in a stage: plain rows keep 128 bytes per row, chunks XOR-swizzled; packed
@@ -571,6 +723,18 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
                 for (int j = 0; j < NF; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[step][i], fb[step][j],
                                                                       acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+        if constexpr (is_dyn(EPI)) {
+#pragma unroll
+            for (int step = 0; step < KS; ++step) {
+#pragma unroll
+                for (int j = 0; j < NF; ++j) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        rs[j] = __builtin_amdgcn_sdot4(fb[step][j][q], 0x01010101, rs[j], false);
+                    }
                 }
             }
         }
@@ -620,6 +784,52 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         step(st + 3, sa3, sb3, sa2, sb2);
     }
     __syncthreads();  // s_mult / s_shift visible even when k == 0
+
+    if constexpr (is_dyn(EPI)) {
+        // lanes r32 and r32 + 32 summed the two 16-byte halves of every k-step of column r32
+        int32_t rsum[NF];
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            rsum[j] = rs[j] + __shfl_xor(rs[j], 32);
+        }
+        bool in_range = true;
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                in_range = in_range && (gm >= a.M || dyn_zp_in_range(a.dyn_za[gm]));
+            }
+        }
+        if (in_range) {
+#pragma unroll
+            for (int j = 0; j < NF; ++j) {
+                const int gn = n0 + wn * 64 + 32 * j + r32;
+#pragma unroll
+                for (int i = 0; i < MF; ++i) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (gm < a.M && gn < a.N) {
+                            dyn_store<EPI>(a, gm, gn, a.d_row0 + gm, acc[i][j][r], rsum[j]);
+                        }
+                    }
+                }
+            }
+        } else {
+            // a zero point beyond 16 bits: this lane's outputs summed term by term
+            for (int e = 0; e < NF * MF * 16; ++e) {
+                const int j = e / (MF * 16), i = (e / 16) % MF, r = e % 16;
+                const int gn = n0 + wn * 64 + 32 * j + r32;
+                const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (gm < a.M && gn < a.N) {
+                    dyn_finish<EPI>(a, gm, gn, a.d_row0 + gm,
+                                    dyn_exact_acc<PK>(a, gm, gn, a.dyn_za[gm]));
+                }
+            }
+        }
+        return;
+    }
 
     // Epilogue: lane holds D[8 * (r / 4) + 4 * h + r % 4][r32] of each 32 x 32 fragment.
 #pragma unroll
@@ -673,6 +883,10 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     }
     const int gm = static_cast<int>(idx / a.N);
     const int gn = static_cast<int>(idx - static_cast<long long>(gm) * a.N);
+    if constexpr (is_dyn(EPI)) {
+        dyn_finish<EPI>(a, gm, gn, a.d_row0 + gm, dyn_exact_acc<PK>(a, gm, gn, a.dyn_za[gm]));
+        return;
+    }
     uint32_t acc = 0;
     if constexpr (AM == A_MATRIX) {
         if constexpr (PK == PK_NONE) {
@@ -946,6 +1160,48 @@ void packed_gemm_run(size_t m, size_t n, size_t k, const void *A, size_t lda, si
     } else {
         launch_int8<A_MATRIX, B_NK, EPI, PK_B>(a, fast, stream, where);
     }
+}
+
+// Shared body of the qai8dx x qsi8cx runs (f32 / f16 D, plain or packed A and B). C is not an
+// input: the reference ignores it (…qai8dx_qsi8cxt_4x1vl_rvv.cpp TQT_UNUSED(C)).
+template <int EPI>
+void dyn_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a,
+             const void *B, size_t ldb, size_t k_idx_b, void *D, size_t ldd, const void *bias,
+             float clamp_min, float clamp_max, const struct tqt_qai8dxp_qsi8cxp_params *params,
+             bool packed, hipStream_t stream, const char *where)
+{
+    if (!params) {
+        return;  // reference …qai8dx_qsi8cxt_4x1vl_rvv.cpp run: if (!params) return
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    TQT_REQUIRE(params->scale_a && params->zero_point_a && params->scale_b,
+                "params arrays must be non-NULL");
+    Int8Args a = base_args(m, n, k);
+    a.scale_b = params->scale_b;
+    a.dyn_sa = params->scale_a;
+    a.dyn_za = params->zero_point_a;
+    a.fbias = bias;
+    a.fcmin = clamp_min;
+    a.fcmax = clamp_max;
+    if (packed) {
+        packed_gemm_run<EPI>(m, n, k, A, lda, k_idx_a, true, B, ldb, k_idx_b, nullptr, 0, D, ldd,
+                             a, stream, where);
+        return;
+    }
+    TQT_REQUIRE(A != nullptr || k == 0, "A == NULL");
+    TQT_REQUIRE(B != nullptr || k == 0, "B == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    a.A = static_cast<const int8_t *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const int8_t *>(B);
+    a.ldb = static_cast<long long>(ldb);
+    a.D = D;
+    a.ldd = static_cast<long long>(ldd);
+    const bool fast = (k % 16 == 0) && (lda % 16 == 0) && (ldb % 16 == 0) && aligned16(A) &&
+                      aligned16(B);
+    launch_int8<A_MATRIX, B_NK, EPI>(a, fast, stream, where);
 }
 
 }  // namespace
@@ -1379,6 +1635,213 @@ void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx95
         clamp_min, clamp_max, conv_params, quant_params, nullptr);
     finish_sync(nullptr,
                 "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
+}
+
+static const size_t kDynMStep = 128;
+static const size_t kDynNStep = 128;
+
+// =============================================================================================
+// gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt (reference …/gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_4x1vl_rvv.cpp; kernel semantics
+// tqt_kernel_gemm_qai8dx_qsi8cx_4x1vl_rvv.h)
+// =============================================================================================
+size_t tqt_get_m_step_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(void)
+{
+    return kDynMStep;
+}
+size_t tqt_get_n_step_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(void)
+{
+    return kDynNStep;
+}
+size_t tqt_get_a_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda)
+{
+    TQT_REQUIRE(m_idx % kDynMStep == 0, "m_idx % m_step == 0");
+    return (m_idx * lda + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_b_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb)
+{
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return (n_idx * ldb + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_c_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kDynMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(float);
+}
+size_t tqt_get_bias_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(size_t n_idx)
+{
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return n_idx * sizeof(float);
+}
+size_t tqt_get_d_offset_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kDynMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(float);
+}
+size_t tqt_get_d_size_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(float);
+}
+
+void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    float clamp_min, float clamp_max, const struct tqt_qai8dxp_qsi8cxp_params *params,
+    void *stream)
+{
+    (void)k_idx_a;
+    (void)k_idx_b;
+    (void)C;
+    (void)ldc;
+    dyn_run<EPI_DYN_F32>(m, n, k, A, lda, 0, B, ldb, 0, D, ldd, bias, clamp_min, clamp_max,
+                         params, false, as_stream(stream),
+                         "tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    float clamp_min, float clamp_max, const struct tqt_qai8dxp_qsi8cxp_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950_async(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd,
+                                    bias, clamp_min, clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950");
+}
+
+// gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp (reference …/gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_4x1vl_rvv.cpp; geometry getters and
+// packers in packing.hip)
+void tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, float clamp_min, float clamp_max,
+    const struct tqt_qai8dxp_qsi8cxp_params *params, void *stream)
+{
+    (void)C;
+    (void)ldc;
+    dyn_run<EPI_DYN_F32>(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, D, ldd, bias,
+                         clamp_min, clamp_max, params, true, as_stream(stream),
+                         "tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, float clamp_min, float clamp_max,
+    const struct tqt_qai8dxp_qsi8cxp_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950_async(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C,
+                                     ldc, D, ldd, bias, clamp_min, clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950");
+}
+
+// =============================================================================================
+// gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt (reference …/gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_4x1vl_rvv.cpp; kernel semantics
+// tqt_kernel_gemm_qai8dx_qsi8cx_4x1vl_rvv.h)
+// =============================================================================================
+size_t tqt_get_m_step_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(void)
+{
+    return kDynMStep;
+}
+size_t tqt_get_n_step_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(void)
+{
+    return kDynNStep;
+}
+size_t tqt_get_a_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda)
+{
+    TQT_REQUIRE(m_idx % kDynMStep == 0, "m_idx % m_step == 0");
+    return (m_idx * lda + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_b_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb)
+{
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return (n_idx * ldb + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_c_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kDynMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(float16_t);
+}
+size_t tqt_get_bias_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(size_t n_idx)
+{
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return n_idx * sizeof(float16_t);
+}
+size_t tqt_get_d_offset_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kDynMStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kDynNStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(float16_t);
+}
+size_t tqt_get_d_size_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(float16_t);
+}
+
+void tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    float16_t clamp_min, float16_t clamp_max, const struct tqt_qai8dxp_qsi8cxp_params *params,
+    void *stream)
+{
+    (void)k_idx_a;
+    (void)k_idx_b;
+    (void)C;
+    (void)ldc;
+    dyn_run<EPI_DYN_F16>(m, n, k, A, lda, 0, B, ldb, 0, D, ldd, bias,
+                         static_cast<float>(clamp_min), static_cast<float>(clamp_max), params,
+                         false, as_stream(stream),
+                         "tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    float16_t clamp_min, float16_t clamp_max, const struct tqt_qai8dxp_qsi8cxp_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950_async(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd,
+                                    bias, clamp_min, clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950");
+}
+
+// gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp (reference …/gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_4x1vl_rvv.cpp; geometry getters and
+// packers in packing.hip)
+void tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, float16_t clamp_min, float16_t clamp_max,
+    const struct tqt_qai8dxp_qsi8cxp_params *params, void *stream)
+{
+    (void)C;
+    (void)ldc;
+    dyn_run<EPI_DYN_F16>(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, D, ldd, bias,
+                         static_cast<float>(clamp_min), static_cast<float>(clamp_max), params,
+                         true, as_stream(stream),
+                         "tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950");
+}
+
+void tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, float16_t clamp_min, float16_t clamp_max,
+    const struct tqt_qai8dxp_qsi8cxp_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950_async(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C,
+                                     ldc, D, ldd, bias, clamp_min, clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950");
 }
 
 const char *tqt_gfx950_target(void)

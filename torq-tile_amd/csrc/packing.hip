@@ -2,8 +2,9 @@
 //   gemm_clamp_i32_i8p_i8p, gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp,
 //   gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp, gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp,
 //   gemm_1xnbias_clamp_f16_f16p_qsi4c2p, igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp,
-//   and the output-type siblings gemm_1xnbias_clamp_{f16,bf16}_qai8dxp_qsi4cxp and
-//   gemm_1xnbias_clamp_f32_f16p_qsi4c2p (same layouts as the types they share a mainloop with).
+//   and the output-type siblings gemm_1xnbias_clamp_{f16,bf16}_qai8dxp_qsi4cxp,
+//   gemm_1xnbias_clamp_f32_f16p_qsi4c2p and gemm_1xnbias_clamp_{f32,f16}_qai8dxp_qsi8cxp (same
+//   layouts as the types they share a mainloop with).
 // Their run functions live beside the mainloops they share (int8_mfma.hip, gemm_i8_i4.hip,
 // gemm_f16_i4.hip). The layout (PackDesc, pack_offset) is defined in tqt_hip_common.hpp; the
 // reference's packers are the permutations of tqt_gemm_pack_rvv.h:354-398, 542-567, 740-856.
@@ -14,6 +15,8 @@
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_f16p_qsi4c2p_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
@@ -587,6 +590,88 @@ void tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950(
     pack_nk(n, k, ldb, ldb_packed, k_idx, kPackW4A16NStep, kPackW4A16Chunk, 0, true, B, B_packed, nullptr, true,
             "tqt_run_bt_pack_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950");
 }
+
+// =============================================================================================
+// gemm_1xnbias_clamp_{f32,f16}_qai8dxp_qsi8cxp (reference …qai8dxp_qsi8cxp_4x1vl_rvv.cpp): the
+// layout and packers of qai8_qai8p_qsi8cxp; bias and D are f32 / f16 (ES bytes per element).
+// =============================================================================================
+#define TQT_DYNP(T, ES)                                                                            \
+    size_t tqt_get_m_step_##T##_mfma_gfx950(void) { return kPackI8MStep; }                         \
+    size_t tqt_get_n_step_##T##_mfma_gfx950(void) { return kPackI8NStep; }                         \
+    size_t tqt_get_a_packed_offset_##T##_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda,       \
+                                                     size_t actual_m)                              \
+    {                                                                                              \
+        TQT_REQ_M(kPackI8MStep);                                                                   \
+        return packed_offset(m_idx, k_idx, lda, actual_m, kPackI8MStep, 1);                        \
+    }                                                                                              \
+    size_t tqt_get_b_packed_offset_##T##_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb,       \
+                                                     size_t actual_n)                              \
+    {                                                                                              \
+        TQT_REQ_N(kPackI8NStep);                                                                   \
+        return packed_offset(n_idx, k_idx, ldb, actual_n, kPackI8NStep, 1);                        \
+    }                                                                                              \
+    size_t tqt_get_c_offset_##T##_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)             \
+    {                                                                                              \
+        TQT_REQ_M(kPackI8MStep);                                                                   \
+        TQT_REQ_N(kPackI8NStep);                                                                   \
+        return (m_idx * ldc + n_idx) * (ES);                                                       \
+    }                                                                                              \
+    size_t tqt_get_bias_offset_##T##_mfma_gfx950(size_t n_idx)                                    \
+    {                                                                                              \
+        TQT_REQ_N(kPackI8NStep);                                                                   \
+        return n_idx * (ES);                                                                       \
+    }                                                                                              \
+    size_t tqt_get_d_offset_##T##_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)             \
+    {                                                                                              \
+        TQT_REQ_M(kPackI8MStep);                                                                   \
+        TQT_REQ_N(kPackI8NStep);                                                                   \
+        return (m_idx * ldd + n_idx) * (ES);                                                       \
+    }                                                                                              \
+    size_t tqt_get_d_size_##T##_mfma_gfx950(size_t m, size_t n) { return m * n * (ES); }          \
+    size_t tqt_get_a_packed_size_##T##_mfma_gfx950(size_t m, size_t k) { return m * k; }           \
+    size_t tqt_get_b_packed_size_##T##_mfma_gfx950(size_t n, size_t k) { return n * k; }           \
+    void tqt_run_a_pack_##T##_mfma_gfx950_async(size_t m, size_t k, size_t lda, size_t lda_packed, \
+                                                size_t k_idx, const void *A, void *A_packed,       \
+                                                void *stream)                                      \
+    {                                                                                              \
+        pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, kPackI8Chunk, 1, false, A, A_packed,   \
+                stream, false, "tqt_run_a_pack_" #T "_mfma_gfx950");                               \
+    }                                                                                              \
+    void tqt_run_a_pack_##T##_mfma_gfx950(size_t m, size_t k, size_t lda, size_t lda_packed,       \
+                                          size_t k_idx, const void *A, void *A_packed)             \
+    {                                                                                              \
+        pack_nk(m, k, lda, lda_packed, k_idx, kPackI8MStep, kPackI8Chunk, 1, false, A, A_packed,   \
+                nullptr, true, "tqt_run_a_pack_" #T "_mfma_gfx950");                               \
+    }                                                                                              \
+    void tqt_run_b_pack_##T##_mfma_gfx950_async(size_t n, size_t k, size_t ldb, size_t ldb_packed, \
+                                                size_t k_idx, const void *B, void *B_packed,       \
+                                                void *stream)                                      \
+    {                                                                                              \
+        pack_kn_i8(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, B, B_packed, stream, false,         \
+                   "tqt_run_b_pack_" #T "_mfma_gfx950");                                           \
+    }                                                                                              \
+    void tqt_run_b_pack_##T##_mfma_gfx950(size_t n, size_t k, size_t ldb, size_t ldb_packed,       \
+                                          size_t k_idx, const void *B, void *B_packed)             \
+    {                                                                                              \
+        pack_kn_i8(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, B, B_packed, nullptr, true,         \
+                   "tqt_run_b_pack_" #T "_mfma_gfx950");                                           \
+    }                                                                                              \
+    void tqt_run_bt_pack_##T##_mfma_gfx950_async(size_t n, size_t k, size_t ldb,                  \
+                                                 size_t ldb_packed, size_t k_idx, const void *B,   \
+                                                 void *B_packed, void *stream)                     \
+    {                                                                                              \
+        pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed,   \
+                stream, false, "tqt_run_bt_pack_" #T "_mfma_gfx950");                              \
+    }                                                                                              \
+    void tqt_run_bt_pack_##T##_mfma_gfx950(size_t n, size_t k, size_t ldb, size_t ldb_packed,      \
+                                           size_t k_idx, const void *B, void *B_packed)            \
+    {                                                                                              \
+        pack_nk(n, k, ldb, ldb_packed, k_idx, kPackI8NStep, kPackI8Chunk, 1, false, B, B_packed,   \
+                nullptr, true, "tqt_run_bt_pack_" #T "_mfma_gfx950");                              \
+    }
+
+TQT_DYNP(gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp, sizeof(float))
+TQT_DYNP(gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp, sizeof(uint16_t))
 
 // =============================================================================================
 // gemm_1xnbias_clamp_f32_f16p_qsi4c2p (reference …f32_f16p_qsi4c2p_8x2vl_rvv.cpp): the packed

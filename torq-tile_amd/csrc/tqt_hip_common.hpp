@@ -347,6 +347,36 @@ __device__ __forceinline__ void store_out(void *p, long long i, float v)
     }
 }
 
+// RISC-V vfmax / vfmin on f32 (IEEE 754-2019 maximumNumber / minimumNumber): a NaN operand
+// yields the other one (the canonical quiet NaN when both are NaN), and -0 orders below +0.
+__device__ __forceinline__ float rv_fmaxf(float a, float b)
+{
+    if (a != a) {
+        return b != b ? __builtin_bit_cast(float, 0x7fc00000u) : b;
+    }
+    if (b != b) {
+        return a;
+    }
+    if (a == b) {
+        return (__builtin_bit_cast(uint32_t, a) >> 31) ? b : a;
+    }
+    return a > b ? a : b;
+}
+
+__device__ __forceinline__ float rv_fminf(float a, float b)
+{
+    if (a != a) {
+        return b != b ? __builtin_bit_cast(float, 0x7fc00000u) : b;
+    }
+    if (b != b) {
+        return a;
+    }
+    if (a == b) {
+        return (__builtin_bit_cast(uint32_t, a) >> 31) ? a : b;
+    }
+    return a < b ? a : b;
+}
+
 // One output of the requantization epilogue (reference tqt_kernel_gemm_i8_i8_4x1vl_rvv.h:
 // requantize_1xn :334-408 = vmulh, vsra by shift & 31, vadd zp, vnclip to i16 then i8;
 // clamp_i8 :231-259 = vmax then vmin).

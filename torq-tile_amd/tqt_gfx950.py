@@ -40,6 +40,11 @@ KERNELS = {
     # f32-output siblings of the W4A16 types: f32 C, bias, clamp bounds and D
     "w4a16f": "gemm_1xnbias_clamp_f32_f16_qsi4c2t",
     "w4a16fp": "gemm_1xnbias_clamp_f32_f16p_qsi4c2p",
+    # W8A8 with per-row dynamically quantized A (qai8dx x qsi8cx), f32 / f16 D
+    "w8dyn": "gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt",
+    "w8dynp": "gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp",
+    "w8dynh": "gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt",
+    "w8dynhp": "gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp",
 }
 
 
@@ -58,6 +63,12 @@ class QAI8QSI8CXParams(ctypes.Structure):
 
 class QAI8DXQSI4CXParams(ctypes.Structure):
     """struct tqt_qai8dx_qsi4cx_params (reference tqt_params_i8_i4.h:23-28)."""
+
+    _fields_ = [("scale_a", c_vp), ("zero_point_a", c_vp), ("scale_b", c_vp)]
+
+
+class QAI8DXPQSI8CXPParams(ctypes.Structure):
+    """struct tqt_qai8dxp_qsi8cxp_params (reference tqt_params_i8_i8.h:45-50)."""
 
     _fields_ = [("scale_a", c_vp), ("zero_point_a", c_vp), ("scale_b", c_vp)]
 
@@ -109,8 +120,8 @@ def _sym(kind, action):
     return "tqt_%s_%s_%s" % (action, name, VARIANT)
 
 
-# (action, restype, argtypes) per kernel type; float16 clamps are not callable from ctypes and
-# are reached through the test shim instead.
+# (action, restype, argtypes) per kernel type; float16 / bfloat16 clamps are not callable from
+# ctypes and those runs are reached through the test shim instead.
 _GEMM_I8_ARGS = [c_size, c_size, c_size, c_vp, c_size, c_size, c_vp, c_size, c_size, c_vp,
                  c_size, c_vp, c_size]
 _SIGS = {
@@ -247,7 +258,18 @@ _SIGS["w4a16fp"] = _packed_sigs(
     "w4a16", ["run_a_pack", "run_bt_pack"], _W4A16F_RUN,
     ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
 _SIGS["w4a16fp"]["get_scale_b_offset"] = (c_size, [c_size] * 3)
-_SHIM_RUNS = ("w4a16", "w4a16p", "w4a8h", "w4a8b", "w4a8hp", "w4a8bp")
+_DYN_RUN = _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float,
+                            ctypes.POINTER(QAI8DXPQSI8CXPParams)]
+_SIGS["w8dyn"] = {a: v for a, v in _SIGS["w4a8"].items() if not a.startswith("run")}
+_SIGS["w8dyn"].update(run=(None, _DYN_RUN), run_async=(None, _DYN_RUN + [c_vp]))
+_SIGS["w8dynh"] = {a: v for a, v in _SIGS["w4a8"].items() if not a.startswith("run")}
+_SIGS["w8dynp"] = _packed_sigs(
+    "w8dyn", ["run_a_pack", "run_b_pack", "run_bt_pack"], _DYN_RUN,
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SIGS["w8dynhp"] = _packed_sigs(
+    "w8dyn", ["run_a_pack", "run_b_pack", "run_bt_pack"], None,
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SHIM_RUNS = ("w4a16", "w4a16p", "w4a8h", "w4a8b", "w4a8hp", "w4a8bp", "w8dynh", "w8dynhp")
 
 
 class Lib:
