@@ -30,6 +30,10 @@
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_interface.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_interface.h"
+#include "tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
+#include "tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_interface.h"
+#include "tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_interface.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_interface.h"
@@ -343,13 +347,43 @@ static const struct tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_ukernel k_w8dynhp
     tqt_run_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950,
 };
 
+static const struct tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_ukernel k_convcl = {
+    tqt_get_m_step_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_n_step_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_b_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_c_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_bias_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_d_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_d_size_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_a_im2col_size_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_get_a_im2col_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_run_im2col_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+    tqt_run_conv_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950,
+};
+
+static const struct tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_ukernel k_convclp = {
+    tqt_get_m_step_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_n_step_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_a_im2colpack_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_c_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_bias_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_d_offset_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_d_size_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_a_im2colpack_size_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_get_b_packed_size_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_run_bt_pack_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_run_a_im2colpack_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+    tqt_run_conv_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
+};
+
 /* m_step and n_step of each kernel type read through its interface struct:
  * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl, then the packed types
  * clamp_i32_i8p_i8p, qai8_qai8_qsi8cxp, qai8_qai8p_qsi8cxp, qai8dxp_qsi4cxp, f16p_qsi4c2p,
  * igemmcl qsi8cxp, then the W4A8 output siblings f16 qsi4cxt, f16 qsi4cxp, bf16 qsi4cxt,
  * bf16 qsi4cxp, then the W4A16 f32-output siblings qsi4c2t, qsi4c2p, then the qai8dx x qsi8cx
- * types f32 qsi8cxt, f32 qsi8cxp, f16 qsi8cxt, f16 qsi8cxp. */
-void tqts_steps_via_interfaces(size_t out[42])
+ * types f32 qsi8cxt, f32 qsi8cxp, f16 qsi8cxt, f16 qsi8cxp, then convcl qsi8cxt, qsi8cxp. */
+void tqts_steps_via_interfaces(size_t out[46])
 {
     out[0] = k_clamp.get_m_step();
     out[1] = k_clamp.get_n_step();
@@ -393,6 +427,10 @@ void tqts_steps_via_interfaces(size_t out[42])
     out[39] = k_w8dynh.get_n_step();
     out[40] = k_w8dynhp.get_m_step();
     out[41] = k_w8dynhp.get_n_step();
+    out[42] = k_convcl.get_m_step();
+    out[43] = k_convcl.get_n_step();
+    out[44] = k_convclp.get_m_step();
+    out[45] = k_convclp.get_n_step();
 }
 
 /* W4A16 run through the interface struct with _Float16 clamps given as binary16 bits. */
@@ -587,5 +625,21 @@ void tqts_run_w8dyn(int f16, int packed, size_t m, size_t n, size_t k, const voi
     } else {
         k_w8dynh.run_gemm(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, NULL, 0, D, ldd, bias, hmin,
                           hmax, params);
+    }
+}
+
+/* convcl through its interface structs: im2col (plain) or fused im2col + pack (packed) of one
+ * group, then the convolution GEMM. */
+void tqts_run_convcl(int packed, size_t group_idx, const void *activation, void *A_buf,
+                     const tqt_conv_params *conv, size_t m, size_t n, size_t k, const void *B,
+                     void *D, const void *bias, int8_t cmin, int8_t cmax,
+                     const struct tqt_qai8_qai8_qsi8cx_params *params)
+{
+    if (packed) {
+        k_convclp.run_a_im2colpack(group_idx, activation, k, 0, A_buf, conv);
+        k_convclp.run_conv(m, n, k, A_buf, k, 0, B, k, 0, NULL, 0, D, n, bias, cmin, cmax, params);
+    } else {
+        k_convcl.run_im2col(group_idx, activation, A_buf, conv);
+        k_convcl.run_conv(m, n, k, A_buf, k, 0, B, k, 0, NULL, 0, D, n, bias, cmin, cmax, params);
     }
 }

@@ -149,6 +149,23 @@ def test_packer_ld_packed_and_k_idx_sub_buffers(gpu, kind, action, src, which):
     np.testing.assert_array_equal(host(halves), exp)
 
 
+@pytest.mark.parametrize("kind,action,src,which", PACKERS)
+def test_packer_overlapping_tail_panel(gpu, kind, action, src, which):
+    """ld_packed = k with k_idx > 0 moves the narrow last panel back onto the end of the panel
+    before it; the reference packs panel after panel, so those bytes hold the last panel's."""
+    step = step_of(kind, which)
+    rows, k = 2 * step + step // 3 + 1, 256
+    dsrc, ld, X = make_source(src, rows, k, seed=11)
+    kb = kbytes_of(src, k)
+    k_idx = 32
+    dst = dbuf(rows * kb)
+    pack(kind, action, rows, k, ld, k, k_idx, dsrc, dst)
+    exp = np.full(rows * kb, SENTINEL, np.uint8)
+    T.pack_panels(X, step, kc=T.PACK_CHUNK[kind], ld_packed=kb, shift=kbytes_of(src, k_idx),
+                  frag=src == "i4f", out=exp)
+    np.testing.assert_array_equal(host(dst), exp)
+
+
 # --------------------------------------------------------------------------------------------
 # packed runs
 # --------------------------------------------------------------------------------------------

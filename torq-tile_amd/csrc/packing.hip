@@ -38,14 +38,15 @@ struct PackSrc
 
 template <bool kFrag>
 __global__ __launch_bounds__(256) void pack_kernel(PackSrc s, uint8_t *dst, PackDesc d,
-                                                   long long nchunks, long long total)
+                                                   long long nchunks, long long total, int row0)
 {
     const long long idx = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     if (idx >= total) {
         return;
     }
-    const int r = static_cast<int>(idx / nchunks);
-    const long long kb0 = 16 * (idx - static_cast<long long>(r) * nchunks);
+    const int rr = static_cast<int>(idx / nchunks);
+    const int r = row0 + rr;
+    const long long kb0 = 16 * (idx - static_cast<long long>(rr) * nchunks);
     const long long rem = d.kbytes - kb0;
     const int cw = rem < 16 ? static_cast<int>(rem) : 16;
     uint8_t *o = dst + pack_offset(d, r, kb0);  // the piece's cw bytes are contiguous
@@ -62,7 +63,10 @@ __global__ __launch_bounds__(256) void pack_kernel(PackSrc s, uint8_t *dst, Pack
     }
 }
 
-// Packs `d.rows` rows of `d.kbytes` bytes from `src` into `dst`.
+// Packs `d.rows` rows of `d.kbytes` bytes from `src` into `dst`. A narrow last panel moved back
+// by the k_idx tail rule can overlap the end of the panel before it; the reference packs panel
+// after panel, so the last panel's bytes win there: it is then written by a second launch,
+// ordered after the first on the stream.
 void pack_rows(const void *src, long long rs, long long cs, void *dst, const PackDesc &d,
                bool frag, void *stream, bool sync, const char *where)
 {
@@ -71,17 +75,25 @@ void pack_rows(const void *src, long long rs, long long cs, void *dst, const Pac
     }
     TQT_REQUIRE(src != nullptr && dst != nullptr, "NULL pack buffer");
     const long long nchunks = (d.kbytes + 15) / 16;
-    const long long total = nchunks * d.rows;
-    const long long blocks = (total + 255) / 256;
-    TQT_REQUIRE(blocks < (1ll << 31), "pack grid too large");
     const PackSrc s = {static_cast<const uint8_t *>(src), rs, cs};
     hipStream_t st = as_stream(stream);
-    if (frag) {
-        hipLaunchKernelGGL(pack_kernel<true>, dim3(blocks), dim3(256), 0, st, s,
-                           static_cast<uint8_t *>(dst), d, nchunks, total);
-    } else {
-        hipLaunchKernelGGL(pack_kernel<false>, dim3(blocks), dim3(256), 0, st, s,
-                           static_cast<uint8_t *>(dst), d, nchunks, total);
+    const int split = tail_panel_start(d);
+    for (int part = 0; part < 2; ++part) {
+        const int row0 = part == 0 ? 0 : split;
+        const int rows = part == 0 ? split : d.rows - split;
+        if (rows <= 0) {
+            continue;
+        }
+        const long long total = nchunks * rows;
+        const long long blocks = (total + 255) / 256;
+        TQT_REQUIRE(blocks < (1ll << 31), "pack grid too large");
+        if (frag) {
+            hipLaunchKernelGGL(pack_kernel<true>, dim3(blocks), dim3(256), 0, st, s,
+                               static_cast<uint8_t *>(dst), d, nchunks, total, row0);
+        } else {
+            hipLaunchKernelGGL(pack_kernel<false>, dim3(blocks), dim3(256), 0, st, s,
+                               static_cast<uint8_t *>(dst), d, nchunks, total, row0);
+        }
     }
     if (sync) {
         finish_sync(st, where);

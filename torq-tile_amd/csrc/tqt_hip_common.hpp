@@ -280,6 +280,16 @@ inline PackDesc make_pack(size_t step, int kc, size_t rows, size_t ld_bytes, siz
     return d;
 }
 
+// First row of the panel that must be written after the others: the narrow last panel when the
+// k_idx tail rule moves it back onto the panel before it (d.rows when there is none).
+inline int tail_panel_start(const PackDesc &d)
+{
+    if (d.step <= 0 || d.shift <= 0 || d.rows <= d.step || d.rows % d.step == 0) {
+        return d.rows;
+    }
+    return d.rows - d.rows % d.step;
+}
+
 // Byte order inside one row of a packed W4A16 weight: each whole 64-byte group (four 32-k blocks
 // of 16 bytes) is a 4 x 4 transpose of dwords, so 16-byte chunk c of the group holds dword c of
 // blocks 0..3 - the 8-k slice lane group c feeds to the four MFMAs of the group. Bytes of a

@@ -45,6 +45,9 @@ KERNELS = {
     "w8dynp": "gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp",
     "w8dynh": "gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt",
     "w8dynhp": "gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp",
+    # explicit-im2col convolution (channel-last): im2col (or im2col + pack) and the W8A8 GEMM
+    "convcl": "convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt",
+    "convclp": "convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp",
 }
 
 
@@ -269,6 +272,41 @@ _SIGS["w8dynp"] = _packed_sigs(
 _SIGS["w8dynhp"] = _packed_sigs(
     "w8dyn", ["run_a_pack", "run_b_pack", "run_bt_pack"], None,
     ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_IM2COL = [c_size, c_vp, c_vp, ctypes.POINTER(ConvParams)]
+_IM2COLPACK = [c_size, c_vp, c_size, c_size, c_vp, ctypes.POINTER(ConvParams)]
+_SIGS["convcl"] = {
+    "get_m_step": (c_size, []),
+    "get_n_step": (c_size, []),
+    "get_b_offset": (c_size, [c_size] * 3),
+    "get_c_offset": (c_size, [c_size] * 3),
+    "get_bias_offset": (c_size, [c_size]),
+    "get_d_offset": (c_size, [c_size] * 3),
+    "get_d_size": (c_size, [c_size] * 2),
+    "get_a_im2col_size": (c_size, [c_size] * 2),
+    "get_a_im2col_offset": (c_size, [c_size] * 3),
+    "run_im2col": (None, _IM2COL),
+    "run_im2col_async": (None, _IM2COL + [c_vp]),
+    "run_conv": _SIGS["w8a8"]["run"],
+    "run_conv_async": _SIGS["w8a8"]["run_async"],
+}
+_SIGS["convclp"] = {
+    "get_m_step": (c_size, []),
+    "get_n_step": (c_size, []),
+    "get_a_im2colpack_offset": (c_size, _OFFP),
+    "get_b_packed_offset": (c_size, _OFFP),
+    "get_c_offset": (c_size, [c_size] * 3),
+    "get_bias_offset": (c_size, [c_size]),
+    "get_d_offset": (c_size, [c_size] * 3),
+    "get_d_size": (c_size, [c_size] * 2),
+    "get_a_im2colpack_size": (c_size, [c_size] * 2),
+    "get_b_packed_size": (c_size, [c_size] * 2),
+    "run_bt_pack": (None, _PACK),
+    "run_bt_pack_async": (None, _PACK + [c_vp]),
+    "run_a_im2colpack": (None, _IM2COLPACK),
+    "run_a_im2colpack_async": (None, _IM2COLPACK + [c_vp]),
+    "run_conv": _SIGS["w8a8p"]["run"],
+    "run_conv_async": _SIGS["w8a8p"]["run_async"],
+}
 _SHIM_RUNS = ("w4a16", "w4a16p", "w4a8h", "w4a8b", "w4a8hp", "w4a8bp", "w8dynh", "w8dynhp")
 
 
