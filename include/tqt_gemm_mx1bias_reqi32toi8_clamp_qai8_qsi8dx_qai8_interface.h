@@ -1,0 +1,51 @@
+/*
+ * Interface of micro-kernel type gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8: function-pointer types and the ukernel
+ * struct that every variant of this type fills. Same names, member order and signatures
+ * as the reference's src/gemm/gemm_i8_i8/gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8/tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_interface.h:22-59,
+ * so a caller that binds a variant through this struct can bind the gfx950 variant
+ * (tqt_*_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950) unchanged.
+ */
+#ifndef TQT_GEMM_MX1BIAS_REQI32TOI8_CLAMP_QAI8_QSI8DX_QAI8_INTERFACE_H
+#define TQT_GEMM_MX1BIAS_REQI32TOI8_CLAMP_QAI8_QSI8DX_QAI8_INTERFACE_H
+
+#include "tqt_gfx950_common.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_m_step_func_t)(void);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_n_step_func_t)(void);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_a_offset_func_t)(
+    size_t m_idx, size_t k_idx, size_t lda);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_b_offset_func_t)(
+    size_t n_idx, size_t k_idx, size_t ldb);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_c_offset_func_t)(
+    size_t m_idx, size_t n_idx, size_t ldc);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_bias_offset_func_t)(size_t m_idx);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_offset_func_t)(
+    size_t m_idx, size_t n_idx, size_t ldd);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_size_func_t)(size_t m, size_t n);
+typedef void (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_run_gemm_func_t)(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qsi8dx_qai8_params *params);
+
+struct tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_ukernel
+{
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_m_step_func_t get_m_step;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_n_step_func_t get_n_step;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_a_offset_func_t get_a_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_b_offset_func_t get_b_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_c_offset_func_t get_c_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_bias_offset_func_t get_bias_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_offset_func_t get_d_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_size_func_t get_d_size;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_run_gemm_func_t run_gemm;
+};
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif

@@ -6,6 +6,7 @@
  *   - struct tqt_qai8_qai8_qsi8cx_params  : reference src/gemm/gemm_i8_i8/tqt_params_i8_i8.h:16-24
  *   - struct tqt_qai8dx_qsi4cx_params     : reference src/gemm/gemm_i8_i4/tqt_params_i8_i4.h:23-28
  *   - struct tqt_qai8dxp_qsi8cxp_params   : reference src/gemm/gemm_i8_i8/tqt_params_i8_i8.h:45-50
+ *   - struct tqt_qai8_qsi8dx_qai8_params  : reference src/gemm/gemm_i8_i8/tqt_params_i8_i8.h:28-36
  *   - struct tqt_conv_params              : reference src/common/tqt_conv.h:20-31
  *   - float16_t, bfloat16_t               : reference src/common/tqt_common.h:27-28
  *
@@ -70,6 +71,20 @@ struct tqt_qai8dxp_qsi8cxp_params
     float *scale_a;
     int32_t *zero_point_a;
     float *scale_b;
+};
+
+/* Quantization parameters for qsi8dx (A = weights, per-row symmetric int8) x qai8 (B =
+ * activations, per-tensor asymmetric) -> qai8 D with an Mx1 (per-row) bias. scale_a has m
+ * entries (or 1 when quant_channel_a == 1). zero_point_b is not read by the kernels: callers fold
+ * it into the int32 bias. */
+struct tqt_qai8_qsi8dx_qai8_params
+{
+    float *scale_a;
+    int32_t quant_channel_a;
+    float scale_b;
+    int32_t zero_point_b;
+    float scale_d;
+    int32_t zero_point_d;
 };
 
 /* 3D convolution geometry (1D/2D set the higher dims to 1). The batch of an NDHWC input

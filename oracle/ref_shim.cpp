@@ -97,6 +97,13 @@ void tqtr_im2col_cl_i8(size_t group_idx, const int8_t *activation, int8_t *col,
     tqt_im2col_cl<int8_t>(group_idx, activation, col, params);
 }
 
+// src/common/tqt_conv.h:51-119
+void tqtr_im2col_cf_i8(size_t group_idx, const int8_t *activation, int8_t *col,
+                       const tqt_conv_params *params)
+{
+    tqt_im2col_cf<int8_t>(group_idx, activation, col, params);
+}
+
 // test/common/data_generator.{h,cpp}: UniformRandomGenerator<T>(low, high, seed).fill_matrix
 void tqtr_fill_uniform_f32(float low, float high, uint32_t seed, float *data, size_t rows,
                            size_t cols)

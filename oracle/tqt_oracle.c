@@ -801,6 +801,100 @@ void tqto_im2col_cl_i8(size_t group_idx, const int8_t *input, int8_t *col,
     }
 }
 
+void tqto_im2col_cf_i8(size_t group_idx, const int8_t *input, int8_t *col,
+                       const struct tqto_conv_params *p)
+{
+    /* src/common/tqt_conv.h:51-119: channel-first (NCDHW) input; row = (ic, kd, kh, kw) of the
+     * group, column = output pixel (od, oh, ow); out-of-bounds taps are zero. */
+    const size_t ID = p->input_shape[0], IH = p->input_shape[1], IW = p->input_shape[2];
+    const size_t OD = p->output_shape[0], OH = p->output_shape[1], OW = p->output_shape[2];
+    const size_t KD = p->kernel_shape[0], KH = p->kernel_shape[1], KW = p->kernel_shape[2];
+    const size_t ICg = p->input_channel / p->groups;
+    const size_t N = OD * OH * OW;
+    const int8_t *in = input + group_idx * ICg * ID * IH * IW;
+    size_t row = 0;
+    for (size_t ic = 0; ic < ICg; ++ic) {
+        for (size_t kd = 0; kd < KD; ++kd) {
+            for (size_t kh = 0; kh < KH; ++kh) {
+                for (size_t kw = 0; kw < KW; ++kw) {
+                    size_t colj = 0;
+                    for (size_t od = 0; od < OD; ++od) {
+                        const long id =
+                            (long)(od * p->stride[0] + kd * p->dilation[0]) - (long)p->pad[0];
+                        for (size_t oh = 0; oh < OH; ++oh) {
+                            const long ih =
+                                (long)(oh * p->stride[1] + kh * p->dilation[1]) - (long)p->pad[1];
+                            for (size_t ow = 0; ow < OW; ++ow) {
+                                const long iw = (long)(ow * p->stride[2] + kw * p->dilation[2]) -
+                                                (long)p->pad[2];
+                                int8_t v = 0;
+                                if (id >= 0 && id < (long)ID && ih >= 0 && ih < (long)IH &&
+                                    iw >= 0 && iw < (long)IW) {
+                                    v = in[ic * ID * IH * IW + ((size_t)id * IH + (size_t)ih) * IW +
+                                           (size_t)iw];
+                                }
+                                col[row * N + colj] = v;
+                                colj++;
+                            }
+                        }
+                    }
+                    row++;
+                }
+            }
+        }
+    }
+}
+
+void tqto_gemm_mx1bias_qsi8dx(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                              const int8_t *B, size_t ldb, const int32_t *C, size_t ldc,
+                              int8_t *D, size_t ldd, const int32_t *bias, int8_t cmin,
+                              int8_t cmax, const float *scale_a, int32_t quant_channel_a,
+                              float scale_b, float scale_d, int32_t zp_d)
+{
+    /* src/gemm/gemm_i8_i8/gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8/…_4x1vl_rvv.cpp:
+     * per-row multiplier from scale_a[i] * scale_b / scale_d (row 0's for all rows when
+     * quant_channel_a == 1), shift = -shift - 1 (:150-166); acc = C (or 0) + sum_k A[i,k]*B[k,j]
+     * in wrapping int32 (kernel :100-112, B [k, n] with row stride ldb), + bias[i]
+     * (add_mx1bias), then the requantization and clamp of the W8A8 kernels. */
+    for (size_t i = 0; i < m; ++i) {
+        const size_t src = (quant_channel_a == 1) ? 0 : i;
+        int32_t mult, shift;
+        const double real_scale = (double)scale_a[src] * (double)scale_b / (double)scale_d;
+        tqto_quantize_multiplier(real_scale, &mult, &shift);
+        shift = -shift - 1;
+        for (size_t j = 0; j < n; ++j) {
+            uint32_t acc = C ? (uint32_t)C[i * ldc + j] : 0u;
+            for (size_t p = 0; p < k; ++p) {
+                acc += (uint32_t)((int32_t)A[i * lda + p] * (int32_t)B[p * ldb + j]);
+            }
+            if (bias) {
+                acc += (uint32_t)bias[i];
+            }
+            D[i * ldd + j] = tqto_requant_one((int32_t)acc, mult, shift, zp_d, cmin, cmax);
+        }
+    }
+}
+
+void tqto_igemmcf_qsi8dx(size_t m, size_t n, const int8_t *input, size_t group_idx,
+                         size_t n_idx, const int8_t *A, size_t lda, int8_t *D, size_t ldd,
+                         const int32_t *bias, int8_t cmin, int8_t cmax,
+                         const struct tqto_conv_params *p, const float *scale_a,
+                         int32_t quant_channel_a, float scale_b, float scale_d, int32_t zp_d)
+{
+    /* src/conv/igemm_i8_i8/igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8/…_1vlx4_rvv.cpp
+     * run_igemm: output channels m (rows of the weights A [m, K]) times output pixels
+     * [n_idx, n_idx + n) of the channel-first im2col, C ignored, D rows at D + i * ldd + pixel:
+     * the mx1bias GEMM on columns n_idx.. of the full channel-first im2col. */
+    const size_t ICg = p->input_channel / p->groups;
+    const size_t K = ICg * p->kernel_shape[0] * p->kernel_shape[1] * p->kernel_shape[2];
+    const size_t N = p->output_shape[0] * p->output_shape[1] * p->output_shape[2];
+    int8_t *col = (int8_t *)malloc((K * N) > 0 ? K * N : 1);
+    tqto_im2col_cf_i8(group_idx, input, col, p);
+    tqto_gemm_mx1bias_qsi8dx(m, n, K, A, lda, col + n_idx, N, NULL, 0, D + n_idx, ldd, bias, cmin,
+                             cmax, scale_a, quant_channel_a, scale_b, scale_d, zp_d);
+    free(col);
+}
+
 void tqto_igemmcl_qsi8cxt(size_t m, size_t n, const int8_t *input, size_t group_idx,
                           size_t m_idx, const int8_t *B, size_t ldb, int8_t *D, size_t ldd,
                           const int32_t *bias, int8_t cmin, int8_t cmax,

@@ -139,6 +139,26 @@ void tqto_im2col_cl_i8(size_t group_idx, const int8_t *input, int8_t *col,
 
 /* igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt
  * (…igemmcl…qsi8cxt_4x1vl_rvv.cpp:81-286): pixels m_idx .. m_idx+m-1, D addressed absolutely. */
+/* Channel-first im2col (src/common/tqt_conv.h:51-119): [ICg*KD*KH*KW, OD*OH*OW] row-major. */
+void tqto_im2col_cf_i8(size_t group_idx, const int8_t *input, int8_t *col,
+                       const struct tqto_conv_params *p);
+
+/* gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8: A [m, k] per-row scaled weights, B [k, n],
+ * C int32 [m, n] (optional), bias int32 [m], per-row requantization, int8 D [m, n]. */
+void tqto_gemm_mx1bias_qsi8dx(size_t m, size_t n, size_t k, const int8_t *A, size_t lda,
+                              const int8_t *B, size_t ldb, const int32_t *C, size_t ldc,
+                              int8_t *D, size_t ldd, const int32_t *bias, int8_t cmin,
+                              int8_t cmax, const float *scale_a, int32_t quant_channel_a,
+                              float scale_b, float scale_d, int32_t zp_d);
+
+/* igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8: the mx1bias GEMM on output-pixel columns
+ * [n_idx, n_idx + n) of the channel-first im2col of one group. */
+void tqto_igemmcf_qsi8dx(size_t m, size_t n, const int8_t *input, size_t group_idx,
+                         size_t n_idx, const int8_t *A, size_t lda, int8_t *D, size_t ldd,
+                         const int32_t *bias, int8_t cmin, int8_t cmax,
+                         const struct tqto_conv_params *p, const float *scale_a,
+                         int32_t quant_channel_a, float scale_b, float scale_d, int32_t zp_d);
+
 void tqto_igemmcl_qsi8cxt(size_t m, size_t n, const int8_t *input, size_t group_idx,
                           size_t m_idx, const int8_t *B, size_t ldb, int8_t *D, size_t ldd,
                           const int32_t *bias, int8_t cmin, int8_t cmax,

@@ -30,6 +30,18 @@
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_interface.h"
 #include "tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_interface.h"
+#include "tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950.h"
+#include "tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_interface.h"
+#include "tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950.h"
+#include "tqt_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_interface.h"
+#include "tqt_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950.h"
+#include "tqt_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_interface.h"
+#include "tqt_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950.h"
+#include "tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_interface.h"
+#include "tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950.h"
+#include "tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_interface.h"
+#include "tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950.h"
 #include "tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_interface.h"
 #include "tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
 #include "tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_interface.h"
@@ -377,13 +389,97 @@ static const struct tqt_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_ukern
     tqt_run_conv_convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950,
 };
 
+static const struct tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_ukernel k_mx1 = {
+    tqt_get_m_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_n_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_a_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_b_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_c_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_bias_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_d_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_d_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+};
+
+static const struct tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_ukernel k_mx1p = {
+    tqt_get_m_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_n_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_a_packed_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_b_packed_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_c_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_bias_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_d_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_d_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_a_packed_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_b_packed_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_run_a_pack_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_run_b_pack_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_run_bt_pack_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+};
+
+static const struct tqt_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_ukernel k_convcf = {
+    tqt_get_m_step_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_n_step_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_a_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_c_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_bias_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_d_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_d_size_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_b_im2col_size_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_b_im2col_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_run_im2col_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_run_conv_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+};
+
+static const struct tqt_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_ukernel k_convcfp = {
+    tqt_get_m_step_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_n_step_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_a_packed_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_b_im2colpack_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_c_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_bias_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_d_offset_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_d_size_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_a_packed_size_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_get_b_im2colpack_size_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_run_a_pack_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_run_b_im2colpack_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+    tqt_run_conv_convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950,
+};
+
+static const struct tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_ukernel k_igemmcf = {
+    tqt_get_m_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_n_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_a_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_c_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_bias_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_d_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_get_d_size_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+    tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950,
+};
+
+static const struct tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_ukernel k_igemmcfp = {
+    tqt_get_m_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_get_n_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_get_a_packed_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_get_c_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_get_bias_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_get_d_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_get_d_size_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_get_a_packed_size_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_run_a_pack_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+    tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950,
+};
+
 /* m_step and n_step of each kernel type read through its interface struct:
  * out[2*t], out[2*t+1] for t = clamp, w8a8, w4a8, w4a16, igemmcl, then the packed types
  * clamp_i32_i8p_i8p, qai8_qai8_qsi8cxp, qai8_qai8p_qsi8cxp, qai8dxp_qsi4cxp, f16p_qsi4c2p,
  * igemmcl qsi8cxp, then the W4A8 output siblings f16 qsi4cxt, f16 qsi4cxp, bf16 qsi4cxt,
  * bf16 qsi4cxp, then the W4A16 f32-output siblings qsi4c2t, qsi4c2p, then the qai8dx x qsi8cx
- * types f32 qsi8cxt, f32 qsi8cxp, f16 qsi8cxt, f16 qsi8cxp, then convcl qsi8cxt, qsi8cxp. */
-void tqts_steps_via_interfaces(size_t out[46])
+ * types f32 qsi8cxt, f32 qsi8cxp, f16 qsi8cxt, f16 qsi8cxp, then convcl qsi8cxt, qsi8cxp, then the
+ * channel-first gemm_mx1bias, its packed form, convcf, convcf packed, igemmcf, igemmcf packed. */
+void tqts_steps_via_interfaces(size_t out[58])
 {
     out[0] = k_clamp.get_m_step();
     out[1] = k_clamp.get_n_step();
@@ -431,6 +527,18 @@ void tqts_steps_via_interfaces(size_t out[46])
     out[43] = k_convcl.get_n_step();
     out[44] = k_convclp.get_m_step();
     out[45] = k_convclp.get_n_step();
+    out[46] = k_mx1.get_m_step();
+    out[47] = k_mx1.get_n_step();
+    out[48] = k_mx1p.get_m_step();
+    out[49] = k_mx1p.get_n_step();
+    out[50] = k_convcf.get_m_step();
+    out[51] = k_convcf.get_n_step();
+    out[52] = k_convcfp.get_m_step();
+    out[53] = k_convcfp.get_n_step();
+    out[54] = k_igemmcf.get_m_step();
+    out[55] = k_igemmcf.get_n_step();
+    out[56] = k_igemmcfp.get_m_step();
+    out[57] = k_igemmcfp.get_n_step();
 }
 
 /* W4A16 run through the interface struct with _Float16 clamps given as binary16 bits. */
@@ -641,5 +749,40 @@ void tqts_run_convcl(int packed, size_t group_idx, const void *activation, void 
     } else {
         k_convcl.run_im2col(group_idx, activation, A_buf, conv);
         k_convcl.run_conv(m, n, k, A_buf, k, 0, B, k, 0, NULL, 0, D, n, bias, cmin, cmax, params);
+    }
+}
+
+/* convcf through its interface structs: channel-first im2col [K, N] (plain) or the fused
+ * im2col + pack of B and the packing of the weights (packed), then the convolution GEMM. */
+void tqts_run_convcf(int packed, size_t group_idx, const void *activation, void *B_buf,
+                     const tqt_conv_params *conv, size_t m, size_t n, size_t k, const void *W,
+                     void *W_buf, void *D, const void *bias, int8_t cmin, int8_t cmax,
+                     const struct tqt_qai8_qsi8dx_qai8_params *params)
+{
+    if (packed) {
+        k_convcfp.run_a_pack(m, k, k, k, 0, W, W_buf);
+        k_convcfp.run_b_im2colpack(group_idx, activation, k, 0, B_buf, conv);
+        k_convcfp.run_conv(m, n, k, W_buf, k, 0, B_buf, k, 0, NULL, 0, D, n, bias, cmin, cmax,
+                           params);
+    } else {
+        k_convcf.run_im2col(group_idx, activation, B_buf, conv);
+        k_convcf.run_conv(m, n, k, W, k, 0, B_buf, n, 0, NULL, 0, D, n, bias, cmin, cmax, params);
+    }
+}
+
+/* igemmcf through its interface struct (the packed form packs the weights into W_buf first). */
+void tqts_run_igemmcf(int packed, size_t m, size_t n, size_t k, const void *input,
+                      size_t group_idx, size_t n_idx, const void *W, void *W_buf, void *D,
+                      size_t ldd, const void *bias, int8_t cmin, int8_t cmax,
+                      const tqt_conv_params *conv,
+                      const struct tqt_qai8_qsi8dx_qai8_params *params)
+{
+    if (packed) {
+        k_igemmcfp.run_a_pack(m, k, k, k, 0, W, W_buf);
+        k_igemmcfp.run_igemm(m, n, k, input, group_idx, n_idx, 0, W_buf, k, 0, NULL, 0, D, ldd,
+                             bias, cmin, cmax, conv, params);
+    } else {
+        k_igemmcf.run_igemm(m, n, k, input, group_idx, n_idx, 0, W, k, 0, NULL, 0, D, ldd, bias,
+                            cmin, cmax, conv, params);
     }
 }

@@ -19,6 +19,7 @@ Fixtures (numpy .npz, no pickles):
                        below, quantize_i8 from the reference) with reference_gemm<float,float>
                        of the unquantized f32 operands, the value its test compares against
   ref_im2col.npz       tqt_im2col_cl<int8_t> on the reference's igemm shape list
+  ref_im2col_cf.npz    tqt_im2col_cf<int8_t> (channel-first) on the same list, with groups
   ref_qm.npz           tqt_quantize_multiplier on edge and random doubles
   ref_quant.npz        quantize_i8 / quantize_bias_i32 / fuse_zp_to_bias / quantize_fp16_to_int4
 """
@@ -217,6 +218,26 @@ def main():
         out["im2col_%d_in" % i] = inp
         out["im2col_%d_col" % i] = col
     np.savez_compressed(os.path.join(HERE, "ref_im2col.npz"),
+                        shapes=np.array(CONV_SHAPES, np.int64), **out)
+
+    # --- channel-first im2col (src/common/tqt_conv.h:51-119), two groups where IC allows ---
+    out = {}
+    for i, (IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, DH, DW) in enumerate(CONV_SHAPES):
+        groups = 2 if IC % 2 == 0 else 1
+        conv = T.make_conv((1, IH, IW), (1, KH, KW), (1, SH, SW), (1, DH, DW), (0, PH, PW), IC,
+                           OC, groups)
+        inp = np.zeros((IC, IH, IW), np.int8)
+        r.tqtr_fill_uniform_i8(-128, 127, 42, p(inp), IC, IH * IW)
+        out["cf_%d_input" % i] = inp
+        out["cf_%d_groups" % i] = np.array([groups], np.int64)
+        for g in range(groups):
+            icg = IC // groups
+            K = icg * KH * KW
+            N = conv.output_shape[1] * conv.output_shape[2]
+            col = np.zeros((K, N), np.int8)
+            r.tqtr_im2col_cf_i8(g, p(inp), p(col), ctypes.byref(conv))
+            out["cf_%d_col_g%d" % (i, g)] = col
+    np.savez_compressed(os.path.join(HERE, "ref_im2col_cf.npz"),
                         shapes=np.array(CONV_SHAPES, np.int64), **out)
 
     # --- requantization multiplier (src/gemm/gemm_i8_i8/tqt_utils_i8_i8.h:98-132) ---

@@ -123,7 +123,7 @@ def test_offsets_follow_reference_formulas(dll):
 
 
 def test_interface_structs_bind_the_gfx950_variant(dll, shim):
-    out = (ctypes.c_size_t * 46)()  # five kernel types, then packed and output-type siblings
+    out = (ctypes.c_size_t * 58)()  # five kernel types, then packed and output-type siblings
     shim.tqts_steps_via_interfaces(out)
     for t, kind in enumerate(TYPES):
         assert out[2 * t] == getter(dll, "tqt_get_m_step_%s%s" % (TYPES[kind], V), 0)()

@@ -368,6 +368,67 @@ def test_w8a8dyn_sixteen_bit_difference_and_signed_zero():
     assert both.view(np.uint32)[0, 0] == 0  # -0 + -0 = -0, then vfmax(-0, +0) = +0
 
 
+def test_im2col_cf_vs_reference_golden():
+    """The channel-first im2col restatement reproduces the reference's tqt_im2col_cf byte for
+    byte on its conv shape list, every group."""
+    g = golden("ref_im2col_cf.npz")
+    for i, (IC, OC, IH, IW, KH, KW, SH, SW, PH, PW, DH, DW) in enumerate(g["shapes"]):
+        groups = int(g["cf_%d_groups" % i][0])
+        conv = T.make_conv((1, IH, IW), (1, KH, KW), (1, SH, SW), (1, DH, DW), (0, PH, PW),
+                           int(IC), int(OC), groups)
+        for grp in range(groups):
+            np.testing.assert_array_equal(T.oracle_im2col_cf(g["cf_%d_input" % i], conv, grp),
+                                          g["cf_%d_col_g%d" % (i, grp)])
+
+
+def test_mx1bias_is_the_transposed_w8a8():
+    """gemm_mx1bias (per-row weights scale, bias and requantization) equals the transpose of the
+    pinned W8A8 oracle (per-column scale, bias and requantization) with the operands swapped:
+    the same int32 sums, and multipliers from the same double product."""
+    m, n, k = 37, 45, 70
+    d = T.gen_mx1bias(m, n, k, seed=5, with_c=False)
+    got = T.oracle_mx1bias(d["A"], d["B"], None, d["bias"], -100, 110, d["scale_a"], m,
+                           d["scale_b"], d["scale_d"], d["zp_d"])
+    exp = T.oracle_w8a8(np.ascontiguousarray(d["B"].T), d["A"], None, d["bias"], -100, 110,
+                        d["scale_b"], d["scale_a"], m, d["scale_d"], d["zp_d"])
+    np.testing.assert_array_equal(got, exp.T)
+    # one shared multiplier (quant_channel_a == 1) and C
+    d = T.gen_mx1bias(m, n, k, seed=6, with_c=True, qca=1)
+    got = T.oracle_mx1bias(d["A"], d["B"], d["C"], d["bias"], -128, 127, d["scale_a"], 1,
+                           d["scale_b"], d["scale_d"], d["zp_d"])
+    exp = T.oracle_w8a8(np.ascontiguousarray(d["B"].T), d["A"], np.ascontiguousarray(d["C"].T),
+                        d["bias"], -128, 127, d["scale_b"], d["scale_a"], 1, d["scale_d"],
+                        d["zp_d"])
+    np.testing.assert_array_equal(got, exp.T)
+
+
+def test_igemmcf_is_im2col_cf_then_mx1bias():
+    """The implicit channel-first oracle on a pixel window [n_idx, n_idx + n) equals the
+    mx1bias GEMM on those columns of the (golden-pinned) channel-first im2col."""
+    rng = np.random.default_rng(8)
+    IC, OC, groups = 12, 10, 2
+    conv = T.make_conv((2, 9, 8), (1, 3, 3), (1, 2, 1), (1, 1, 2), (0, 1, 1), IC, OC, groups)
+    inp = rng.integers(-128, 128, size=(IC, 2, 9, 8), dtype=np.int64).astype(np.int8)
+    icg = IC // groups
+    K = icg * 9
+    N = conv.output_shape[0] * conv.output_shape[1] * conv.output_shape[2]
+    ocg = OC // groups
+    W = rng.integers(-127, 128, size=(ocg, K), dtype=np.int64).astype(np.int8)
+    bias = rng.integers(-500, 500, size=ocg, dtype=np.int64).astype(np.int32)
+    sa = rng.uniform(0.002, 0.01, size=ocg).astype(np.float32)
+    for grp in range(groups):
+        for n_idx, nn in ((0, N), (5, N - 9)):
+            D = np.zeros((ocg, N), np.int8)
+            T.oracle().tqto_igemmcf_qsi8dx(ocg, nn, T.ptr(inp), grp, n_idx, T.ptr(W), K, T.ptr(D),
+                                           N, T.ptr(bias), -128, 127, ctypes.byref(conv),
+                                           T.ptr(sa), ocg, 0.03, 0.1, 4)
+            col = T.oracle_im2col_cf(inp, conv, grp)
+            exp = T.oracle_mx1bias(W, np.ascontiguousarray(col[:, n_idx:n_idx + nn]), None, bias,
+                                   -128, 127, sa, ocg, 0.03, 0.1, 4)
+            np.testing.assert_array_equal(D[:, n_idx:n_idx + nn], exp)
+            assert not D[:, :n_idx].any() and not D[:, n_idx + nn:].any()
+
+
 def test_w4a16_rvv_numerics_within_reference_tolerance():
     """The RVV-numerics restatement (f16 weights, f16 FMA chain) stays within the reference
     test's own tolerance (abs 1.0, cosine 0.9999) of the f32 oracle on the reference inputs."""

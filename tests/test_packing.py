@@ -227,11 +227,12 @@ def test_packed_sizes_equal_unpacked_sizes(lib, mod):
 
 
 def test_packed_steps_via_interface_structs(lib, mod, shim):
-    out = (ctypes.c_size_t * 46)()
+    out = (ctypes.c_size_t * 58)()
     shim.tqts_steps_via_interfaces(out)
     kinds = (["clamp", "w8a8", "w4a8", "w4a16", "igemmcl"] + list(PACKED) +
              ["w4a8h", "w4a8hp", "w4a8b", "w4a8bp", "w4a16f", "w4a16fp", "w8dyn", "w8dynp",
-              "w8dynh", "w8dynhp", "convcl", "convclp"])
+              "w8dynh", "w8dynhp", "convcl", "convclp", "mx1", "mx1p", "convcf", "convcfp",
+              "igemmcf", "igemmcfp"])
     for t, kind in enumerate(kinds):
         assert out[2 * t] == _getter(lib, sym(mod, kind, "get_m_step"), 0)()
         assert out[2 * t + 1] == _getter(lib, sym(mod, kind, "get_n_step"), 0)()

@@ -121,6 +121,13 @@ def oracle():
                                               c_size, c_vp, c_size, c_vp, c_size, c_vp, u16,
                                               u16]),
         "tqto_im2col_cl_i8": (None, [c_size, c_vp, c_vp, ctypes.POINTER(ConvParamsC)]),
+        "tqto_im2col_cf_i8": (None, [c_size, c_vp, c_vp, ctypes.POINTER(ConvParamsC)]),
+        "tqto_gemm_mx1bias_qsi8dx": (None, [c_size] * 3 + [c_vp, c_size, c_vp, c_size, c_vp,
+                                                 c_size, c_vp, c_size, c_vp, i8, i8, c_vp, i32,
+                                                 f32, f32, i32]),
+        "tqto_igemmcf_qsi8dx": (None, [c_size, c_size, c_vp, c_size, c_size, c_vp, c_size, c_vp,
+                                        c_size, c_vp, i8, i8, ctypes.POINTER(ConvParamsC), c_vp,
+                                        i32, f32, f32, i32]),
         "tqto_igemmcl_qsi8cxt": (None, [c_size, c_size, c_vp, c_size, c_size, c_vp, c_size, c_vp,
                                          c_size, c_vp, i8, i8, ctypes.POINTER(ConvParamsC), f32,
                                          c_vp, i32, f32, i32]),
@@ -173,6 +180,7 @@ def ref():
         "tqtr_reference_conv_cl_f32": (None, [c_size, c_vp, c_vp, c_vp, c_vp,
                                                ctypes.POINTER(ConvParamsC), f32, f32]),
         "tqtr_im2col_cl_i8": (None, [c_size, c_vp, c_vp, ctypes.POINTER(ConvParamsC)]),
+        "tqtr_im2col_cf_i8": (None, [c_size, c_vp, c_vp, ctypes.POINTER(ConvParamsC)]),
         "tqtr_fill_uniform_f32": (None, [f32, f32, u32, c_vp, c_size, c_size]),
         "tqtr_fill_uniform_f16": (None, [f32, f32, u32, c_vp, c_size, c_size]),
         "tqtr_fill_uniform_i8": (None, [i8, i8, u32, c_vp, c_size, c_size]),
@@ -313,6 +321,44 @@ def gen_w8a8dyn(m, n, k, seed=42, zp_range=(-128, 127)):
         zp_a=rng.integers(zp_range[0], zp_range[1] + 1, size=m).astype(np.int32),
         scale_b=rng.uniform(0.001, 0.01, size=n).astype(np.float32),
         bias=rng.uniform(-10, 10, size=n).astype(np.float32))
+
+
+def oracle_im2col_cf(inp, conv, group_idx=0):
+    """Channel-first im2col of one group: [ICg*KD*KH*KW, OD*OH*OW] int8."""
+    icg = conv.input_channel // conv.groups
+    K = icg * conv.kernel_shape[0] * conv.kernel_shape[1] * conv.kernel_shape[2]
+    N = conv.output_shape[0] * conv.output_shape[1] * conv.output_shape[2]
+    col = np.zeros((K, N), np.int8)
+    oracle().tqto_im2col_cf_i8(group_idx, ptr(np.ascontiguousarray(inp)), ptr(col),
+                               ctypes.byref(conv))
+    return col
+
+
+def oracle_mx1bias(A, B, C, bias, cmin, cmax, scale_a, qca, scale_b, scale_d, zp_d):
+    """gemm_mx1bias: A [m, k] int8, B [k, n] int8, C int32 [m, n] or None, bias int32 [m]."""
+    m, k = A.shape
+    n = B.shape[1]
+    D = np.zeros((m, n), np.int8)
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    sa = np.ascontiguousarray(scale_a, np.float32)
+    oracle().tqto_gemm_mx1bias_qsi8dx(m, n, k, ptr(A), k, ptr(B), n, ptr(C), n, ptr(D), n,
+                                      ptr(bias), cmin, cmax, ptr(sa), qca, scale_b, scale_d, zp_d)
+    return D
+
+
+def gen_mx1bias(m, n, k, seed=42, with_c=False, qca=None):
+    """Weights A [m, k] with per-row scales, activations B [k, n], int32 bias [m]."""
+    rng = np.random.default_rng(seed)
+    return dict(
+        A=rng.integers(-127, 128, size=(m, k), dtype=np.int64).astype(np.int8),
+        B=rng.integers(-128, 128, size=(k, n), dtype=np.int64).astype(np.int8),
+        C=(rng.integers(-3000, 3001, size=(m, n), dtype=np.int64).astype(np.int32)
+           if with_c else None),
+        bias=rng.integers(-2000, 2001, size=m, dtype=np.int64).astype(np.int32),
+        scale_a=rng.uniform(0.001, 0.01, size=m).astype(np.float32),
+        qca=m if qca is None else qca,
+        scale_b=np.float32(0.02), scale_d=np.float32(0.08), zp_d=-5)
 
 
 def oracle_igemmcl(inp, W, bias, cmin, cmax, conv, scale_a, scale_b, qcb, scale_d, zp_d,

@@ -4,6 +4,9 @@
 //   igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt  (A gathered from an NDHWC image)
 //   gemm_1xnbias_clamp_{f32,f16}_qai8dx_qsi8cxt         (per-row dynamically quantized A,
 //                                                        f32 / f16 out)
+//   gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8      (weights x [k, n] activations, per-row
+//                                                        bias and requantization)
+//   igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8   (B gathered from an NCDHW image)
 // and their packed siblings.
 //
 // Three kernels, chosen per call:
@@ -29,6 +32,11 @@
 #include "tqt_gemm_1xnbias_clamp_f16_qai8dx_qsi8cxt_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi8cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi8cxp_mfma_gfx950.h"
+#include "tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950.h"
+#include "tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950.h"
+#include "tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950.h"
+#include "tqt_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950.h"
+#include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -40,8 +48,18 @@ constexpr int kPrefetch = 4;  // k-steps in flight in registers (int8_mfma_kerne
 constexpr int kConvMaxChunks = 1024;  // fast implicit convolution: k <= 16384
 
 enum AMode { A_MATRIX = 0, A_CONV_CL = 1 };
-enum BMode { B_NK = 0, B_KN = 1 };
-enum EpiMode { EPI_CLAMP_I32 = 0, EPI_REQUANT_I8 = 1, EPI_DYN_F32 = 2, EPI_DYN_F16 = 3 };
+// B_CF: B is the channel-first im2col [K, N] of an NCDHW input, gathered on the fly
+// (k = (ic, kd, kh, kw), n = output pixel p0 + column)
+enum BMode { B_NK = 0, B_KN = 1, B_CF = 2 };
+// EPI_REQUANT_ROW: the requantization of EPI_REQUANT_I8 with its bias and multiplier per row
+// (gemm_mx1bias: the scale array belongs to A, the scalar scale to B)
+enum EpiMode {
+    EPI_CLAMP_I32 = 0,
+    EPI_REQUANT_I8 = 1,
+    EPI_DYN_F32 = 2,
+    EPI_DYN_F16 = 3,
+    EPI_REQUANT_ROW = 4
+};
 
 __host__ __device__ constexpr bool is_dyn(int epi)
 {
@@ -58,7 +76,7 @@ struct ConvGeom
 {
     int ID, IH, IW;
     int OH, OW;
-    int KH, KW;
+    int KD, KH, KW;
     int SD, SH, SW;
     int DD, DH, DW;
     int PD, PH, PW;
@@ -71,16 +89,18 @@ struct Int8Args
     int M, N, K;
     const int8_t *A;  // matrix A, or the group's channel base of the NDHWC input
     long long lda;
-    const int8_t *B;
+    const int8_t *B;  // matrix B, or (B_CF) the group's base of the NCDHW input
     long long ldb;
     const int32_t *C;
     long long ldc;
     void *D;
     long long ldd;
     long long d_row0;  // igemmcl: D row of local pixel 0 (= m_idx); 0 otherwise
-    long long p0;      // igemmcl: global pixel index of local pixel 0 (= m_idx)
+    long long p0;      // igemmcl / igemmcf: global pixel index of local pixel 0
     const int32_t *bias;
     int32_t cmin, cmax;
+    // requantization: multiplier of column j (row i for EPI_REQUANT_ROW) from
+    // scale_a * scale_b[j or 0] / scale_d (quant_channel_b == 1: index 0)
     float scale_a;
     const float *scale_b;
     int32_t quant_channel_b;
@@ -172,6 +192,37 @@ __device__ __forceinline__ int lds_off(int row, int chunk)
     return row * kBK + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
+// Byte (k, pixel (od, oh, ow)) of the channel-first im2col of the input at a.B (0 for a padding
+// tap). Every load reads valid memory: a padding tap reads the plane's first byte.
+__device__ __forceinline__ uint32_t cf_byte(const Int8Args &a, const int8_t *plane, int kd,
+                                            int kh, int kw, int od, int oh, int ow, bool ok)
+{
+    const ConvGeom &g = a.cv;
+    const int id = od * g.SD + kd * g.DD - g.PD;
+    const int ih = oh * g.SH + kh * g.DH - g.PH;
+    const int iw = ow * g.SW + kw * g.DW - g.PW;
+    ok = ok && id >= 0 && id < g.ID && ih >= 0 && ih < g.IH && iw >= 0 && iw < g.IW;
+    const long long off = ok ? (static_cast<long long>(id) * g.IH + ih) * g.IW + iw : 0;
+    const uint32_t v = static_cast<uint8_t>(plane[off]);
+    return ok ? v : 0u;
+}
+
+// Tap of channel-first im2col row k: the input channel's plane and (kd, kh, kw).
+__device__ __forceinline__ const int8_t *cf_tap(const Int8Args &a, int k, int &kd, int &kh,
+                                                int &kw)
+{
+    const ConvGeom &g = a.cv;
+    const int khw = g.KH * g.KW;
+    const int kdhw = g.KD * khw;
+    const int ic = k / kdhw;
+    int r = k - ic * kdhw;
+    kd = r / khw;
+    r -= kd * khw;
+    kh = r / g.KW;
+    kw = r - kh * g.KW;
+    return a.B + static_cast<long long>(ic) * g.ID * g.IH * g.IW;
+}
+
 template <int BM, int AM, int BMd, int EPI, int PK>
 __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 {
@@ -223,6 +274,11 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, n0 + tid,
                                   s_mult[tid], s_shift[tid]);
         }
+    } else if constexpr (EPI == EPI_REQUANT_ROW) {
+        if (tid < BM && m0 + tid < a.M) {
+            column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, m0 + tid,
+                                  s_mult[tid], s_shift[tid]);
+        }
     }
 
     // Per-thread load assignment (fixed across the K loop): 4 consecutive threads read one row's
@@ -266,6 +322,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     int b_row[B_CHUNKS], b_chk[B_CHUNKS], b_mul[B_CHUNKS];
     bool b_ok[B_CHUNKS];
     const int8_t *b_ptr[B_CHUNKS];
+    [[maybe_unused]] int b_od[B_CHUNKS], b_oh[B_CHUNKS], b_ow[B_CHUNKS];
 #pragma unroll
     for (int j = 0; j < B_CHUNKS; ++j) {
         const int c = tid + j * kThreads;
@@ -293,6 +350,14 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             b_ok[j] = gn < a.N;
             b_mul[j] = 1;
             b_ptr[j] = a.B + (b_ok[j] ? gn : 0);
+            if constexpr (BMd == B_CF) {
+                // output pixel of the chunk's first column
+                const long long p = a.p0 + (b_ok[j] ? gn : 0);
+                const long long ohw = static_cast<long long>(a.cv.OH) * a.cv.OW;
+                b_od[j] = static_cast<int>(p / ohw);
+                b_oh[j] = static_cast<int>((p / a.cv.OW) % a.cv.OH);
+                b_ow[j] = static_cast<int>(p % a.cv.OW);
+            }
         }
     }
 
@@ -336,7 +401,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                 st.b[j] = *reinterpret_cast<const i32x4 *>(
                     ok ? b_ptr[j] + pack_k<kPackI8Chunk, (PK & PK_B) != 0>(k0, b_mul[j]) : a.B);
                 st.bm |= ok ? (1u << j) : 0u;
-            } else {
+            } else if constexpr (BMd == B_KN) {
                 const int k = k0 + b_row[j];
                 const int gn = n0 + b_chk[j] * 16;
                 const bool ok = b_ok[j] && k < a.K;
@@ -351,6 +416,30 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                     }
                     st.b[j] = tmp;
                 }
+                st.bm |= ok ? (1u << j) : 0u;
+            } else {
+                // 16 consecutive output pixels of one channel-first im2col row, gathered
+                const int k = k0 + b_row[j];
+                const int gn = n0 + b_chk[j] * 16;
+                const bool ok = b_ok[j] && k < a.K;
+                int kd, kh, kw;
+                const int8_t *plane = cf_tap(a, ok ? k : 0, kd, kh, kw);
+                int od = b_od[j], oh = b_oh[j], ow = b_ow[j];
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    w[i >> 2] |= cf_byte(a, plane, kd, kh, kw, od, oh, ow, ok && gn + i < a.N)
+                                 << (8 * (i & 3));
+                    if (++ow == a.cv.OW) {
+                        ow = 0;
+                        if (++oh == a.cv.OH) {
+                            oh = 0;
+                            ++od;
+                        }
+                    }
+                }
+                st.b[j] = i32x4{static_cast<int>(w[0]), static_cast<int>(w[1]),
+                                static_cast<int>(w[2]), static_cast<int>(w[3])};
                 st.bm |= ok ? (1u << j) : 0u;
             }
         }
@@ -430,7 +519,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
     // step j with j % PF == s; the sets rotate by unrolling, since a register copy would wait
     // for the load still filling it). Loads past the last step reload it, so every load is
     // unconditional and the compiler tracks each set's loads exactly.
-    constexpr int PF = BMd == B_KN ? 2 : kPrefetch;  // the K x N transpose needs the registers
+    constexpr int PF = BMd != B_NK ? 2 : kPrefetch;  // the K x N transpose needs the registers
     Step ps[PF];
     auto step_k0 = [&](int st) { return min(st, nk - 1) * kBK; };
     if (nk > 0) {
@@ -531,8 +620,9 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                 if (a.C) {
                     v += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
                 }
+                constexpr bool kRow = EPI == EPI_REQUANT_ROW;
                 if (a.bias) {
-                    v += static_cast<uint32_t>(a.bias[gn]);
+                    v += static_cast<uint32_t>(a.bias[kRow ? gm : gn]);
                 }
                 const long long drow = a.d_row0 + gm;
                 if constexpr (EPI == EPI_CLAMP_I32) {
@@ -541,8 +631,9 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                     x = x > a.cmax ? a.cmax : x;
                     static_cast<int32_t *>(a.D)[drow * a.ldd + gn] = x;
                 } else {
+                    const int q = kRow ? gm - m0 : lc;
                     static_cast<int8_t *>(a.D)[drow * a.ldd + gn] = requant_dev(
-                        static_cast<int32_t>(v), s_mult[lc], s_shift[lc], a.zp_d, a.cmin, a.cmax);
+                        static_cast<int32_t>(v), s_mult[q], s_shift[q], a.zp_d, a.cmin, a.cmax);
                 }
             }
         }
@@ -608,6 +699,11 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     if constexpr (EPI == EPI_REQUANT_I8) {
         if (tid < kBN && n0 + tid < a.N) {
             column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, n0 + tid,
+                                  s_mult[tid], s_shift[tid]);
+        }
+    } else if constexpr (EPI == EPI_REQUANT_ROW) {
+        if (tid < BM && m0 + tid < a.M) {
+            column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, m0 + tid,
                                   s_mult[tid], s_shift[tid]);
         }
     }
@@ -839,7 +935,8 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         if (gn >= a.N) {
             continue;
         }
-        const uint32_t bias = a.bias ? static_cast<uint32_t>(a.bias[gn]) : 0u;
+        constexpr bool kRow = EPI == EPI_REQUANT_ROW;
+        const uint32_t bias = (a.bias && !kRow) ? static_cast<uint32_t>(a.bias[gn]) : 0u;
         int32_t mult = 0, shift = 0;
         if constexpr (EPI == EPI_REQUANT_I8) {
             mult = s_mult[lc];
@@ -854,6 +951,13 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
                     continue;
                 }
                 uint32_t v = static_cast<uint32_t>(acc[i][j][r]) + bias;
+                if constexpr (kRow) {
+                    mult = s_mult[gm - m0];
+                    shift = s_shift[gm - m0];
+                    if (a.bias) {
+                        v += static_cast<uint32_t>(a.bias[gm]);
+                    }
+                }
                 if (a.C) {
                     v += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
                 }
@@ -891,19 +995,52 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     if constexpr (AM == A_MATRIX) {
         if constexpr (PK == PK_NONE) {
             const int8_t *arow = a.A + static_cast<long long>(gm) * a.lda;
-            for (int k = 0; k < a.K; ++k) {
-                const int32_t bv = (BMd == B_NK) ? a.B[static_cast<long long>(gn) * a.ldb + k]
-                                                 : a.B[static_cast<long long>(k) * a.ldb + gn];
-                acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * bv);
+            if constexpr (BMd == B_CF) {
+                const long long p = a.p0 + gn;
+                const long long ohw = static_cast<long long>(a.cv.OH) * a.cv.OW;
+                const int od = static_cast<int>(p / ohw);
+                const int oh = static_cast<int>((p / a.cv.OW) % a.cv.OH);
+                const int ow = static_cast<int>(p % a.cv.OW);
+                for (int k = 0; k < a.K; ++k) {
+                    int kd, kh, kw;
+                    const int8_t *plane = cf_tap(a, k, kd, kh, kw);
+                    const int32_t bv = static_cast<int8_t>(
+                        static_cast<uint8_t>(cf_byte(a, plane, kd, kh, kw, od, oh, ow, true)));
+                    acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * bv);
+                }
+            } else {
+                for (int k = 0; k < a.K; ++k) {
+                    const int32_t bv = (BMd == B_NK) ? a.B[static_cast<long long>(gn) * a.ldb + k]
+                                                     : a.B[static_cast<long long>(k) * a.ldb + gn];
+                    acc += static_cast<uint32_t>(static_cast<int32_t>(arow[k]) * bv);
+                }
             }
         } else {
             // packed operands (B_NK): the same sum, addressed through the panel layout; the run
             // functions of the p-variants describe an unpacked operand with step 0 (row-major)
             const PackRow ra = pack_row_info(a.pa, gm);
             const PackRow rb = pack_row_info(a.pb, gn);
-            for (int k = 0; k < a.K; ++k) {
-                acc += static_cast<uint32_t>(static_cast<int32_t>(a.A[pack_row_byte(ra, k)]) *
-                                             static_cast<int32_t>(a.B[pack_row_byte(rb, k)]));
+            if constexpr (BMd == B_CF) {
+                // packed weights (A) times the gathered channel-first im2col
+                const long long p = a.p0 + gn;
+                const long long ohw = static_cast<long long>(a.cv.OH) * a.cv.OW;
+                const int od = static_cast<int>(p / ohw);
+                const int oh = static_cast<int>((p / a.cv.OW) % a.cv.OH);
+                const int ow = static_cast<int>(p % a.cv.OW);
+                for (int k = 0; k < a.K; ++k) {
+                    int kd, kh, kw;
+                    const int8_t *plane = cf_tap(a, k, kd, kh, kw);
+                    const int32_t bv = static_cast<int8_t>(
+                        static_cast<uint8_t>(cf_byte(a, plane, kd, kh, kw, od, oh, ow, true)));
+                    acc += static_cast<uint32_t>(
+                        static_cast<int32_t>(a.A[pack_row_byte(ra, k)]) * bv);
+                }
+            } else {
+                for (int k = 0; k < a.K; ++k) {
+                    acc += static_cast<uint32_t>(
+                        static_cast<int32_t>(a.A[pack_row_byte(ra, k)]) *
+                        static_cast<int32_t>(a.B[pack_row_byte(rb, k)]));
+                }
             }
         }
     } else {
@@ -940,8 +1077,9 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     if (a.C) {
         acc += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
     }
+    constexpr bool kRow = EPI == EPI_REQUANT_ROW;
     if (a.bias) {
-        acc += static_cast<uint32_t>(a.bias[gn]);
+        acc += static_cast<uint32_t>(a.bias[kRow ? gm : gn]);
     }
     const long long drow = a.d_row0 + gm;
     if constexpr (EPI == EPI_CLAMP_I32) {
@@ -951,7 +1089,8 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
         static_cast<int32_t *>(a.D)[drow * a.ldd + gn] = x;
     } else {
         int32_t mult, shift;
-        column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, gn, mult, shift);
+        column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, kRow ? gm : gn,
+                              mult, shift);
         static_cast<int8_t *>(a.D)[drow * a.ldd + gn] =
             requant_dev(static_cast<int32_t>(acc), mult, shift, a.zp_d, a.cmin, a.cmax);
     }
@@ -1081,6 +1220,7 @@ void igemm_run(size_t m, size_t n, const void *input, size_t group_idx, size_t m
     g.IW = static_cast<int>(p.input_shape[2]);
     g.OH = static_cast<int>(p.output_shape[1]);
     g.OW = static_cast<int>(p.output_shape[2]);
+    g.KD = static_cast<int>(p.kernel_shape[0]);
     g.KH = static_cast<int>(p.kernel_shape[1]);
     g.KW = static_cast<int>(p.kernel_shape[2]);
     g.SD = static_cast<int>(p.stride[0]);
@@ -1202,6 +1342,95 @@ void dyn_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_i
     const bool fast = (k % 16 == 0) && (lda % 16 == 0) && (ldb % 16 == 0) && aligned16(A) &&
                       aligned16(B);
     launch_int8<A_MATRIX, B_NK, EPI>(a, fast, stream, where);
+}
+
+// Requantization fields of the mx1bias types: the per-row scale array (weights, A) takes the
+// place of the per-column one, the activation's scalar scale that of scale_a, so that
+// column_multiplier_dev computes scale_a[i] * scale_b / scale_d (reference
+// …mx1bias…qsi8dx_qai8_4x1vl_rvv.cpp run: tqt_quantize_multiplier per row, shift = -shift - 1).
+void set_mx1bias(Int8Args &a, const void *bias, int8_t clamp_min, int8_t clamp_max,
+                 const struct tqt_qai8_qsi8dx_qai8_params *p)
+{
+    TQT_REQUIRE(p->scale_a != nullptr, "params->scale_a == NULL");
+    a.bias = static_cast<const int32_t *>(bias);
+    a.cmin = clamp_min;
+    a.cmax = clamp_max;
+    a.scale_a = p->scale_b;
+    a.scale_b = p->scale_a;
+    a.quant_channel_b = p->quant_channel_a;
+    a.scale_d = p->scale_d;
+    a.zp_d = p->zero_point_d;
+}
+
+// Shared body of the igemmcf runs: output channels m (rows of the weights) times output pixels
+// [n_idx, n_idx + n) of the channel-first im2col of group group_idx, gathered from the NCDHW
+// input; D rows at D + i * ldd + n_idx. `packed`: the weights are in the packed layout.
+void igemmcf_run(size_t m, size_t n, const void *input, size_t group_idx, size_t n_idx,
+                 const void *A, size_t lda, size_t k_idx_a, void *D, size_t ldd, const void *bias,
+                 int8_t clamp_min, int8_t clamp_max, const tqt_conv_params *conv_params,
+                 const struct tqt_qai8_qsi8dx_qai8_params *quant_params, bool packed,
+                 hipStream_t stream, const char *where)
+{
+    if (!conv_params || !quant_params) {
+        return;  // reference …igemmcf…qsi8dx_qai8_1vlx4_rvv.cpp run: !conv_params || !params
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    const tqt_conv_params &p = *conv_params;
+    TQT_REQUIRE(p.groups >= 1 && p.input_channel % p.groups == 0, "input_channel % groups != 0");
+    TQT_REQUIRE(input != nullptr && A != nullptr && D != nullptr, "NULL tensor pointer");
+    for (int i = 0; i < 3; ++i) {
+        TQT_REQUIRE(p.input_shape[i] < (1u << 30) && p.output_shape[i] < (1u << 30) &&
+                        p.kernel_shape[i] < (1u << 15) && p.stride[i] < (1u << 15) &&
+                        p.dilation[i] < (1u << 15) && p.pad[i] < (1u << 15),
+                    "conv geometry out of range");
+    }
+    const size_t icg = p.input_channel / p.groups;
+    const size_t plane = p.input_shape[0] * p.input_shape[1] * p.input_shape[2];
+    const size_t kfull = p.kernel_shape[0] * p.kernel_shape[1] * p.kernel_shape[2] * icg;
+    const size_t npix = p.output_shape[0] * p.output_shape[1] * p.output_shape[2];
+    TQT_REQUIRE(n_idx + n <= npix, "n_idx + n exceeds the output pixels");
+    Int8Args a = base_args(m, n, kfull);
+    a.A = static_cast<const int8_t *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const int8_t *>(input) + group_idx * icg * plane;
+    a.D = static_cast<int8_t *>(D) + n_idx;
+    a.ldd = static_cast<long long>(ldd);
+    a.p0 = static_cast<long long>(n_idx);
+    set_mx1bias(a, bias, clamp_min, clamp_max, quant_params);
+    ConvGeom &g = a.cv;
+    g.ID = static_cast<int>(p.input_shape[0]);
+    g.IH = static_cast<int>(p.input_shape[1]);
+    g.IW = static_cast<int>(p.input_shape[2]);
+    g.OH = static_cast<int>(p.output_shape[1]);
+    g.OW = static_cast<int>(p.output_shape[2]);
+    g.KD = static_cast<int>(p.kernel_shape[0]);
+    g.KH = static_cast<int>(p.kernel_shape[1]);
+    g.KW = static_cast<int>(p.kernel_shape[2]);
+    g.SD = static_cast<int>(p.stride[0]);
+    g.SH = static_cast<int>(p.stride[1]);
+    g.SW = static_cast<int>(p.stride[2]);
+    g.DD = static_cast<int>(p.dilation[0]);
+    g.DH = static_cast<int>(p.dilation[1]);
+    g.DW = static_cast<int>(p.dilation[2]);
+    g.PD = static_cast<int>(p.pad[0]);
+    g.PH = static_cast<int>(p.pad[1]);
+    g.PW = static_cast<int>(p.pad[2]);
+    g.IC = static_cast<int>(p.input_channel);
+    g.ICg = static_cast<int>(icg);
+    TQT_REQUIRE(g.OH > 0 && g.OW > 0 && kfull > 0, "empty conv geometry");
+    // fast path: whole 16-byte weight chunks (the gathered B side has no alignment needs)
+    if (packed) {
+        TQT_REQUIRE(lda >= kfull, "lda < k");
+        a.pa = make_pack(kPackI8MStep, kPackI8Chunk, m, lda, kfull, k_idx_a);
+        const bool fast = kfull % 16 == 0 && kfull < (1u << 24) && aligned16(A) &&
+                          k_idx_a % 16 == 0;
+        launch_int8<A_MATRIX, B_CF, EPI_REQUANT_ROW, PK_A>(a, fast, stream, where);
+    } else {
+        const bool fast = kfull % 16 == 0 && lda % 16 == 0 && aligned16(A);
+        launch_int8<A_MATRIX, B_CF, EPI_REQUANT_ROW>(a, fast, stream, where);
+    }
 }
 
 }  // namespace
@@ -1635,6 +1864,354 @@ void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx95
         clamp_min, clamp_max, conv_params, quant_params, nullptr);
     finish_sync(nullptr,
                 "tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx950");
+}
+
+// =============================================================================================
+// gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8 (reference …/gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_4x1vl_rvv.cpp): weights A [m, k] (per-row
+// scale) times activations B [k, n], int32 C (optional) and Mx1 bias, per-row requantization
+// =============================================================================================
+static const size_t kMx1MStep = 128;
+static const size_t kMx1NStep = 128;
+
+size_t tqt_get_m_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(void)
+{
+    return kMx1MStep;
+}
+size_t tqt_get_n_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(void)
+{
+    return kMx1NStep;
+}
+size_t tqt_get_a_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    return (m_idx * lda + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_b_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb)
+{
+    TQT_REQUIRE(n_idx % kMx1NStep == 0, "n_idx % n_step == 0");
+    return (k_idx * ldb + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_c_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kMx1NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_bias_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    return m_idx * sizeof(int32_t);
+}
+size_t tqt_get_d_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kMx1NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_d_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(int8_t);
+}
+
+void tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qsi8dx_qai8_params *params,
+    void *stream)
+{
+    (void)k_idx_a;
+    (void)k_idx_b;
+    if (!params) {
+        return;  // reference …mx1bias…qsi8dx_qai8_4x1vl_rvv.cpp run: if (!params) return
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    TQT_REQUIRE(A != nullptr || k == 0, "A == NULL");
+    TQT_REQUIRE(B != nullptr || k == 0, "B == NULL");
+    TQT_REQUIRE(D != nullptr, "D == NULL");
+    Int8Args a = base_args(m, n, k);
+    a.A = static_cast<const int8_t *>(A);
+    a.lda = static_cast<long long>(lda);
+    a.B = static_cast<const int8_t *>(B);
+    a.ldb = static_cast<long long>(ldb);
+    a.C = static_cast<const int32_t *>(C);
+    a.ldc = static_cast<long long>(ldc);
+    a.D = D;
+    a.ldd = static_cast<long long>(ldd);
+    set_mx1bias(a, bias, clamp_min, clamp_max, params);
+    const bool fast = (k % 16 == 0) && (lda % 16 == 0) && (ldb % 16 == 0) && aligned16(A) &&
+                      aligned16(B);
+    launch_int8<A_MATRIX, B_KN, EPI_REQUANT_ROW>(a, fast, as_stream(stream),
+                                                 "tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950");
+}
+
+void tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
+    size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
+    int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qsi8dx_qai8_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950_async(m, n, k, A, lda, k_idx_a, B, ldb, k_idx_b, C, ldc, D, ldd,
+                                    bias, clamp_min, clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950");
+}
+
+// =============================================================================================
+// gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p (reference …/gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_4x1vl_rvv.cpp): the packed layout and packers of
+// gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp (weights are the packed A rows, activations the packed B rows)
+// =============================================================================================
+size_t tqt_get_m_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(void)
+{
+    return kPackI8MStep;
+}
+size_t tqt_get_n_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(void)
+{
+    return kPackI8NStep;
+}
+size_t tqt_get_a_packed_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda,
+                                                  size_t actual_m)
+{
+    return tqt_get_a_packed_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(m_idx, k_idx, lda, actual_m);
+}
+size_t tqt_get_b_packed_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t n_idx, size_t k_idx, size_t ldb,
+                                                  size_t actual_n)
+{
+    return tqt_get_b_packed_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(n_idx, k_idx, ldb, actual_n);
+}
+size_t tqt_get_c_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kPackI8MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kPackI8NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_bias_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t m_idx)
+{
+    TQT_REQUIRE(m_idx % kPackI8MStep == 0, "m_idx % m_step == 0");
+    return m_idx * sizeof(int32_t);
+}
+size_t tqt_get_d_offset_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kPackI8MStep == 0, "m_idx % m_step == 0");
+    TQT_REQUIRE(n_idx % kPackI8NStep == 0, "n_idx % n_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_d_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(int8_t);
+}
+size_t tqt_get_a_packed_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t m, size_t k)
+{
+    return m * k;
+}
+size_t tqt_get_b_packed_size_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t n, size_t k)
+{
+    return n * k;
+}
+#define TQT_MX1_PACKER(ACTION, R)                                                                  \
+    void tqt_##ACTION##_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950_async(                            \
+        size_t R, size_t k, size_t ld, size_t ld_packed, size_t k_idx, const void *src, void *dst, \
+        void *stream)                                                                              \
+    {                                                                                              \
+        tqt_##ACTION##_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950_async(R, k, ld, ld_packed, k_idx,    \
+                                                                       src, dst, stream);          \
+    }                                                                                              \
+    void tqt_##ACTION##_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(size_t R, size_t k, size_t ld,    \
+                                                                     size_t ld_packed,             \
+                                                                     size_t k_idx,                 \
+                                                                     const void *src, void *dst)   \
+    {                                                                                              \
+        tqt_##ACTION##_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(R, k, ld, ld_packed, k_idx, src,     \
+                                                                 dst);                             \
+    }
+TQT_MX1_PACKER(run_a_pack, m)
+TQT_MX1_PACKER(run_b_pack, n)
+TQT_MX1_PACKER(run_bt_pack, n)
+#undef TQT_MX1_PACKER
+
+void tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const struct tqt_qai8_qsi8dx_qai8_params *params, void *stream)
+{
+    if (!params) {
+        return;
+    }
+    if (m == 0 || n == 0) {
+        return;
+    }
+    Int8Args a = base_args(m, n, k);
+    set_mx1bias(a, bias, clamp_min, clamp_max, params);
+    packed_gemm_run<EPI_REQUANT_ROW>(m, n, k, A_packed, lda, k_idx_a, true, B_packed, ldb,
+                                     k_idx_b, C, ldc, D, ldd, a, as_stream(stream),
+                                     "tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950");
+}
+
+void tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *A_packed, size_t lda, size_t k_idx_a,
+    const void *B_packed, size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const struct tqt_qai8_qsi8dx_qai8_params *params)
+{
+    if (!params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950_async(m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C,
+                                     ldc, D, ldd, bias, clamp_min, clamp_max, params, nullptr);
+    finish_sync(nullptr, "tqt_run_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p_mfma_gfx950");
+}
+
+// =============================================================================================
+// igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8 (reference …/igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_1vlx4_rvv.cpp) and its packed-weights
+// sibling igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8: the mx1bias GEMM with B gathered from the
+// channel-first input
+// =============================================================================================
+size_t tqt_get_m_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(void)
+{
+    return kMx1MStep;
+}
+size_t tqt_get_n_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(void)
+{
+    return kMx1NStep;
+}
+size_t tqt_get_a_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    return (m_idx * lda + k_idx) * sizeof(int8_t);
+}
+size_t tqt_get_c_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_bias_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    return m_idx * sizeof(int32_t);
+}
+size_t tqt_get_d_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kMx1MStep == 0, "m_idx % m_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_d_size_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(int8_t);
+}
+
+void tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t n_idx,
+    size_t k_idx_b, const void *A, size_t lda, size_t k_idx_a, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qsi8dx_qai8_params *quant_params,
+    void *stream)
+{
+    (void)k;
+    (void)k_idx_b;
+    (void)k_idx_a;
+    (void)C;
+    (void)ldc;
+    igemmcf_run(m, n, input, group_idx, n_idx, A, lda, 0, D, ldd, bias, clamp_min, clamp_max,
+                conv_params, quant_params, false, as_stream(stream),
+                "tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950");
+}
+
+void tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t n_idx,
+    size_t k_idx_b, const void *A, size_t lda, size_t k_idx_a, const void *C, size_t ldc, void *D,
+    size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qsi8dx_qai8_params *quant_params)
+{
+    if (!conv_params || !quant_params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950_async(m, n, k, input, group_idx, n_idx, k_idx_b, A, lda,
+                                           k_idx_a, C, ldc, D, ldd, bias, clamp_min, clamp_max,
+                                           conv_params, quant_params, nullptr);
+    finish_sync(nullptr, "tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950");
+}
+
+size_t tqt_get_m_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(void)
+{
+    return kPackI8MStep;
+}
+size_t tqt_get_n_step_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(void)
+{
+    return kMx1NStep;
+}
+size_t tqt_get_a_packed_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(size_t m_idx, size_t k_idx, size_t lda,
+                                                   size_t actual_m)
+{
+    return tqt_get_a_packed_offset_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(m_idx, k_idx, lda, actual_m);
+}
+size_t tqt_get_c_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldc)
+{
+    TQT_REQUIRE(m_idx % kPackI8MStep == 0, "m_idx % m_step == 0");
+    return (m_idx * ldc + n_idx) * sizeof(int32_t);
+}
+size_t tqt_get_bias_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(size_t m_idx)
+{
+    TQT_REQUIRE(m_idx % kPackI8MStep == 0, "m_idx % m_step == 0");
+    return m_idx * sizeof(int32_t);
+}
+size_t tqt_get_d_offset_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(size_t m_idx, size_t n_idx, size_t ldd)
+{
+    TQT_REQUIRE(m_idx % kPackI8MStep == 0, "m_idx % m_step == 0");
+    return (m_idx * ldd + n_idx) * sizeof(int8_t);
+}
+size_t tqt_get_d_size_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(size_t m, size_t n)
+{
+    return m * n * sizeof(int8_t);
+}
+size_t tqt_get_a_packed_size_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(size_t m, size_t k)
+{
+    return m * k;
+}
+void tqt_run_a_pack_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950_async(size_t m, size_t k, size_t ldw, size_t ldw_packed,
+                                              size_t k_idx, const void *weight,
+                                              void *weight_packed, void *stream)
+{
+    tqt_run_a_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950_async(m, k, ldw, ldw_packed, k_idx, weight, weight_packed,
+                                             stream);
+}
+void tqt_run_a_pack_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(size_t m, size_t k, size_t ldw, size_t ldw_packed,
+                                        size_t k_idx, const void *weight, void *weight_packed)
+{
+    tqt_run_a_pack_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_mfma_gfx950(m, k, ldw, ldw_packed, k_idx, weight, weight_packed);
+}
+
+void tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950_async(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t n_idx,
+    size_t k_idx_b, const void *A_packed, size_t lda, size_t k_idx_a, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qsi8dx_qai8_params *quant_params,
+    void *stream)
+{
+    (void)k;
+    (void)k_idx_b;
+    (void)C;
+    (void)ldc;
+    igemmcf_run(m, n, input, group_idx, n_idx, A_packed, lda, k_idx_a, D, ldd, bias, clamp_min,
+                clamp_max, conv_params, quant_params, true, as_stream(stream),
+                "tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950");
+}
+
+void tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950(
+    size_t m, size_t n, size_t k, const void *input, size_t group_idx, size_t n_idx,
+    size_t k_idx_b, const void *A_packed, size_t lda, size_t k_idx_a, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, int8_t clamp_min, int8_t clamp_max,
+    const tqt_conv_params *conv_params, const struct tqt_qai8_qsi8dx_qai8_params *quant_params)
+{
+    if (!conv_params || !quant_params || m == 0 || n == 0) {
+        return;
+    }
+    tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950_async(m, n, k, input, group_idx, n_idx, k_idx_b, A_packed,
+                                            lda, k_idx_a, C, ldc, D, ldd, bias, clamp_min,
+                                            clamp_max, conv_params, quant_params, nullptr);
+    finish_sync(nullptr, "tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950");
 }
 
 static const size_t kDynMStep = 128;

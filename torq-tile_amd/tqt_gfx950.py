@@ -48,6 +48,13 @@ KERNELS = {
     # explicit-im2col convolution (channel-last): im2col (or im2col + pack) and the W8A8 GEMM
     "convcl": "convcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt",
     "convclp": "convcl_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp",
+    # channel-first int8: weights x [k, n] activations with per-row (Mx1) bias and requantization
+    "mx1": "gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8",
+    "mx1p": "gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p",
+    "convcf": "convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8",
+    "convcfp": "convcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8p",
+    "igemmcf": "igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8",
+    "igemmcfp": "igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8",
 }
 
 
@@ -74,6 +81,19 @@ class QAI8DXPQSI8CXPParams(ctypes.Structure):
     """struct tqt_qai8dxp_qsi8cxp_params (reference tqt_params_i8_i8.h:45-50)."""
 
     _fields_ = [("scale_a", c_vp), ("zero_point_a", c_vp), ("scale_b", c_vp)]
+
+
+class QAI8QSI8DXQAI8Params(ctypes.Structure):
+    """struct tqt_qai8_qsi8dx_qai8_params (reference tqt_params_i8_i8.h:28-36)."""
+
+    _fields_ = [
+        ("scale_a", c_vp),
+        ("quant_channel_a", ctypes.c_int32),
+        ("scale_b", ctypes.c_float),
+        ("zero_point_b", ctypes.c_int32),
+        ("scale_d", ctypes.c_float),
+        ("zero_point_d", ctypes.c_int32),
+    ]
 
 
 class ConvParams(ctypes.Structure):
@@ -306,6 +326,74 @@ _SIGS["convclp"] = {
     "run_a_im2colpack_async": (None, _IM2COLPACK + [c_vp]),
     "run_conv": _SIGS["w8a8p"]["run"],
     "run_conv_async": _SIGS["w8a8p"]["run_async"],
+}
+_MX1_REQ = [c_vp, ctypes.c_int8, ctypes.c_int8, ctypes.POINTER(QAI8QSI8DXQAI8Params)]
+_SIGS["mx1"] = {a: v for a, v in _SIGS["w8a8"].items() if not a.startswith("run")}
+_SIGS["mx1"].update(run=(None, _GEMM_I8_ARGS + _MX1_REQ),
+                    run_async=(None, _GEMM_I8_ARGS + _MX1_REQ + [c_vp]))
+_SIGS["mx1p"] = _packed_sigs(
+    "mx1", ["run_a_pack", "run_b_pack", "run_bt_pack"], _GEMM_I8_ARGS + _MX1_REQ,
+    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
+_SIGS["convcf"] = {
+    "get_m_step": (c_size, []),
+    "get_n_step": (c_size, []),
+    "get_a_offset": (c_size, [c_size] * 3),
+    "get_c_offset": (c_size, [c_size] * 3),
+    "get_bias_offset": (c_size, [c_size]),
+    "get_d_offset": (c_size, [c_size] * 3),
+    "get_d_size": (c_size, [c_size] * 2),
+    "get_b_im2col_size": (c_size, [c_size] * 2),
+    "get_b_im2col_offset": (c_size, [c_size] * 3),
+    "run_im2col": (None, _IM2COL),
+    "run_im2col_async": (None, _IM2COL + [c_vp]),
+    "run_conv": _SIGS["mx1"]["run"],
+    "run_conv_async": _SIGS["mx1"]["run_async"],
+}
+_SIGS["convcfp"] = {
+    "get_m_step": (c_size, []),
+    "get_n_step": (c_size, []),
+    "get_a_packed_offset": (c_size, _OFFP),
+    "get_b_im2colpack_offset": (c_size, _OFFP),
+    "get_c_offset": (c_size, [c_size] * 3),
+    "get_bias_offset": (c_size, [c_size]),
+    "get_d_offset": (c_size, [c_size] * 3),
+    "get_d_size": (c_size, [c_size] * 2),
+    "get_a_packed_size": (c_size, [c_size] * 2),
+    "get_b_im2colpack_size": (c_size, [c_size] * 2),
+    "run_a_pack": (None, _PACK),
+    "run_a_pack_async": (None, _PACK + [c_vp]),
+    "run_b_im2colpack": (None, _IM2COLPACK),
+    "run_b_im2colpack_async": (None, _IM2COLPACK + [c_vp]),
+    "run_conv": _SIGS["mx1p"]["run"],
+    "run_conv_async": _SIGS["mx1p"]["run_async"],
+}
+_IGEMMCF = ([c_size] * 3 + [c_vp, c_size, c_size, c_size, c_vp, c_size, c_size, c_vp, c_size, c_vp,
+                            c_size, c_vp, ctypes.c_int8, ctypes.c_int8,
+                            ctypes.POINTER(ConvParams), ctypes.POINTER(QAI8QSI8DXQAI8Params)])
+_SIGS["igemmcf"] = {
+    "get_m_step": (c_size, []),
+    "get_n_step": (c_size, []),
+    "get_a_offset": (c_size, [c_size] * 3),
+    "get_c_offset": (c_size, [c_size] * 3),
+    "get_bias_offset": (c_size, [c_size]),
+    "get_d_offset": (c_size, [c_size] * 3),
+    "get_d_size": (c_size, [c_size] * 2),
+    "run_igemm": (None, _IGEMMCF),
+    "run_igemm_async": (None, _IGEMMCF + [c_vp]),
+}
+_SIGS["igemmcfp"] = {
+    "get_m_step": (c_size, []),
+    "get_n_step": (c_size, []),
+    "get_a_packed_offset": (c_size, _OFFP),
+    "get_c_offset": (c_size, [c_size] * 3),
+    "get_bias_offset": (c_size, [c_size]),
+    "get_d_offset": (c_size, [c_size] * 3),
+    "get_d_size": (c_size, [c_size] * 2),
+    "get_a_packed_size": (c_size, [c_size] * 2),
+    "run_a_pack": (None, _PACK),
+    "run_a_pack_async": (None, _PACK + [c_vp]),
+    "run_igemm": (None, _IGEMMCF),
+    "run_igemm_async": (None, _IGEMMCF + [c_vp]),
 }
 _SHIM_RUNS = ("w4a16", "w4a16p", "w4a8h", "w4a8b", "w4a8hp", "w4a8bp", "w8dynh", "w8dynhp")
 
