@@ -20,6 +20,8 @@
 //     multiple of 16, or channel counts not a multiple of 16.
 // All three accumulate exactly in int32 and fuse the epilogue (C, bias, requantization,
 // saturation, clamp) into the store.
+#include <type_traits>
+
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950.h"
 #include "tqt_gemm_clamp_i32_i8_i8_mfma_gfx950.h"
@@ -53,6 +55,13 @@ enum AMode { A_MATRIX = 0, A_CONV_CL = 1 };
 enum BMode { B_NK = 0, B_KN = 1, B_CF = 2 };
 // EPI_REQUANT_ROW: the requantization of EPI_REQUANT_I8 with its bias and multiplier per row
 // (gemm_mx1bias: the scale array belongs to A, the scalar scale to B)
+// s_waitcnt immediate waiting for vmcnt <= vm and lgkmcnt == 0.
+__host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm)
+{
+    // s_waitcnt immediate (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    return (vm & 15) | (7 << 4) | ((vm >> 4) << 14);
+}
+
 enum EpiMode {
     EPI_CLAMP_I32 = 0,
     EPI_REQUANT_I8 = 1,
@@ -143,13 +152,13 @@ __device__ uint32_t dyn_exact_acc(const Int8Args &a, int gm, int gn, int32_t zp)
 // rounded to f16, + the f16 bias in f16, then the bounds. Every step rounds once (the library is
 // built without contraction).
 template <int EPI>
-__device__ __forceinline__ void dyn_finish(const Int8Args &a, int gm, int gn, long long drow,
-                                           uint32_t x)
+__device__ __forceinline__ void dyn_finish_v(const Int8Args &a, int gn, long long drow, uint32_t x,
+                                             float sb, float sa, float fb)
 {
-    const float sigma = __fmul_rn(a.scale_b[gn], a.dyn_sa[gm]);
+    const float sigma = __fmul_rn(sb, sa);
     const float f = __fmul_rn(static_cast<float>(static_cast<int32_t>(x)), sigma);
     if constexpr (EPI == EPI_DYN_F32) {
-        float v = __fadd_rn(f, a.fbias ? static_cast<const float *>(a.fbias)[gn] : 0.0f);
+        float v = __fadd_rn(f, fb);
         v = rv_fmaxf(v, a.fcmin);
         v = rv_fminf(v, a.fcmax);
         static_cast<float *>(a.D)[drow * a.ldd + gn] = v;
@@ -160,8 +169,7 @@ __device__ __forceinline__ void dyn_finish(const Int8Args &a, int gm, int gn, lo
         float fr = f;
         asm volatile("" : "+v"(fr));
         const _Float16 h = static_cast<_Float16>(fr);
-        const _Float16 b = a.fbias ? static_cast<const _Float16 *>(a.fbias)[gn]
-                                   : static_cast<_Float16>(0.0f);
+        const _Float16 b = static_cast<_Float16>(fb);  // exact: fb holds a binary16 value
         const _Float16 hs = h + b;  // one binary16 rounding
         float v = rv_fmaxf(static_cast<float>(hs), a.fcmin);  // exact on binary16 values
         v = rv_fminf(v, a.fcmax);
@@ -174,15 +182,32 @@ __device__ __forceinline__ bool dyn_zp_in_range(int32_t zp)
     return zp >= kDynZpMin && zp <= kDynZpMax;
 }
 
-// MFMA-kernel epilogue of the qai8dx x qsi8cx types for a zero point in range: acc = sum q_a *
-// q_b, rs = sum q_b of the column.
+// The column's bias as f32 (an f16 bias converts exactly); +0 without a bias.
 template <int EPI>
-__device__ __forceinline__ void dyn_store(const Int8Args &a, int gm, int gn, long long drow,
-                                          int32_t acc, int32_t rs)
+__device__ __forceinline__ float dyn_bias(const Int8Args &a, int gn)
 {
-    const uint32_t zp = static_cast<uint32_t>(a.dyn_za[gm]);
-    dyn_finish<EPI>(a, gm, gn, drow, static_cast<uint32_t>(acc) - zp * static_cast<uint32_t>(rs));
+    if (!a.fbias) {
+        return 0.0f;
+    }
+    if constexpr (EPI == EPI_DYN_F32) {
+        return static_cast<const float *>(a.fbias)[gn];
+    } else {
+        return static_cast<float>(static_cast<const _Float16 *>(a.fbias)[gn]);
+    }
 }
+
+// One output from memory-held inputs (the exact per-output path).
+template <int EPI>
+__device__ __forceinline__ void dyn_finish(const Int8Args &a, int gm, int gn, long long drow,
+                                           uint32_t x)
+{
+    dyn_finish_v<EPI>(a, gn, drow, x, a.scale_b[gn], a.dyn_sa[gm], dyn_bias<EPI>(a, gn));
+}
+
+// The MFMA kernels' epilogues load every per-row (zero point, scale) and per-column (scale, bias)
+// input of a lane's outputs before its first store and wait for them once: stores count in
+// vmcnt, so a load between two stores would make the compiler's wait for it drain the earlier
+// store as well, serializing the lane's stores.
 
 // LDS tile of R rows x 64 bytes. The 16-byte column chunk of row r is XOR-swizzled with
 // (r >> 2) & 3 so that the 16 rows read by one 16-lane group of ds_read_b128 hit distinct
@@ -564,15 +589,27 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             const int32_t t = rs[j] + __shfl_xor(rs[j], 16);
             rsum[j] = t + __shfl_xor(t, 32);
         }
+        int32_t zr[MT][4];
+        float sar[MT][4];
+        float sbc[NT], fbc[NT];
         bool in_range = true;
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
-                in_range = in_range && (gm >= a.M || dyn_zp_in_range(a.dyn_za[gm]));
+                zr[i][r] = gm < a.M ? a.dyn_za[gm] : 0;
+                sar[i][r] = gm < a.M ? a.dyn_sa[gm] : 0.0f;
+                in_range = in_range && dyn_zp_in_range(zr[i][r]);
             }
         }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
+            sbc[j] = gn < a.N ? a.scale_b[gn] : 0.0f;
+            fbc[j] = gn < a.N ? dyn_bias<EPI>(a, gn) : 0.0f;
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // the compiler then adds no waits below
         if (in_range) {
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
@@ -583,7 +620,10 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
                     for (int r = 0; r < 4; ++r) {
                         const int gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
                         if (gm < a.M && gn < a.N) {
-                            dyn_store<EPI>(a, gm, gn, a.d_row0 + gm, acc[i][j][r], rsum[j]);
+                            const uint32_t x = static_cast<uint32_t>(acc[i][j][r]) -
+                                               static_cast<uint32_t>(zr[i][r]) *
+                                                   static_cast<uint32_t>(rsum[j]);
+                            dyn_finish_v<EPI>(a, gn, a.d_row0 + gm, x, sbc[j], sar[i][r], fbc[j]);
                         }
                     }
                 }
@@ -603,40 +643,75 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
         return;
     }
 
-    // Epilogue: lane holds D[4 * (lane / 16) + r][lane % 16] of every 16x16 sub-tile.
+    // Epilogue: lane holds D[4 * (lane / 16) + r][lane % 16] of every 16x16 sub-tile. C and the
+    // bias of every output of the lane are loaded first and waited for once (stores count in
+    // vmcnt: a load between stores would make its wait drain them).
+    constexpr bool kRow = EPI == EPI_REQUANT_ROW;
+    uint32_t add[MT][NT][4];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-            const int lc = wn * 64 + j * 16 + (lane & 15);
-            const int gn = n0 + lc;
+            const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
-                if (gm >= a.M || gn >= a.N) {
+                uint32_t v = 0;
+                if (gm < a.M && gn < a.N) {
+                    if (a.C) {
+                        v += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
+                    }
+                    if (a.bias) {
+                        v += static_cast<uint32_t>(a.bias[kRow ? gm : gn]);
+                    }
+                }
+                add[i][j][r] = v;
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // the compiler then adds no waits below
+    // A lane's output rows are row_l plus compile-time offsets: one per-lane base plus multiples
+    // of the uniform ldd; whole row tiles skip the per-output row check.
+    const int row_l = m0 + wm * WM + 4 * (lane >> 4);
+    const long long d_l = (a.d_row0 + row_l) * a.ldd;
+    auto epilogue = [&](auto checked) {
+        constexpr bool kChecked = decltype(checked)::value;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const int lc = wn * 64 + j * 16 + (lane & 15);
+                const int gn = n0 + lc;
+                if (gn >= a.N) {
                     continue;
                 }
-                uint32_t v = static_cast<uint32_t>(acc[i][j][r]);
-                if (a.C) {
-                    v += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
-                }
-                constexpr bool kRow = EPI == EPI_REQUANT_ROW;
-                if (a.bias) {
-                    v += static_cast<uint32_t>(a.bias[kRow ? gm : gn]);
-                }
-                const long long drow = a.d_row0 + gm;
-                if constexpr (EPI == EPI_CLAMP_I32) {
-                    int32_t x = static_cast<int32_t>(v);
-                    x = x < a.cmin ? a.cmin : x;
-                    x = x > a.cmax ? a.cmax : x;
-                    static_cast<int32_t *>(a.D)[drow * a.ldd + gn] = x;
-                } else {
-                    const int q = kRow ? gm - m0 : lc;
-                    static_cast<int8_t *>(a.D)[drow * a.ldd + gn] = requant_dev(
-                        static_cast<int32_t>(v), s_mult[q], s_shift[q], a.zp_d, a.cmin, a.cmax);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int dr = i * 16 + r;
+                    const int gm = row_l + dr;
+                    if (kChecked && gm >= a.M) {
+                        continue;
+                    }
+                    const uint32_t v = static_cast<uint32_t>(acc[i][j][r]) + add[i][j][r];
+                    const long long e = d_l + dr * a.ldd + gn;
+                    if constexpr (EPI == EPI_CLAMP_I32) {
+                        int32_t x = static_cast<int32_t>(v);
+                        x = x < a.cmin ? a.cmin : x;
+                        x = x > a.cmax ? a.cmax : x;
+                        static_cast<int32_t *>(a.D)[e] = x;
+                    } else {
+                        const int q = kRow ? gm - m0 : lc;
+                        static_cast<int8_t *>(a.D)[e] = requant_dev(
+                            static_cast<int32_t>(v), s_mult[q], s_shift[q], a.zp_d, a.cmin, a.cmax);
+                    }
                 }
             }
         }
+    };
+    if (m0 + BM <= a.M) {
+        epilogue(std::false_type{});
+    } else {
+        epilogue(std::true_type{});
     }
 }
 
@@ -658,11 +733,30 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 // ---------------------------------------------------------------------------------------------
 constexpr int kSK = 128;  // k bytes per pipeline stage
 
-__host__ __device__ constexpr int waitcnt_vm_lgkm0(int vm)
+// One global -> LDS load of 16 bytes per lane (lane i writes lds + 16 * i; lds is wave-uniform).
+// It is inline asm rather than __builtin_amdgcn_global_load_lds on purpose: the compiler tracks
+// the builtin's LDS write and, where its alias tracking of the ring stages is lost (the pipelined
+// loop's back edge), guards the next LDS reads with vmcnt(0), which drains every stage in flight
+// and serializes the stream (measured: 22.9 us -> 16 us per W8A8 M512 launch without it). The
+// kernels order these writes themselves with explicit vmcnt waits and s_barrier; the "memory"
+// clobber keeps the compiler's own LDS accesses on their side of each load. M0 carries the LDS
+// base (the low 32 bits of a flat LDS address are its LDS offset); nothing else in these kernels
+// uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_lds16(const int8_t *src, int8_t *lds)
 {
-    // s_waitcnt immediate (gfx9): vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
-    return (vm & 15) | (7 << 4) | ((vm >> 4) << 14);
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t base =
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base)
+                 : "memory", "m0");
+#else
+    (void)src;
+    (void)lds;
+#endif
 }
+#pragma clang diagnostic pop
 
 template <int BM, int EPI, int PK>
 __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int tiles_m, int tiles,
@@ -696,17 +790,34 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     const int wm = wave >> 1;
     const int wn = wave & 1;
 
-    if constexpr (EPI == EPI_REQUANT_I8) {
-        if (tid < kBN && n0 + tid < a.N) {
-            column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, n0 + tid,
-                                  s_mult[tid], s_shift[tid]);
-        }
-    } else if constexpr (EPI == EPI_REQUANT_ROW) {
-        if (tid < BM && m0 + tid < a.M) {
-            column_multiplier_dev(a.scale_a, a.scale_b, a.quant_channel_b, a.scale_d, m0 + tid,
-                                  s_mult[tid], s_shift[tid]);
+    // Epilogue inputs are loaded now and used after the main loop, so their latency hides under
+    // it: the multipliers' scale_b (finished into s_mult / s_shift after the loop: computing
+    // them here would hold back this wave's first loads by a memory round trip) and the biases.
+    constexpr bool kRow = EPI == EPI_REQUANT_ROW;
+    [[maybe_unused]] float pre_sb = 0.f;
+    [[maybe_unused]] int32_t pre_rbias = 0;  // per-row bias (EPI_REQUANT_ROW)
+    [[maybe_unused]] uint32_t pre_cbias[2] = {0u, 0u};
+    [[maybe_unused]] const bool mult_lane = kRow ? (tid < BM && m0 + tid < a.M)
+                                                 : (tid < kBN && n0 + tid < a.N);
+    if constexpr (EPI == EPI_REQUANT_I8 || kRow) {
+        if (mult_lane) {
+            const int idx = kRow ? m0 + tid : n0 + tid;
+            pre_sb = a.scale_b[a.quant_channel_b == 1 ? 0 : idx];
+            if (kRow && a.bias) {
+                pre_rbias = a.bias[idx];
+            }
         }
     }
+    if constexpr (!is_dyn(EPI) && !kRow) {
+        if (a.bias) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int gn = n0 + wn * 64 + 32 * j + (lane & 31);
+                pre_cbias[j] = gn < a.N ? static_cast<uint32_t>(a.bias[gn]) : 0u;
+            }
+        }
+    }
+    __shared__ int32_t s_rbias[kRow ? BM : 1];
 
     // Load-side lane roles. Plain rows: lane = 8 * row-in-block + LDS slot, the slot holding
     // k-chunk slot ^ ((row >> 1) & 7) of that row, so 8 consecutive lanes read one row's 128
@@ -752,20 +863,16 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     }
 
     auto issue = [&](int st, int8_t *sa, int8_t *sb) {
-        [[maybe_unused]] const int k0 = st * kSK;  // read by the device pass only
+        const int k0 = st * kSK;
 #pragma unroll
         for (int j = 0; j < A_DMA; ++j) {
-#if defined(__HIP_DEVICE_COMPILE__)
-            __builtin_amdgcn_global_load_lds(a_row[j] + pack_k<kPackI8Chunk, kAP>(k0, a_mul[j]),
-                                             sa + (wave * A_DMA + j) * 1024, 16, 0, 0);
-#endif
+            dma_lds16(a_row[j] + pack_k<kPackI8Chunk, kAP>(k0, a_mul[j]),
+                      sa + (wave * A_DMA + j) * 1024);
         }
 #pragma unroll
         for (int j = 0; j < B_DMA; ++j) {
-#if defined(__HIP_DEVICE_COMPILE__)
-            __builtin_amdgcn_global_load_lds(b_row[j] + pack_k<kPackI8Chunk, kBP>(k0, b_mul[j]),
-                                             sb + (wave * B_DMA + j) * 1024, 16, 0, 0);
-#endif
+            dma_lds16(b_row[j] + pack_k<kPackI8Chunk, kBP>(k0, b_mul[j]),
+                      sb + (wave * B_DMA + j) * 1024);
         }
     };
 
@@ -879,7 +986,21 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         step(st + 2, sa2, sb2, sa1, sb1);
         step(st + 3, sa3, sb3, sa2, sb2);
     }
-    __syncthreads();  // s_mult / s_shift visible even when k == 0
+    // Every load of this wave has landed (the last step waits for vmcnt(0)); saying so here lets
+    // the compiler's own wait tracking drop the vmcnt(0) it would otherwise place before each
+    // output of the epilogue for the epilogue inputs loaded above. Stores count in vmcnt too, so
+    // each of those waits would drain the previous output's store (measured: 4.5 us of a
+    // 22.4 us W8A8 M512 launch).
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    if constexpr (EPI == EPI_REQUANT_I8 || kRow) {
+        if (mult_lane) {
+            column_multiplier_val(a.scale_a, pre_sb, a.scale_d, s_mult[tid], s_shift[tid]);
+            if constexpr (kRow) {
+                s_rbias[tid] = pre_rbias;
+            }
+        }
+    }
+    __syncthreads();  // s_mult / s_shift / s_rbias visible to every wave
 
     if constexpr (is_dyn(EPI)) {
         // lanes r32 and r32 + 32 summed the two 16-byte halves of every k-step of column r32
@@ -888,15 +1009,27 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         for (int j = 0; j < NF; ++j) {
             rsum[j] = rs[j] + __shfl_xor(rs[j], 32);
         }
+        int32_t zr[MF][16];
+        float sar[MF][16];
+        float sbc[NF], fbc[NF];
         bool in_range = true;
 #pragma unroll
         for (int i = 0; i < MF; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                in_range = in_range && (gm >= a.M || dyn_zp_in_range(a.dyn_za[gm]));
+                zr[i][r] = gm < a.M ? a.dyn_za[gm] : 0;
+                sar[i][r] = gm < a.M ? a.dyn_sa[gm] : 0.0f;
+                in_range = in_range && dyn_zp_in_range(zr[i][r]);
             }
         }
+#pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            const int gn = n0 + wn * 64 + 32 * j + r32;
+            sbc[j] = gn < a.N ? a.scale_b[gn] : 0.0f;
+            fbc[j] = gn < a.N ? dyn_bias<EPI>(a, gn) : 0.0f;
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // the compiler then adds no waits below
         if (in_range) {
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
@@ -907,7 +1040,10 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
                     for (int r = 0; r < 16; ++r) {
                         const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
                         if (gm < a.M && gn < a.N) {
-                            dyn_store<EPI>(a, gm, gn, a.d_row0 + gm, acc[i][j][r], rsum[j]);
+                            const uint32_t x = static_cast<uint32_t>(acc[i][j][r]) -
+                                               static_cast<uint32_t>(zr[i][r]) *
+                                                   static_cast<uint32_t>(rsum[j]);
+                            dyn_finish_v<EPI>(a, gn, a.d_row0 + gm, x, sbc[j], sar[i][r], fbc[j]);
                         }
                     }
                 }
@@ -927,52 +1063,77 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         return;
     }
 
-    // Epilogue: lane holds D[8 * (r / 4) + 4 * h + r % 4][r32] of each 32 x 32 fragment.
+    // Epilogue: lane holds D[8 * (r / 4) + 4 * h + r % 4][r32] of each 32 x 32 fragment. A
+    // lane's output rows are row_l plus compile-time offsets, so their addresses are one
+    // per-lane base plus multiples of the uniform ldd (scalar arithmetic); whole row tiles skip
+    // the per-output row check.
+    const int row_l = m0 + wm * WM + 4 * h;
+    auto epilogue = [&](auto checked) {
+        constexpr bool kChecked = decltype(checked)::value;
 #pragma unroll
-    for (int j = 0; j < NF; ++j) {
-        const int lc = wn * 64 + 32 * j + r32;
-        const int gn = n0 + lc;
-        if (gn >= a.N) {
-            continue;
-        }
-        constexpr bool kRow = EPI == EPI_REQUANT_ROW;
-        const uint32_t bias = (a.bias && !kRow) ? static_cast<uint32_t>(a.bias[gn]) : 0u;
-        int32_t mult = 0, shift = 0;
-        if constexpr (EPI == EPI_REQUANT_I8) {
-            mult = s_mult[lc];
-            shift = s_shift[lc];
-        }
+        for (int j = 0; j < NF; ++j) {
+            const int lc = wn * 64 + 32 * j + r32;
+            const int gn = n0 + lc;
+            if (gn >= a.N) {
+                continue;
+            }
+            const uint32_t bias = pre_cbias[j];  // 0 without a bias and for kRow
+            int32_t mult = 0, shift = 0;
+            if constexpr (EPI == EPI_REQUANT_I8) {
+                mult = s_mult[lc];
+                shift = s_shift[lc];
+            }
+            // C (optional) for every output of this column first, so the compiler waits for
+            // them once rather than between stores
+            uint32_t cv[MF][16] = {};
+            if (a.C) {
+                const long long c0 = static_cast<long long>(row_l) * a.ldc + gn;
 #pragma unroll
-        for (int i = 0; i < MF; ++i) {
+                for (int i = 0; i < MF; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (gm >= a.M) {
-                    continue;
-                }
-                uint32_t v = static_cast<uint32_t>(acc[i][j][r]) + bias;
-                if constexpr (kRow) {
-                    mult = s_mult[gm - m0];
-                    shift = s_shift[gm - m0];
-                    if (a.bias) {
-                        v += static_cast<uint32_t>(a.bias[gm]);
+                    for (int r = 0; r < 16; ++r) {
+                        const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+                        if (!kChecked || row_l + dr < a.M) {
+                            cv[i][r] = static_cast<uint32_t>(a.C[c0 + dr * a.ldc]);
+                        }
                     }
                 }
-                if (a.C) {
-                    v += static_cast<uint32_t>(a.C[static_cast<long long>(gm) * a.ldc + gn]);
-                }
-                const long long drow = a.d_row0 + gm;
-                if constexpr (EPI == EPI_CLAMP_I32) {
-                    int32_t x = static_cast<int32_t>(v);
-                    x = x < a.cmin ? a.cmin : x;
-                    x = x > a.cmax ? a.cmax : x;
-                    static_cast<int32_t *>(a.D)[drow * a.ldd + gn] = x;
-                } else {
-                    static_cast<int8_t *>(a.D)[drow * a.ldd + gn] =
-                        requant_dev(static_cast<int32_t>(v), mult, shift, a.zp_d, a.cmin, a.cmax);
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // no compiler waits below
+            }
+            const long long d0 = (a.d_row0 + row_l) * a.ldd + gn;
+#pragma unroll
+            for (int i = 0; i < MF; ++i) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+                    const int gm = row_l + dr;
+                    if (kChecked && gm >= a.M) {
+                        continue;
+                    }
+                    uint32_t v = static_cast<uint32_t>(acc[i][j][r]) + bias + cv[i][r];
+                    if constexpr (kRow) {
+                        mult = s_mult[gm - m0];
+                        shift = s_shift[gm - m0];
+                        v += static_cast<uint32_t>(s_rbias[gm - m0]);  // 0 without a bias
+                    }
+                    const long long e = d0 + dr * a.ldd;
+                    if constexpr (EPI == EPI_CLAMP_I32) {
+                        int32_t x = static_cast<int32_t>(v);
+                        x = x < a.cmin ? a.cmin : x;
+                        x = x > a.cmax ? a.cmax : x;
+                        static_cast<int32_t *>(a.D)[e] = x;
+                    } else {
+                        static_cast<int8_t *>(a.D)[e] = requant_dev(static_cast<int32_t>(v), mult,
+                                                                    shift, a.zp_d, a.cmin, a.cmax);
+                    }
                 }
             }
         }
+    };
+    if (m0 + BM <= a.M) {
+        epilogue(std::false_type{});
+    } else {
+        epilogue(std::true_type{});
     }
 }
 

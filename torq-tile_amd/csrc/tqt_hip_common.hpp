@@ -136,14 +136,22 @@ __device__ __forceinline__ void quantize_multiplier_dev(double x, int32_t &mult,
 
 // Column multiplier exactly as the run functions compute it: double(scale_a) * double(scale_b)
 // / double(scale_d), column 0 reused for every column when quant_channel_b == 1.
+// column_multiplier_val takes the column's scale_b already loaded (kernels that load it early
+// and finish the multiplier later).
+__device__ __forceinline__ void column_multiplier_val(float scale_a, float scale_b_col,
+                                                      float scale_d, int32_t &mult, int32_t &shift)
+{
+    const double real = static_cast<double>(scale_a) * static_cast<double>(scale_b_col) /
+                        static_cast<double>(scale_d);
+    quantize_multiplier_dev(real, mult, shift);
+}
+
 __device__ __forceinline__ void column_multiplier_dev(float scale_a, const float *scale_b,
                                                       int32_t quant_channel_b, float scale_d,
                                                       int col, int32_t &mult, int32_t &shift)
 {
     const int src = (quant_channel_b == 1) ? 0 : col;
-    const double real = static_cast<double>(scale_a) * static_cast<double>(scale_b[src]) /
-                        static_cast<double>(scale_d);
-    quantize_multiplier_dev(real, mult, shift);
+    column_multiplier_val(scale_a, scale_b[src], scale_d, mult, shift);
 }
 
 // ---------------------------------------------------------------------------------------------
