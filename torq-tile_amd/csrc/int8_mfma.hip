@@ -106,6 +106,7 @@ struct Int8Args
     long long ldd;
     long long d_row0;  // igemmcl: D row of local pixel 0 (= m_idx); 0 otherwise
     long long p0;      // igemmcl / igemmcf: global pixel index of local pixel 0
+    int conv_bytes;    // igemmcl streaming path: input bytes from A to the end of the input
     const int32_t *bias;
     int32_t cmin, cmax;
     // requantization: multiplier of column j (row i for EPI_REQUANT_ROW) from
@@ -716,7 +717,10 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Streaming kernel for plain A and B = [n, k] (W8A8 and its packed siblings), k % 128 == 0.
+// Streaming kernel for plain A and B = [n, k] (W8A8 and its packed siblings), k % 128 == 0, and
+// for the implicit convolution (igemmcl) when the group channel count is a multiple of 128: a
+// stage is then 128 channels of one tap, each A row the 128 contiguous input bytes of its output
+// pixel's tap, read through a buffer resource whose range check returns zeros for padding taps.
 //
 // A workgroup of 4 wave64s (2 x 2) owns a BM x 128 output tile (BM = 64 or 128) and walks k in
 // stages of 128 bytes through a 4-deep ring of LDS stages filled by direct global->LDS loads
@@ -756,9 +760,26 @@ __device__ __forceinline__ void dma_lds16(const int8_t *src, int8_t *lds)
     (void)lds;
 #endif
 }
+
+// The same load through a buffer resource: voffset is a byte offset from the resource's base,
+// and an offset at or past its num_records reads zeros (the implicit convolution's padding taps).
+__device__ __forceinline__ void dma_lds16_buf(i32x4 rsrc, int voffset, int8_t *lds)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t base =
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset),
+                 "s"(rsrc), "s"(base)
+                 : "memory", "m0");
+#else
+    (void)rsrc;
+    (void)voffset;
+    (void)lds;
+#endif
+}
 #pragma clang diagnostic pop
 
-template <int BM, int EPI, int PK>
+template <int BM, int EPI, int PK, bool kConv = false>
 __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int tiles_m, int tiles,
                                                                int per_xcd)
 {
@@ -829,6 +850,13 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     constexpr bool kBP = (PK & PK_B) != 0;
     const int8_t *a_row[A_DMA];
     int a_mul[A_DMA];
+    // Implicit convolution (NDHWC input, ICg % 128 == 0): stage st is 128 channels of one tap,
+    // so row r of a stage is 128 contiguous input bytes of output pixel p0 + m0 + r's window
+    // (zeros for a padding tap, read through the buffer resource's range check). c_o* is the
+    // window's first input coordinate, c_base the byte offset of that pixel plus the lane's
+    // 16-byte chunk.
+    [[maybe_unused]] int c_od[A_DMA], c_oh[A_DMA], c_ow[A_DMA], c_base[A_DMA];
+    [[maybe_unused]] i32x4 c_rsrc;
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) {
         const int blk = wave * A_DMA + j;
@@ -837,13 +865,33 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         const int gm = min(m0 + r, a.M - 1);
         long long base;
         a_mul[j] = 1;  // k multiplier of a packed row (its panel width)
-        if constexpr (kAP) {
+        if constexpr (kConv) {
+            const ConvGeom &g = a.cv;
+            // p0 + M < 2^31 on this path: 32-bit unsigned divisions
+            const uint32_t p = static_cast<uint32_t>(a.p0) + static_cast<uint32_t>(gm);
+            const uint32_t q1 = p / static_cast<uint32_t>(g.OW);
+            const uint32_t q2 = q1 / static_cast<uint32_t>(g.OH);
+            c_od[j] = static_cast<int>(q2) * g.SD - g.PD;
+            c_oh[j] = static_cast<int>(q1 - q2 * static_cast<uint32_t>(g.OH)) * g.SH - g.PH;
+            c_ow[j] = static_cast<int>(p - q1 * static_cast<uint32_t>(g.OW)) * g.SW - g.PW;
+            c_base[j] = ((c_od[j] * g.IH + c_oh[j]) * g.IW + c_ow[j]) * g.IC + chunk * 16;
+            base = 0;
+        } else if constexpr (kAP) {
             base = pack_row(a.pa, gm, a_mul[j]);
         } else {
             base = static_cast<long long>(gm) * a.lda;
         }
         a_row[j] = a.A + base + pack_k<kPackI8Chunk, kAP>(chunk * 16, a_mul[j]);
     }
+    if constexpr (kConv) {
+        const uint64_t ab = reinterpret_cast<uint64_t>(a.A);
+        c_rsrc[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(ab & 0xffffffffu));
+        c_rsrc[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((ab >> 32) & 0xffffu));
+        c_rsrc[2] = __builtin_amdgcn_readfirstlane(a.conv_bytes);  // num_records
+        c_rsrc[3] = 0x00020000;                                    // raw 32-bit dwords
+    }
+    // tap cursor of the next stage to issue (stages are issued in order)
+    [[maybe_unused]] int t_ic = 0, t_kw = 0, t_kh = 0, t_kd = 0;
     const int8_t *b_row[B_DMA];
     int b_mul[B_DMA];
 #pragma unroll
@@ -864,10 +912,35 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
 
     auto issue = [&](int st, int8_t *sa, int8_t *sb) {
         const int k0 = st * kSK;
+        if constexpr (kConv) {
+            const ConvGeom &g = a.cv;
+            const int dd = t_kd * g.DD, dh = t_kh * g.DH, dw = t_kw * g.DW;
+            const int toff = ((dd * g.IH + dh) * g.IW + dw) * g.IC + t_ic;
 #pragma unroll
-        for (int j = 0; j < A_DMA; ++j) {
-            dma_lds16(a_row[j] + pack_k<kPackI8Chunk, kAP>(k0, a_mul[j]),
-                      sa + (wave * A_DMA + j) * 1024);
+            for (int j = 0; j < A_DMA; ++j) {
+                const int id = c_od[j] + dd, ih = c_oh[j] + dh, iw = c_ow[j] + dw;
+                const bool ok = id >= 0 && id < g.ID && ih >= 0 && ih < g.IH && iw >= 0 &&
+                                iw < g.IW;
+                dma_lds16_buf(c_rsrc, ok ? c_base[j] + toff : a.conv_bytes,
+                              sa + (wave * A_DMA + j) * 1024);
+            }
+            t_ic += kSK;
+            if (t_ic == g.ICg) {
+                t_ic = 0;
+                if (++t_kw == g.KW) {
+                    t_kw = 0;
+                    if (++t_kh == g.KH) {
+                        t_kh = 0;
+                        ++t_kd;
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < A_DMA; ++j) {
+                dma_lds16(a_row[j] + pack_k<kPackI8Chunk, kAP>(k0, a_mul[j]),
+                          sa + (wave * A_DMA + j) * 1024);
+            }
         }
 #pragma unroll
         for (int j = 0; j < B_DMA; ++j) {
@@ -1257,7 +1330,7 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     }
 }
 
-template <int EPI, int PK>
+template <int EPI, int PK, bool kConv = false>
 void launch_stream(const Int8Args &a, hipStream_t stream)
 {
     const long long tiles_n = (a.N + kBN - 1) / kBN;
@@ -1270,11 +1343,11 @@ void launch_stream(const Int8Args &a, hipStream_t stream)
     const long long per_xcd = (tiles + 7) / 8;
     TQT_REQUIRE(tiles < (1ll << 30), "grid too large");
     if (big) {
-        hipLaunchKernelGGL((int8_stream_kernel<128, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
+        hipLaunchKernelGGL((int8_stream_kernel<128, EPI, PK, kConv>), dim3(8 * per_xcd), dim3(kThreads), 0,
                            stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
                            static_cast<int>(per_xcd));
     } else {
-        hipLaunchKernelGGL((int8_stream_kernel<64, EPI, PK>), dim3(8 * per_xcd), dim3(kThreads), 0,
+        hipLaunchKernelGGL((int8_stream_kernel<64, EPI, PK, kConv>), dim3(8 * per_xcd), dim3(kThreads), 0,
                            stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
                            static_cast<int>(per_xcd));
     }
@@ -1286,12 +1359,19 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
     if (a.M <= 0 || a.N <= 0) {
         return;
     }
-    // The streaming kernel is for plain matrices: for the implicit convolution (k = 1152 at the
-    // config, nine stages) its 4-deep ring never reaches steady state and the double-buffered
-    // kernel is faster.
+    // The streaming kernel takes plain (or packed) matrices and the implicit convolution whose
+    // group channel count is a multiple of its 128-byte stage (conv_bytes > 0, set by the
+    // convolution's run when its geometry allows).
     if constexpr (BMd == B_NK && AM == A_MATRIX) {
         if (fast && a.K % kSK == 0) {
             launch_stream<EPI, PK>(a, stream);
+            check_launch(where);
+            return;
+        }
+    }
+    if constexpr (BMd == B_NK && AM == A_CONV_CL && EPI == EPI_REQUANT_I8) {
+        if (fast && a.conv_bytes > 0 && a.cv.ICg % kSK == 0) {
+            launch_stream<EPI, PK, true>(a, stream);
             check_launch(where);
             return;
         }
@@ -1400,6 +1480,11 @@ void igemm_run(size_t m, size_t n, const void *input, size_t group_idx, size_t m
     // 10 bits each, and input offsets that fit 31 bits
     const size_t in_bytes = p.input_shape[0] * p.input_shape[1] * p.input_shape[2] *
                             static_cast<size_t>(p.input_channel);
+    // streaming path: the input from the group's base must fit the buffer resource's 31-bit
+    // offsets
+    a.conv_bytes = (in_bytes < (1ull << 31) && m_idx + m < (1ull << 31))
+                       ? static_cast<int>(in_bytes - group_idx * icg)
+                       : 0;
     const bool geo_fast = (icg % 16 == 0) && (p.input_channel % 16 == 0) && aligned16(a.A) &&
                           aligned16(B) && kfull / 16 <= kConvMaxChunks &&
                           (p.kernel_shape[0] - 1) * p.dilation[0] < 1024 &&
