@@ -3,10 +3,14 @@
 // Fast path (decode-shaped, any m in chunks of 15 rows, k % 256 == 0): one workgroup of 8
 // wave64s owns a 16-channel weight tile (16 rows of B) for one chunk of up to 15 activation
 // rows; wave w owns one eighth of k.
-//   * Weights stream in 128-bit loads shaped 8 rows x 128 bytes per wave instruction (whole
-//     cache lines), are staged through wave-private LDS (16-byte chunks XOR-swizzled by row)
-//     and read back in the MFMA B-operand layout. Each 128-byte-per-row "pair" of k (two MFMA
-//     steps) is consumed as soon as its two loads land, so compute overlaps the stream.
+//   * Plain weights stream in 128-bit loads shaped 8 rows x 128 bytes per wave instruction
+//     (whole cache lines), are staged through wave-private LDS (16-byte chunks XOR-swizzled by
+//     row) and read back in the MFMA B-operand layout. Packed weights (16-byte chunks stored
+//     chunk-major in 16-row panels) load straight into the B-operand layout, 1 KB contiguous
+//     per instruction, with no staging (measured faster; for the plain layout the same direct
+//     loads, 16 rows x 64 bytes per instruction, are slower than the staged whole lines). Each
+//     128-byte-per-row "pair" of k (two MFMA steps) is consumed as soon as its two loads land,
+//     so compute overlaps the stream.
 //   * Nibbles become signed bytes in two bit operations each: ((w << 4) & 0xf0f0f0f0) ^
 //     0x80808080 is the byte 16 * (lo - 8) and (w & 0xf0f0f0f0) ^ 0x80808080 is 16 * (hi - 8).
 //     v_mfma_i32_16x16x64_i8 then accumulates exactly 16 * sum_k a * (q - 8); the workgroup
@@ -111,7 +115,9 @@ __device__ __forceinline__ void decode_w16(const u32x4 w, i32x4 &q0, i32x4 &q1)
 template <bool kActInLds, int PK, int OUT>
 __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][2 * kPairsPerBatch][1024];
+    constexpr bool kDirect = (PK & PK_B) != 0;  // weights straight into operand registers
+    __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][kDirect ? 1 : 2 * kPairsPerBatch]
+                                                       [kDirect ? 16 : 1024];
     // activations of each wave's k-slice (one 16-byte chunk per lane at most)
     __shared__ __attribute__((aligned(16))) int8_t s_a[kWaves][kActInLds ? 1024 : 16];
     __shared__ int32_t s_part[kWaves][16][16];
@@ -194,11 +200,12 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
             a_rowp = a.A + static_cast<long long>(r) * a.lda;
         }
     }
+    // staged path: rows 8 * h + r8; direct path: row fr, chunks 4 * h + fg of each pair
     const uint8_t *w_rowp[2];
     int w_mul[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int row = 8 * h + r8;
+        const int row = kDirect ? fr : 8 * h + r8;
         const int grow = n0 + row < a.N ? n0 + row : n0;
         w_mul[h] = 1;
         if constexpr ((PK & PK_B) != 0) {
@@ -234,9 +241,10 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 #pragma unroll
         for (int j = 0; j < 2 * kPairsPerBatch; ++j) {
             const int pair = min(pb + (j >> 1), p_end - 1);
+            const int chunk = kDirect ? 4 * (j & 1) + fg : c8;
             wr[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
-                w_rowp[j & 1] +
-                pack_k<kPackW4A8Chunk, (PK & PK_B) != 0>(pair * (kPairK / 2) + c8 * 16, w_mul[j & 1])));
+                w_rowp[j & 1] + pack_k<kPackW4A8Chunk, (PK & PK_B) != 0>(
+                                    pair * (kPairK / 2) + chunk * 16, w_mul[j & 1])));
         }
         // keep every load of the batch ahead of the compute (the scheduler would sink them to
         // their uses and serialize the stream); emits no instruction
@@ -249,10 +257,12 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 #pragma unroll
         for (int pp = 0; pp < kPairsPerBatch; ++pp) {
             // stage this pair: (row, chunk) at row * 128 + ((chunk ^ (row & 7)) << 4)
+            if constexpr (!kDirect) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int j = 2 * pp + h;
-                *reinterpret_cast<u32x4 *>(&s_w[wave][j][r8 * 128 + ((c8 ^ r8) << 4)]) = wr[j];
+                for (int h = 0; h < 2; ++h) {
+                    const int j = 2 * pp + h;
+                    *reinterpret_cast<u32x4 *>(&s_w[wave][j][r8 * 128 + ((c8 ^ r8) << 4)]) = wr[j];
+                }
             }
             const int pair = pb + pp;
             if (pair >= p_end) {
@@ -277,11 +287,16 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 }
                 i32x4 x0, x1, q0, q1;
                 permute_act(v0, v1, x0, x1);
-                const int jj = 2 * pp + (fr >> 3);
-                const int rr = fr & 7;
-                const int c = 4 * h + fg;
-                decode_w16(*reinterpret_cast<const u32x4 *>(&s_w[wave][jj][rr * 128 + ((c ^ rr) << 4)]),
-                           q0, q1);
+                if constexpr (kDirect) {
+                    decode_w16(wr[2 * pp + h], q0, q1);
+                } else {
+                    const int jj = 2 * pp + (fr >> 3);
+                    const int rr = fr & 7;
+                    const int c = 4 * h + fg;
+                    decode_w16(*reinterpret_cast<const u32x4 *>(
+                                   &s_w[wave][jj][rr * 128 + ((c ^ rr) << 4)]),
+                               q0, q1);
+                }
                 acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, q0, acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, q1, acc1, 0, 0, 0);
             }
