@@ -61,8 +61,9 @@ def check(X, **kw):
     np.testing.assert_array_equal(z, ez)
 
 
+# k <= 4096 keeps the row in registers between the two passes; 4094 and 4101 sit either side
 @pytest.mark.parametrize("m,k", [(1, 4096), (4, 4096), (8, 4096), (37, 100), (3, 7), (2, 1),
-                                 (5, 65536)])
+                                 (5, 65536), (2, 4094), (3, 4101)])
 def test_random_rows(gpu, m, k):
     rng = np.random.default_rng(m * 1000 + k)
     check(rng.standard_normal((m, k)).astype(np.float32) * np.float32(rng.uniform(0.01, 50)))

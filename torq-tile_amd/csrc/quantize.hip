@@ -20,6 +20,7 @@ namespace tqt {
 namespace {
 
 constexpr int kQThreads = 256;
+constexpr int kQCache = 4;  // float4 per thread kept in registers (rows of k <= 4096)
 
 __device__ __forceinline__ int8_t quantize_one(float x, float s, float zpf)
 {
@@ -41,10 +42,30 @@ __global__ __launch_bounds__(kQThreads) void quantize_qai8dx_kernel(
 
     float lo = FLT_MAX, hi = -FLT_MAX;
     const int k4 = vec ? k / 4 : 0;
-    for (int i = tid; i < k4; i += kQThreads) {
-        const f32x4 v = reinterpret_cast<const f32x4 *>(x)[i];
-        lo = fminf(lo, fminf(fminf(v[0], v[1]), fminf(v[2], v[3])));
-        hi = fmaxf(hi, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    // Rows of up to kQCache * kQThreads float4 stay in registers between the min/max pass and
+    // the quantizing pass (all of their loads in flight at once, no second read of the row).
+    const bool cached = k4 > 0 && k4 <= kQCache * kQThreads;  // k4 > 0: vec and x[0..3] valid
+    f32x4 cache[kQCache];
+    if (cached) {
+#pragma unroll
+        for (int c = 0; c < kQCache; ++c) {
+            const int i = tid + c * kQThreads;
+            cache[c] = reinterpret_cast<const f32x4 *>(x)[i < k4 ? i : 0];
+        }
+#pragma unroll
+        for (int c = 0; c < kQCache; ++c) {
+            if (tid + c * kQThreads < k4) {
+                const f32x4 v = cache[c];
+                lo = fminf(lo, fminf(fminf(v[0], v[1]), fminf(v[2], v[3])));
+                hi = fmaxf(hi, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+            }
+        }
+    } else {
+        for (int i = tid; i < k4; i += kQThreads) {
+            const f32x4 v = reinterpret_cast<const f32x4 *>(x)[i];
+            lo = fminf(lo, fminf(fminf(v[0], v[1]), fminf(v[2], v[3])));
+            hi = fmaxf(hi, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+        }
     }
     for (int i = 4 * k4 + tid; i < k; i += kQThreads) {
         lo = fminf(lo, x[i]);
@@ -87,7 +108,21 @@ __global__ __launch_bounds__(kQThreads) void quantize_qai8dx_kernel(
         zp_a[row] = zp;
     }
     const float zpf = static_cast<float>(zp);
-    for (int i = tid; i < k4; i += kQThreads) {
+    if (cached) {
+#pragma unroll
+        for (int c = 0; c < kQCache; ++c) {
+            const int i = tid + c * kQThreads;
+            if (i < k4) {
+                const f32x4 v = cache[c];
+                const uint32_t b0 = static_cast<uint8_t>(quantize_one(v[0], s, zpf));
+                const uint32_t b1 = static_cast<uint8_t>(quantize_one(v[1], s, zpf));
+                const uint32_t b2 = static_cast<uint8_t>(quantize_one(v[2], s, zpf));
+                const uint32_t b3 = static_cast<uint8_t>(quantize_one(v[3], s, zpf));
+                reinterpret_cast<uint32_t *>(q)[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        }
+    }
+    for (int i = cached ? k4 : tid; i < k4; i += kQThreads) {
         const f32x4 v = reinterpret_cast<const f32x4 *>(x)[i];
         const uint32_t b0 = static_cast<uint8_t>(quantize_one(v[0], s, zpf));
         const uint32_t b1 = static_cast<uint8_t>(quantize_one(v[1], s, zpf));
