@@ -81,6 +81,20 @@ def test_w8a8_variants(gpu):
         np.testing.assert_array_equal(got, exp, err_msg=str(upd.keys()))
 
 
+@pytest.mark.parametrize("m,n,k", [(64, 256, 512), (7, 9, 33)])
+def test_w8a8_inverted_clamp(gpu, m, n, k):
+    """clamp_min > clamp_max: the reference's max-then-min leaves clamp_max everywhere
+    (stream kernel and generic kernel)."""
+    d = T.gen_w8a8(m, n, k, seed=m + n)
+    for cmin, cmax in ((50, -30), (127, -128), (-5, -5)):
+        got = _gr().run_w8a8(d, cmin, cmax)
+        exp = T.oracle_w8a8(d["A"], d["B"], d["C"], d["bias"], cmin, cmax, d["scale_a"],
+                            d["scale_b"], n, d["scale_d"], d["zp_d"])
+        np.testing.assert_array_equal(got, exp)
+        if cmin > cmax:
+            assert (got == cmax).all()
+
+
 def test_w8a8_config2_full(gpu):
     """BASELINE cfg 2 at full size: M=512, K=4096, N=4096, bit-exact."""
     d = T.gen_w8a8(512, 4096, 4096, seed=42)

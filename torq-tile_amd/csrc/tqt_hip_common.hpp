@@ -398,15 +398,18 @@ __device__ __forceinline__ float rv_fminf(float a, float b)
 // One output of the requantization epilogue (reference tqt_kernel_gemm_i8_i8_4x1vl_rvv.h:
 // requantize_1xn :334-408 = vmulh, vsra by shift & 31, vadd zp, vnclip to i16 then i8;
 // clamp_i8 :231-259 = vmax then vmin).
+// cmin and cmax are int8 values (the run functions take them as int8_t): then the saturation to
+// [-128, 127] followed by max(., cmin) and min(., cmax) equals max(., min(cmin, cmax)) followed
+// by min(., cmax), which also covers cmin > cmax (every output is cmax); the first of those is
+// uniform, so two operations per output remain.
 __device__ __forceinline__ int8_t requant_dev(int32_t acc, int32_t mult, int32_t shift,
                                               int32_t zp, int32_t cmin, int32_t cmax)
 {
     int32_t y = __mulhi(acc, mult);  // high 32 bits of the signed 64-bit product
     y = y >> (shift & 31);
     y = static_cast<int32_t>(static_cast<uint32_t>(y) + static_cast<uint32_t>(zp));
-    y = y < -128 ? -128 : (y > 127 ? 127 : y);
-    y = y < cmin ? cmin : y;
-    y = y > cmax ? cmax : y;
+    y = max(y, min(cmin, cmax));
+    y = min(y, cmax);
     return static_cast<int8_t>(y);
 }
 
