@@ -874,7 +874,13 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
             c_od[j] = static_cast<int>(q2) * g.SD - g.PD;
             c_oh[j] = static_cast<int>(q1 - q2 * static_cast<uint32_t>(g.OH)) * g.SH - g.PH;
             c_ow[j] = static_cast<int>(p - q1 * static_cast<uint32_t>(g.OW)) * g.SW - g.PW;
-            c_base[j] = ((c_od[j] * g.IH + c_oh[j]) * g.IW + c_ow[j]) * g.IC + chunk * 16;
+            // unsigned (wrapping) arithmetic: for a padding position the partial offsets leave
+            // the input; once a tap is in range the sum is its true offset (< 2^31)
+            c_base[j] = static_cast<int>(
+                ((static_cast<uint32_t>(c_od[j]) * g.IH + static_cast<uint32_t>(c_oh[j])) * g.IW +
+                 static_cast<uint32_t>(c_ow[j])) *
+                    g.IC +
+                chunk * 16u);
             base = 0;
         } else if constexpr (kAP) {
             base = pack_row(a.pa, gm, a_mul[j]);
@@ -915,13 +921,16 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         if constexpr (kConv) {
             const ConvGeom &g = a.cv;
             const int dd = t_kd * g.DD, dh = t_kh * g.DH, dw = t_kw * g.DW;
-            const int toff = ((dd * g.IH + dh) * g.IW + dw) * g.IC + t_ic;
+            const uint32_t toff =
+                ((static_cast<uint32_t>(dd) * g.IH + dh) * g.IW + dw) * g.IC + t_ic;
 #pragma unroll
             for (int j = 0; j < A_DMA; ++j) {
                 const int id = c_od[j] + dd, ih = c_oh[j] + dh, iw = c_ow[j] + dw;
                 const bool ok = id >= 0 && id < g.ID && ih >= 0 && ih < g.IH && iw >= 0 &&
                                 iw < g.IW;
-                dma_lds16_buf(c_rsrc, ok ? c_base[j] + toff : a.conv_bytes,
+                dma_lds16_buf(c_rsrc,
+                              ok ? static_cast<int>(static_cast<uint32_t>(c_base[j]) + toff)
+                                 : a.conv_bytes,
                               sa + (wave * A_DMA + j) * 1024);
             }
             t_ic += kSK;
