@@ -16,6 +16,10 @@ extern "C" {
 
 typedef size_t (*tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_m_step_func_t)(void);
 typedef size_t (*tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_n_step_func_t)(void);
+typedef size_t (*tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_a_packed_offset_func_t)(
+    size_t m_idx, size_t k_idx, size_t lda, size_t actual_m);
+typedef size_t (*tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_b_packed_offset_func_t)(
+    size_t n_idx, size_t k_idx, size_t ldb, size_t actual_n);
 typedef size_t (*tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_c_offset_func_t)(
     size_t m_idx, size_t n_idx, size_t ldc);
 typedef size_t (*tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_bias_offset_func_t)(size_t n_idx);
@@ -43,6 +47,8 @@ struct tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_ukernel
 {
     tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_m_step_func_t get_m_step;
     tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_n_step_func_t get_n_step;
+    tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_a_packed_offset_func_t get_a_packed_offset;
+    tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_b_packed_offset_func_t get_b_packed_offset;
     tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_c_offset_func_t get_c_offset;
     tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_bias_offset_func_t get_bias_offset;
     tqt_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8p_qsi8cxp_get_d_offset_func_t get_d_offset;

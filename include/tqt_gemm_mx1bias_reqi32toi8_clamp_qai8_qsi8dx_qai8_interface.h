@@ -14,34 +14,34 @@
 extern "C" {
 #endif
 
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_m_step_func_t)(void);
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_n_step_func_t)(void);
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_a_offset_func_t)(
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_m_step_func)(void);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_n_step_func)(void);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_a_offset_func)(
     size_t m_idx, size_t k_idx, size_t lda);
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_b_offset_func_t)(
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_b_offset_func)(
     size_t n_idx, size_t k_idx, size_t ldb);
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_c_offset_func_t)(
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_c_offset_func)(
     size_t m_idx, size_t n_idx, size_t ldc);
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_bias_offset_func_t)(size_t m_idx);
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_offset_func_t)(
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_bias_offset_func)(size_t m_idx);
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_offset_func)(
     size_t m_idx, size_t n_idx, size_t ldd);
-typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_size_func_t)(size_t m, size_t n);
-typedef void (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_run_gemm_func_t)(
+typedef size_t (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_size_func)(size_t m, size_t n);
+typedef void (*tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_run_gemm_func)(
     size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_idx_a, const void *B,
     size_t ldb, size_t k_idx_b, const void *C, size_t ldc, void *D, size_t ldd, const void *bias,
     int8_t clamp_min, int8_t clamp_max, const struct tqt_qai8_qsi8dx_qai8_params *params);
 
 struct tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_ukernel
 {
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_m_step_func_t get_m_step;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_n_step_func_t get_n_step;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_a_offset_func_t get_a_offset;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_b_offset_func_t get_b_offset;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_c_offset_func_t get_c_offset;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_bias_offset_func_t get_bias_offset;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_offset_func_t get_d_offset;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_size_func_t get_d_size;
-    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_run_gemm_func_t run_gemm;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_m_step_func get_m_step;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_n_step_func get_n_step;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_a_offset_func get_a_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_b_offset_func get_b_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_c_offset_func get_c_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_bias_offset_func get_bias_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_offset_func get_d_offset;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_get_d_size_func get_d_size;
+    tqt_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_run_gemm_func run_gemm;
 };
 
 #ifdef __cplusplus

@@ -16,6 +16,8 @@ extern "C" {
 
 typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_m_step_func_t)(void);
 typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_n_step_func_t)(void);
+typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_b_packed_offset_func_t)(
+    size_t n_idx, size_t k_idx, size_t ldb, size_t actual_n);
 typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_c_offset_func_t)(
     size_t m_idx, size_t n_idx, size_t ldc);
 typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_bias_offset_func_t)(
@@ -24,6 +26,8 @@ typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_d_of
     size_t m_idx, size_t n_idx, size_t ldd);
 typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_d_size_func_t)(
     size_t m, size_t n);
+typedef size_t (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_b_packed_size_func_t)(
+    size_t n, size_t k);
 typedef void (*tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_run_bt_pack_func_t)(
     size_t n, size_t k, size_t ldw, size_t ldw_packed, size_t k_idx, const void *weight,
     void *weight_packed);
@@ -37,10 +41,12 @@ struct tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_ukernel
 {
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_m_step_func_t get_m_step;
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_n_step_func_t get_n_step;
+    tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_b_packed_offset_func_t get_b_packed_offset;
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_c_offset_func_t get_c_offset;
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_bias_offset_func_t get_bias_offset;
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_d_offset_func_t get_d_offset;
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_d_size_func_t get_d_size;
+    tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_get_b_packed_size_func_t get_b_packed_size;
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_run_bt_pack_func_t run_bt_pack;
     tqt_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_run_igemm_func_t run_igemm;
 };
