@@ -745,7 +745,8 @@ constexpr int kSK = 128;  // k bytes per pipeline stage
 // kernels order these writes themselves with explicit vmcnt waits and s_barrier; the "memory"
 // clobber keeps the compiler's own LDS accesses on their side of each load. M0 carries the LDS
 // base (the low 32 bits of a flat LDS address are its LDS offset); nothing else in these kernels
-// uses M0.
+// uses M0. gfx9 needs one wait state between an SALU write of M0 and an LDS-DMA load that reads
+// it; the compiler cannot insert it inside an asm block, so the asm carries its own s_nop 0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma_lds16(const int8_t *src, int8_t *lds)
@@ -753,7 +754,7 @@ __device__ __forceinline__ void dma_lds16(const int8_t *src, int8_t *lds)
 #if defined(__HIP_DEVICE_COMPILE__)
     const uint32_t base =
         __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base)
                  : "memory", "m0");
 #else
     (void)src;
@@ -768,7 +769,7 @@ __device__ __forceinline__ void dma_lds16_buf(i32x4 rsrc, int voffset, int8_t *l
 #if defined(__HIP_DEVICE_COMPILE__)
     const uint32_t base =
         __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset),
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset),
                  "s"(rsrc), "s"(base)
                  : "memory", "m0");
 #else
