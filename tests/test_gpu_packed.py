@@ -4,9 +4,8 @@
   (tqt_testlib.pack_panels), including tail panels, rows whose length is not a multiple of the
   16-byte chunk, ld_packed > k, and k_idx sub-buffers (the reference's tail rule).
 * Packed runs: bit-exact against the CPU oracle (int32, int8 and W4A8 f32 outputs) or, for
-  W4A16, bit-exact against the unpacked run of the same inputs (itself held to the oracle by
-  test_gpu_parity.py) - packing is a permutation, so a packed run must reproduce the unpacked
-  result exactly. The reference's own packed test drivers (quantized_gemm_test_runner.h:482-699:
+  W4A16, bit-exact against the unpacked run of the same inputs - packing is a permutation, so a
+  packed run must reproduce the unpacked result exactly - and within 2 f16 ULP of the oracle. The reference's own packed test drivers (quantized_gemm_test_runner.h:482-699:
   pack, walk m_step x n_step tiles through the packed offset getters, compare) are replayed.
 * k_idx: a K split into sub-buffers packed with their k_idx and run one after the other with C
   accumulation reproduces the full product.
@@ -292,10 +291,27 @@ def run_w4a16p(shim, d, lda_extra=0):
 
 @pytest.mark.parametrize("m,n,k,bl", W4A16_SHAPES)
 def test_w4a16_packed_run_matches_unpacked(gpu, shim, m, n, k, bl):
+    """Bit-identical to the unpacked run, and both held to the golden-pinned f32 oracle with
+    the same <= 2 f16 ULP bar as the unpacked parity tests."""
+    from test_gpu_parity import check_w4a16
+
     d = T.gen_w4a16(m, n, k, bl=bl, seed=m + n + k, with_c=(n % 3 == 0))
     got, cmin, cmax = run_w4a16p(shim, d, lda_extra=(64 if m > 32 else 0))
-    exp = _g().run_w4a16(shim, d, cmin, cmax)
-    np.testing.assert_array_equal(got, exp)
+    unpacked = _g().run_w4a16(shim, d, cmin, cmax)
+    np.testing.assert_array_equal(got, unpacked)
+    exp = T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], bl, d["C16"], d["bias16"], cmin, cmax)
+    check_w4a16(got, exp, d, (-65504.0, 65504.0))
+
+
+def test_w4a16_packed_config4_full(gpu, shim):
+    """BASELINE cfg 4 at full size (M=32, K=4096, N=14336, bl=32) through the packed type:
+    <= 2 f16 ULP against the oracle."""
+    from test_gpu_parity import check_w4a16
+
+    d = T.gen_w4a16(32, 14336, 4096, bl=32, seed=42)
+    got, cmin, cmax = run_w4a16p(shim, d)
+    exp = T.oracle_w4a16(d["A16"], d["Bp"], d["S16"], 32, None, d["bias16"], cmin, cmax)
+    check_w4a16(got, exp, d, (-65504.0, 65504.0))
 
 
 IGEMM_SHAPES = [(32, 48, 9, 9, 3, 3, (1, 1), (1, 1), (1, 1)),

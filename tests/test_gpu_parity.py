@@ -197,12 +197,23 @@ def ulp_distance_f16(got_bits, exp_vals, S):
 
 
 def check_w4a16(got, exp, d, clamp):
+    """<= 2 f16 ULP against the f32-accumulating oracle and against exact math, with the ULP
+    floored at 2^-13 * sum|a*w|. The outputs that pass only because of that floor (more than
+    2 ULP of max(|expected|, 2^-14) from the oracle) are counted, printed and held to at most
+    0.1% of the outputs (and 8 at least), so the floor cannot hide a systematic error."""
     exact, S = w4a16_exact_and_scale(d)
     exact = np.clip(exact, clamp[0], clamp[1])
-    d_oracle = ulp_distance_f16(got, T.bits_f16(exp).astype(np.float64), S)
+    e_oracle = T.bits_f16(exp).astype(np.float64)
+    d_oracle = ulp_distance_f16(got, e_oracle, S)
     d_exact = ulp_distance_f16(got, exact.astype(np.float16).astype(np.float64), S)
     assert d_oracle.max() <= 2.0, "max ULP vs oracle %s" % d_oracle.max()
     assert d_exact.max() <= 2.0, "max ULP vs exact %s" % d_exact.max()
+    d_plain = ulp_distance_f16(got, e_oracle, np.zeros_like(S))
+    on_floor = int((d_plain > 2.0).sum())
+    print("W4A16 %dx%d: %d of %d outputs within 2 ULP only on the 2^-13*sum|a*w| floor "
+          "(max plain ULP %.1f)" % (got.shape[0], got.shape[1], on_floor, got.size,
+                                   float(d_plain.max())))
+    assert on_floor <= max(8, got.size // 1000), on_floor
     return d_oracle, d_exact
 
 

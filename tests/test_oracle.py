@@ -709,3 +709,154 @@ def test_live_reference_matches_golden():
     r.tqtr_reference_gemm_i32_i8(int(m), int(n), int(k), T.ptr(A), int(k), T.ptr(B), int(n), 0,
                                  None, int(n), T.ptr(D), int(n), -100000, 100000)
     np.testing.assert_array_equal(D, g["clamp_5_D"])
+
+
+# ------------------------------------------------------------------------------------------
+# Per-row asymmetric activation quantization (qai8dx; test/gemm/test_gemm_i8_i4_rvv.cpp:40-77)
+# ------------------------------------------------------------------------------------------
+
+def oracle_per_row(X):
+    X = np.ascontiguousarray(X, np.float32)
+    m, k = X.shape
+    q = np.zeros((m, k), np.int8)
+    s = np.zeros(m, np.float32)
+    z = np.zeros(m, np.int32)
+    T.oracle().tqto_quantize_a_per_row_asym(T.ptr(X), m, k, T.ptr(q), T.ptr(s), T.ptr(z))
+    return q, s, z
+
+
+def per_row_violations(X, q, s, z):
+    """Properties that asymmetric per-row int8 quantization over [min(x, 0), max(x, 0)] must
+    have, independent of how it is computed. Returns a list of violated properties (empty when
+    all hold). Every element is checked against the golden-pinned quantize_i8 too."""
+    bad = []
+    o = T.oracle()
+    for r in range(X.shape[0]):
+        x = X[r].astype(np.float64)
+        lo, hi = min(x.min(), 0.0), max(x.max(), 0.0)
+        sr, zr, qr = float(s[r]), int(z[r]), q[r].astype(np.int64)
+        if lo == hi == 0.0:
+            if not (sr == 1.0 and zr == 0 and not qr.any()):
+                bad.append("zero row")
+            continue
+        # the scale spreads [lo, hi] over the 255 steps of int8
+        if abs(sr * 255.0 - (hi - lo)) > 4e-7 * (hi - lo) + 255 * 2.0 ** -149:
+            bad.append("scale")
+        if not -128 <= zr <= 127:
+            bad.append("zero point range")
+        if lo == 0.0 and zr != -128:
+            bad.append("one-signed row (>= 0) zero point")
+        if hi == 0.0 and zr != 127:
+            bad.append("one-signed row (<= 0) zero point")
+        # real zero is representable: x = 0 quantizes to the zero point
+        if int(o.tqto_quantize_i8(0.0, sr, zr)) != zr:
+            bad.append("zero not exact")
+        # the row's extremes land on the ends of the int8 range (a negative minimum on -128, a
+        # positive maximum on 127), unless x / s sits within 1e-3 of a rounding tie or the
+        # scale is subnormal (then s no longer carries 24 bits, and 255 s != hi - lo)
+        def near_tie(v):
+            if sr < 2.0 ** -126:
+                return True
+            u = abs(float(np.float32(v) / np.float32(sr)))
+            return abs(u - np.floor(u) - 0.5) < 1e-3
+
+        if x.min() < 0 and not near_tie(x.min()) and qr[np.argmin(x)] != -128:
+            bad.append("minimum not on -128")
+        if x.max() > 0 and not near_tie(x.max()) and qr[np.argmax(x)] != 127:
+            bad.append("maximum not on 127")
+        # round to nearest: dequantized values lie within half a step, unless saturated
+        deq = (qr - zr) * sr
+        inner = (qr > -128) & (qr < 127)
+        if np.any(np.abs(deq - x)[inner] > 0.5 * sr * (1 + 1e-5)):
+            bad.append("rounding")
+        if np.any(x[qr == -128] > (-128 - zr + 0.5) * sr * (1 + 1e-5) + 1e-30):
+            bad.append("low saturation")
+        if np.any(x[qr == 127] < (127 - zr - 0.5) * sr * (1 - 1e-5) - 1e-30):
+            bad.append("high saturation")
+        # monotone in x
+        order = np.argsort(x, kind="stable")
+        if np.any(np.diff(qr[order]) < 0):
+            bad.append("monotone")
+        # each element is the golden-pinned quantize_i8 step with this row's parameters
+        if any(int(o.tqto_quantize_i8(float(v), sr, zr)) != int(w) for v, w in
+               zip(X[r][:64], q[r][:64])):
+            bad.append("quantize_i8 step")
+    return bad
+
+
+def test_per_row_quantize_known_answers():
+    """Hand-worked rows whose range is 255 (or 510) in binary-exact values, so the scale is
+    exactly 1 (or 2) and each zero point and value follows from nearbyint (half to even) alone:
+      [-100.75, 154.25]: zp = nearbyint(-128 + 100.75 = -27.25) = -27 (floor would give -28);
+      [-100.25, 154.75]: zp = nearbyint(-27.75) = -28 (truncation would give -27);
+      [-100.5, 154.5]:   zp = nearbyint(-27.5) = -28 and 154.5 -> 154 (half to even);
+      s = 2, [-201.5, 308.5]: zp = nearbyint(-128 + 100.75) = -27."""
+    X = np.array([
+        [-100.75, 0.0, 154.25, 10.5, 11.5, -3.5],
+        [-100.25, 0.0, 154.75, 10.5, 11.5, -3.5],
+        [-100.5, 0.0, 154.5, 10.5, 11.5, -3.5],
+        [-201.5, 0.0, 308.5, 21.0, 23.0, -7.0],
+    ], np.float32)
+    q, s, z = oracle_per_row(X)
+    np.testing.assert_array_equal(s, [1.0, 1.0, 1.0, 2.0])
+    np.testing.assert_array_equal(z, [-27, -28, -28, -27])
+    # value = nearbyint(x / s) + zp, saturated: -100.75 -> -101 - 27 = -128; 154.25 -> 127;
+    # 10.5 -> 10 (even); 11.5 -> 12; -3.5 -> -4
+    np.testing.assert_array_equal(q, [
+        [-128, -27, 127, -17, -15, -31],
+        [-128, -28, 127, -18, -16, -32],
+        [-128, -28, 126, -18, -16, -32],
+        [-128, -27, 127, -17, -15, -31],
+    ])
+
+
+def test_per_row_quantize_special_rows():
+    X = np.array([
+        [0.0] * 8,                                   # all zero -> (1.0, 0, zeros)
+        [0.5, 1.0, 2.0, 0.25, 3.0, 0.125, 1.5, 0.0],  # all >= 0 -> zp -128
+        [-0.5, -1.0, -2.0, -0.25, -3.0, 0.0, -1.5, -0.125],  # all <= 0 -> zp 127
+        [7.0] * 8,                                   # constant positive: every value 127
+        [-7.0] * 8,                                  # constant negative: every value -128
+        [1e-40, -1e-40, 0, 0, 0, 0, 0, 1e-40],       # subnormal range
+    ], np.float32)
+    q, s, z = oracle_per_row(X)
+    assert (s[0], z[0]) == (1.0, 0) and not q[0].any()
+    assert z[1] == -128 and z[2] == 127
+    assert (q[3] == 127).all() and z[3] == -128
+    assert (q[4] == -128).all() and z[4] == 127
+    assert per_row_violations(X, q, s, z) == []
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_per_row_quantize_properties(seed):
+    rng = np.random.default_rng(seed)
+    X = np.concatenate([
+        rng.standard_normal((6, 512)),
+        rng.standard_normal((2, 512)) * 1e-3 + 0.5,       # one-signed, narrow
+        rng.uniform(-5, 1, (2, 512)),                      # skewed
+        rng.standard_normal((2, 512)) * 1e4,
+    ]).astype(np.float32)
+    q, s, z = oracle_per_row(X)
+    assert per_row_violations(X, q, s, z) == []
+
+
+def test_per_row_quantize_properties_reject_planted_mistakes():
+    """The property checker has teeth: quantizers with one step changed (restated in numpy on
+    the CPU) each violate a property on ordinary rows."""
+    rng = np.random.default_rng(7)
+    X = rng.standard_normal((6, 256)).astype(np.float32)
+
+    def quantizer(scale_div=255.0, zp_off=-128.0, round_zp=np.rint, clip=True):
+        lo = np.minimum(X.min(axis=1), 0).astype(np.float32)
+        hi = np.maximum(X.max(axis=1), 0).astype(np.float32)
+        s = ((hi - lo) / np.float32(scale_div)).astype(np.float32)
+        z = round_zp(np.float32(zp_off) - lo / s).astype(np.int64)
+        if clip:
+            z = np.clip(z, -128, 127)
+        q = np.clip(np.rint(X / s[:, None]) + z[:, None], -128, 127).astype(np.int8)
+        return q, s, z.astype(np.int32)
+
+    assert per_row_violations(X, *quantizer()) == []          # the unplanted form passes
+    for plant in (dict(scale_div=256.0), dict(zp_off=-127.0), dict(zp_off=0.0),
+                  dict(round_zp=np.floor)):
+        assert per_row_violations(X, *quantizer(**plant)), plant
