@@ -46,6 +46,8 @@ W4A8 = dict(m=1, n=11008, k=4096)
 W4A16 = dict(m=32, n=14336, k=4096, bl=32)
 CONV = dict(ID=8, IH=56, IW=56, IC=128, OC=128, KH=3, KW=3, pad=1)
 CLAMP = dict(m=64, n=256, k=512)
+# W4A8 M=1 algorithmic bytes: B n*k/2 + scale_b 4n + bias 4n + A m*k + 8m + D 4mn
+W4A8_BYTES = 11008 * 4096 // 2 + 8 * 11008 + 4096 + 8 + 4 * 11008
 
 
 def load_lib():
@@ -68,12 +70,30 @@ class Timer:
     Default: the `steps` launches (each on its own weight copy) are captured once into a HIP
     graph and the graph is replayed between the two events, so the figure is the kernels'
     back-to-back cost without per-launch host overhead. `stream_ms` also times the same launches
-    issued one by one on the stream."""
+    issued one by one on the stream.
+
+    Cache state: right before the start event, a kernel reads a buffer of twice the Infinity
+    Cache (MALL), so no timed launch finds a copy that warm-up or an earlier replay left in the
+    MALL or an L2 (a read, so no dirty lines are left whose write-back the timed launches would
+    pay); inside the timed region a copy is read again only after `copies` launches, which
+    together read more than the MALL holds (copies_for)."""
 
     def __init__(self, torch, stream, graphs=True):
         self.torch = torch
         self.stream = stream
         self.graphs = graphs
+        self.sup = load_support()
+        self.flush_buf = torch.zeros(2 * CACHE_BYTES, dtype=torch.uint8, device="cuda")
+        self.flush_sink = torch.zeros(2 * CACHE_BYTES // (8 * 4096), dtype=torch.int32,
+                                      device="cuda")
+
+    def flush(self):
+        """Read (not write) 2x the MALL on the timing stream: evicts the operands from the MALL
+        and the L2s and leaves no dirty lines whose write-back the timed launches would pay."""
+        if self.sup.tqtb_read_floor_async(self.flush_buf.data_ptr(), self.flush_buf.numel(),
+                                          self.flush_sink.data_ptr(), self.flush_sink.numel(), 8,
+                                          self.stream.cuda_stream):
+            raise RuntimeError("cache flush launch failed")
 
     def _events(self):
         torch = self.torch
@@ -84,6 +104,7 @@ class Timer:
         for i in range(warmup):
             launch(i % copies)
         torch.cuda.synchronize()
+        self.flush()
         start, end = self._events()
         start.record(self.stream)
         for i in range(steps):
@@ -105,6 +126,7 @@ class Timer:
                 launch((warmup + i) % copies)
         graph.replay()  # untimed: first replay uploads the graph
         torch.cuda.synchronize()
+        self.flush()
         start, end = self._events()
         start.record(self.stream)
         graph.replay()
@@ -230,6 +252,24 @@ def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m, packed=False, dynq
                 ops=2.0 * m * n * k, copies=nc, inputs=(A, Bp, sa, za, sb, bias))
 
 
+def load_support():
+    """libtqt_bench_support.so: the read-floor kernel and the W4A16 forwarders that take the f16
+    clamp bounds as bit patterns (ctypes cannot pass _Float16 by value)."""
+    path = os.path.join(ROOT, "torq-tile_amd", "libtqt_bench_support.so")
+    if not os.path.exists(path):
+        raise RuntimeError("bench support library not built: %s (make -C torq-tile_amd)" % path)
+    sup = ctypes.CDLL(path)
+    sz, vp = ctypes.c_size_t, ctypes.c_void_p
+    sup.tqtb_read_floor_async.restype = ctypes.c_int
+    sup.tqtb_read_floor_async.argtypes = [vp, sz, vp, sz, ctypes.c_int, vp]
+    sup.tqtb_run_w4a16_async.restype = None
+    sup.tqtb_run_w4a16_async.argtypes = ([sz] * 4 + [vp, sz, vp, sz, vp, sz, vp, sz, vp, sz, vp,
+                                                    ctypes.c_uint16, ctypes.c_uint16, vp])
+    sup.tqtb_run_w4a16p_async.restype = None
+    sup.tqtb_run_w4a16p_async.argtypes = sup.tqtb_run_w4a16_async.argtypes
+    return sup
+
+
 def bench_w4a16(torch, mod, lib, timer, warmup, steps, rng, packed=False):
     """packed: the f16p_qsi4c2p sibling on the same inputs (packed once before timing)."""
     m, n, k, bl = W4A16["m"], W4A16["n"], W4A16["k"], W4A16["bl"]
@@ -249,39 +289,50 @@ def bench_w4a16(torch, mod, lib, timer, warmup, steps, rng, packed=False):
         dS.append(dS[0].clone())
     dbias = torch.from_numpy(bias).cuda()
     dD = torch.empty((m, n), dtype=torch.float16, device="cuda")
-    shim = ctypes.CDLL(os.path.join(ROOT, "tests", "abi_shim", "libtqt_test_shim.so"))
-    f = shim.tqts_run_w4a16_async
-    f.restype = None
-    f.argtypes = [ctypes.c_size_t] * 4 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
-                                          ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
-                                          ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
-                                          ctypes.c_size_t, ctypes.c_void_p, ctypes.c_uint16,
-                                          ctypes.c_uint16, ctypes.c_void_p]
+    sup = load_support()
+    f = sup.tqtb_run_w4a16p_async if packed else sup.tqtb_run_w4a16_async
     cmin = int(np.float16(-65504.0).view(np.uint16))
     cmax = int(np.float16(65504.0).view(np.uint16))
     s = timer.stream.cuda_stream
-    if packed:
-        fp = shim.tqts_run_w4a16p
-        fp.restype = None
-        fp.argtypes = ([ctypes.c_size_t] * 4 +
-                       [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p,
-                        ctypes.c_size_t, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
-                        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_size_t,
-                        ctypes.c_void_p, ctypes.c_uint16, ctypes.c_uint16, ctypes.c_void_p])
 
     def launch(i):
-        if packed:
-            fp(m, n, k, bl, dA.data_ptr(), k, 0, dB[i].data_ptr(), k, 0, dS[i].data_ptr(),
-               k // bl, None, n, dD.data_ptr(), n, dbias.data_ptr(), cmin, cmax, s)
-        else:
-            f(m, n, k, bl, dA.data_ptr(), k, dB[i].data_ptr(), k, dS[i].data_ptr(), k // bl, None,
-              n, dD.data_ptr(), n, dbias.data_ptr(), cmin, cmax, s)
+        f(m, n, k, bl, dA.data_ptr(), k, dB[i].data_ptr(), k, dS[i].data_ptr(), k // bl, None, n,
+          dD.data_ptr(), n, dbias.data_ptr(), cmin, cmax, s)
 
     ms = timer.run(launch, nc, warmup, steps)
     algo_bytes = Bp.nbytes + S.nbytes + A.nbytes + bias.nbytes + 2 * m * n
     flops = 2.0 * m * n * k
     return dict(ms=ms, gbs=algo_bytes / (ms * 1e-3) / 1e9, tflops=flops / (ms * 1e-3) / 1e12,
                 bytes=algo_bytes, ops=flops, copies=nc)
+
+
+FLOOR_LOADS = (1, 2, 4, 8, 16)
+
+
+def bench_floor(torch, timer, warmup, steps, nbytes):
+    """Single-launch HBM read floor for `nbytes` (the W4A8 M=1 operand bytes): one launch of a
+    plain streaming read per step (each workgroup reads loads x 4 KiB contiguous, all its loads
+    issued at once), over rotating copies like the kernel legs, for each per-lane load count in
+    FLOOR_LOADS; the fastest is the floor."""
+    sup = load_support()
+    nbytes = (nbytes + 15) // 16 * 16
+    nc = copies_for(nbytes)
+    src = [torch.zeros(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nc)]
+    sink_words = nbytes // 4096 + 1
+    sink = torch.zeros(sink_words, dtype=torch.int32, device="cuda")
+    s = timer.stream.cuda_stream
+    per_loads = {}
+    for loads in FLOOR_LOADS:
+        def launch(i, loads=loads):
+            if sup.tqtb_read_floor_async(src[i].data_ptr(), nbytes, sink.data_ptr(), sink_words,
+                                         loads, s):
+                raise RuntimeError("read floor launch failed")
+
+        per_loads[loads] = timer.run(launch, nc, warmup, steps)
+    best = min(per_loads, key=per_loads.get)
+    ms = per_loads[best]
+    return dict(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes, copies=nc, loads=best,
+                us_by_loads={b: round(v * 1e3, 3) for b, v in per_loads.items()})
 
 
 def bench_conv(torch, mod, lib, timer, warmup, steps, rng):
@@ -357,8 +408,23 @@ def bench_copy(torch, timer, warmup, steps):
 # HBM traffic per launch from rocprofv3 counters (FETCH_SIZE, then WRITE_SIZE)
 # ------------------------------------------------------------------------------------------
 
-PMC_LEGS = "w8a8,w4a8,copy"
-KERNEL_KEYS = {"w8a8": "int8_stream_kernel", "w4a8": "w4a8_mfma_kernel", "copy": "bitwise_not"}
+PMC_LEGS = "w8a8,w4a8,w4a16,conv,copy"
+TRAFFIC_LEGS = ("w8a8", "w4a8", "w4a16", "conv")
+
+
+def leg_of_kernel(name):
+    """Which bench leg a (demangled) kernel name belongs to, for the legs in PMC_LEGS."""
+    if "bitwise_not" in name:
+        return "copy"
+    if "w4a8_mfma_kernel" in name:
+        return "w4a8"
+    if "w4a16_" in name:
+        return "w4a16"
+    if "int8_stream_kernel<" in name or "igemm" in name:
+        # int8_stream_kernel<BM, EPI, PK, conv>: the convolution mode has conv = true
+        head = name.split(">")[0].rstrip()
+        return "conv" if (head.endswith("true") or "igemm" in name) else "w8a8"
+    return None
 
 
 def pmc_pass(counter, timeout_s=120):
@@ -388,16 +454,15 @@ def pmc_pass(counter, timeout_s=120):
         proc.wait()
         shutil.rmtree(out, ignore_errors=True)
         return None
-    vals = {leg: [] for leg in KERNEL_KEYS}
+    vals = {leg: [] for leg in PMC_LEGS.split(",")}
     for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
         with open(path, newline="") as fh:
             for row in csv.DictReader(fh):
                 if row.get("Counter_Name") != counter:
                     continue
-                name = row.get("Kernel_Name", "")
-                for leg, key in KERNEL_KEYS.items():
-                    if key in name:
-                        vals[leg].append(float(row["Counter_Value"]))
+                leg = leg_of_kernel(row.get("Kernel_Name", ""))
+                if leg in vals:
+                    vals[leg].append(float(row["Counter_Value"]))
     shutil.rmtree(out, ignore_errors=True)
     if not all(vals.values()):
         return None
@@ -405,8 +470,9 @@ def pmc_pass(counter, timeout_s=120):
 
 
 def hbm_traffic():
-    """HBM bytes per launch of the W8A8 and W4A8 kernels: FETCH_SIZE and WRITE_SIZE (KiB per
-    dispatch), each scaled by bytes / counter of the copy kernel, whose traffic is known."""
+    """HBM bytes per launch of the W8A8, W4A8, W4A16 and igemmcl kernels: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by bytes / counter of the copy kernel, whose
+    traffic is known."""
     fetch = pmc_pass("FETCH_SIZE")
     write = pmc_pass("WRITE_SIZE") if fetch else None
     if not fetch or not write:
@@ -416,7 +482,7 @@ def hbm_traffic():
     w_scale = nbytes / write["copy"]
     res = {"fetch_scale_bytes_per_KiB": round(f_scale, 2),
            "write_scale_bytes_per_KiB": round(w_scale, 2)}
-    for leg in ("w8a8", "w4a8"):
+    for leg in TRAFFIC_LEGS:
         res[leg] = {"read": fetch[leg] * f_scale, "write": write[leg] * w_scale,
                     "total": fetch[leg] * f_scale + write[leg] * w_scale}
     return res
@@ -426,38 +492,81 @@ def hbm_traffic():
 # CPU baseline (oracle restatement of the reference kernel; bounded sample)
 # ------------------------------------------------------------------------------------------
 
-def cpu_baseline(w8, budget_s=10.0, single_budget_s=8.0):
-    """The oracle's W8A8 (the reference's 4x16 tile loop in portable C) on the host cores: all
-    cores (OpenMP over tiles; the reported value) and one thread (reported beside it), each timed
-    over whole M=512 K=4096 N=4096 GEMMs for a bounded time."""
+def host_cpu():
+    """(threads to use, description): this process's CPU affinity capped at 16 threads, the CPU
+    share of one GPU on the GPU box (OMP_NUM_THREADS there), with nproc and the CPU model."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = max(1, min(16, avail))
+    return threads, dict(nproc=os.cpu_count(), affinity=avail, threads=threads, model=model)
+
+
+def cpu_baseline(w8, w4, budget_s=8.0, single_budget_s=6.0):
+    """The oracle's W8A8 and W4A8 (the reference's 4x16 tile loop in portable C, built with
+    -O3 -ffp-contract=off -fopenmp) on the host cores: OpenMP over output tiles (the
+    reference's threading model) on `threads` threads, and on one thread, each repeated over
+    whole config-sized calls for a bounded time. value = W8A8 TOPS on all threads."""
     import tqt_testlib as T
 
     o = T.oracle()
     A, B, sb, bias, _ = w8["inputs"]
     m, n, k = W8A8["m"], W8A8["n"], W8A8["k"]
     D = np.empty((m, n), np.int8)
+    A4, Bp4, sa4, za4, sb4, bias4 = w4["inputs"]
+    n4, k4 = W4A8["n"], W4A8["k"]
+    D4 = np.empty((1, n4), np.float32)
 
-    def timed(threads, budget):
+    def w8a8_call():
+        o.tqto_gemm_qai8_qai8_qsi8cxt(m, n, k, T.ptr(A), k, T.ptr(B), k, None, n, T.ptr(D), n,
+                                      T.ptr(bias), -128, 127, 0.02, T.ptr(sb), n, 0.05, 0)
+
+    def w4a8_call():
+        o.tqto_gemm_qai8dx_qsi4cxt_f32(1, n4, k4, T.ptr(A4), k4, T.ptr(Bp4), k4, None, n4,
+                                       T.ptr(D4), n4, T.ptr(bias4), -np.inf, np.inf, T.ptr(sa4),
+                                       T.ptr(za4), T.ptr(sb4))
+
+    def timed(call, threads, budget):
         o.tqto_set_threads(threads)
+        call()  # warm
         reps = 0
         t0 = time.perf_counter()
         while True:
-            o.tqto_gemm_qai8_qai8_qsi8cxt(m, n, k, T.ptr(A), k, T.ptr(B), k, None, n, T.ptr(D),
-                                          n, T.ptr(bias), -128, 127, 0.02, T.ptr(sb), n, 0.05, 0)
+            call()
             reps += 1
             el = time.perf_counter() - t0
             if el >= budget:
-                return reps, el, reps * 2.0 * m * n * k / el / 1e12
+                return reps, el
 
-    cores = min(16, os.cpu_count() or 1)
-    reps, el, tops = timed(cores, budget_s)
-    reps1, el1, tops1 = timed(1, single_budget_s)
-    o.tqto_set_threads(cores)
-    return dict(value=round(tops, 4), unit="TOPS", cores=cores, kind="port",
-                value_single_thread=round(tops1, 4),
-                sample="%d full W8A8 M=512 K=4096 N=4096 GEMMs on %d threads in %.1f s; %d on 1 "
-                       "thread in %.1f s (portable C, reference 4x16 tile loop, OpenMP over "
-                       "tiles)" % (reps, cores, el, reps1, el1))
+    threads, host = host_cpu()
+    r8, e8 = timed(w8a8_call, threads, budget_s)
+    r81, e81 = timed(w8a8_call, 1, single_budget_s)
+    r4, e4 = timed(w4a8_call, threads, budget_s / 2)
+    r41, e41 = timed(w4a8_call, 1, single_budget_s / 2)
+    o.tqto_set_threads(threads)
+    ops8 = 2.0 * m * n * k
+    w4_bytes = w4["bytes"]
+    return dict(value=round(r8 * ops8 / e8 / 1e12, 4), unit="TOPS", cores=threads, kind="port",
+                value_single_thread=round(r81 * ops8 / e81 / 1e12, 4),
+                w4a8={"value": round(r4 * w4_bytes / e4 / 1e9, 3), "unit": "GB/s",
+                      "value_single_thread": round(r41 * w4_bytes / e41 / 1e9, 3),
+                      "us_per_call": round(e4 / r4 * 1e6, 1)},
+                host=host,
+                sample="W8A8 M=512 K=4096 N=4096: %d calls on %d threads in %.1f s, %d on 1 thread "
+                       "in %.1f s; W4A8 M=1 K=4096 N=11008: %d calls on %d threads in %.1f s, %d "
+                       "on 1 thread in %.1f s (oracle/ portable C: the reference's 4x16 tile "
+                       "loop, OpenMP over tiles, -O3 -ffp-contract=off)"
+                       % (r8, threads, e8, r81, e81, r4, threads, e4, r41, e41))
 
 
 def main():
@@ -472,7 +581,7 @@ def main():
                     help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,w4a16p,w4a8dq,conv,"
-                         "clamp,copy): "
+                         "clamp,copy,floor): "
                          "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -505,29 +614,44 @@ def main():
             "conv": lambda: bench_conv(torch, mod, lib, timer, W, K, rng),
             "clamp": lambda: bench_clamp(torch, mod, lib, timer, W, K, rng),
             "copy": lambda: bench_copy(torch, timer, W, K),
+            "floor": lambda: bench_floor(torch, timer, W, K, W4A8_BYTES),
         }
         with torch.cuda.stream(stream):
             for leg in args.only.split(","):
                 r = legs[leg]()
-                print(json.dumps({"leg": leg, "us_per_launch": round(r["ms"] * 1e3, 3),
-                                  "bytes": r["bytes"], "copies": r["copies"]}), flush=True)
+                line = {"leg": leg, "us_per_launch": round(r["ms"] * 1e3, 3),
+                        "bytes": r["bytes"], "copies": r["copies"]}
+                if "us_by_loads" in r:
+                    line["us_by_loads"] = r["us_by_loads"]
+                print(json.dumps(line), flush=True)
         return
 
+    def progress(name, r):
+        print("bench: %s %.3f us per launch" % (name, r["ms"] * 1e3), file=sys.stderr,
+              flush=True)
+        return r
+
     with torch.cuda.stream(stream):
-        w8 = bench_w8a8(torch, mod, lib, timer, W, K, rng)
-        w4 = {mm: bench_w4a8(torch, mod, lib, timer, W, K, rng, mm) for mm in (1, 4, 8)}
-        w416 = bench_w4a16(torch, mod, lib, timer, W, K, rng)
-        cv = bench_conv(torch, mod, lib, timer, W, K, rng)
-        cl = bench_clamp(torch, mod, lib, timer, W, K, rng)
-        w8p = bench_w8a8(torch, mod, lib, timer, W, K, rng, packed=True)
-        w4p = bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True)
-        w416p = bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True)
-        w4dq = bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True)
+        w8 = progress("w8a8", bench_w8a8(torch, mod, lib, timer, W, K, rng))
+        w4 = {mm: progress("w4a8 M=%d" % mm, bench_w4a8(torch, mod, lib, timer, W, K, rng, mm))
+              for mm in (1, 4, 8)}
+        w416 = progress("w4a16", bench_w4a16(torch, mod, lib, timer, W, K, rng))
+        cv = progress("igemmcl", bench_conv(torch, mod, lib, timer, W, K, rng))
+        cl = progress("clamp_i32", bench_clamp(torch, mod, lib, timer, W, K, rng))
+        w8p = progress("w8a8 packed", bench_w8a8(torch, mod, lib, timer, W, K, rng, packed=True))
+        w4p = progress("w4a8 packed",
+                       bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True))
+        w416p = progress("w4a16 packed",
+                         bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True))
+        w4dq = progress("w4a8 decode step",
+                        bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True))
+        fl = progress("read floor", bench_floor(torch, timer, W, K, w4[1]["bytes"]))
 
     w41 = w4[1]
     traffic = None if args.no_traffic else hbm_traffic()
-    t_w8 = round(traffic["w8a8"]["total"]) if traffic else None
-    t_w4 = round(traffic["w4a8"]["total"]) if traffic else None
+    print("bench: traffic counters %s" % ("done" if traffic else "skipped or unavailable"),
+          file=sys.stderr, flush=True)
+    tr = {leg: (round(traffic[leg]["total"]) if traffic else None) for leg in TRAFFIC_LEGS}
     out = {
         "metric": "W4A8 GEMV HBM GB/s (M=1) + W8A8 GEMM int8 TOPS (M=512), % roofline",
         "value": round(w8["tops"], 3),
@@ -550,14 +674,20 @@ def main():
                    "M": 512, "K": 4096, "N": 4096},
         "roofline": {"bound": "mfma", "achieved": round(w8["tops"], 3), "peak": INT8_PEAK_TOPS,
                      "unit": "TOPS", "frac": round(w8["tops"] / INT8_PEAK_TOPS, 4),
-                     "traffic": t_w8, "algorithmic_bytes": w8["bytes"]},
+                     "traffic": tr["w8a8"], "algorithmic_bytes": w8["bytes"]},
         "w4a8": {
             "workload": "gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt M=1 K=4096 N=11008 (W4A8 decode)",
             "value": round(w41["gbs"], 2), "unit": "GB/s", "us_per_launch": round(w41["ms"] * 1e3, 3),
             "us_per_launch_stream_launches": round(w41["ms_stream"] * 1e3, 3),
             "roofline": {"bound": "hbm", "achieved": round(w41["gbs"], 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(w41["gbs"] / HBM_PEAK_GBS, 4),
-                         "traffic": t_w4, "algorithmic_bytes": w41["bytes"]},
+                         "traffic": tr["w4a8"], "algorithmic_bytes": w41["bytes"]},
+            # one launch of a plain 16-byte streaming read of the same bytes (rotating copies,
+            # fastest of FLOOR_LOADS shapes): the single-launch HBM read floor on this GPU
+            "read_floor": {"us": round(fl["ms"] * 1e3, 3), "GB/s": round(fl["gbs"], 2),
+                           "frac": round(fl["gbs"] / HBM_PEAK_GBS, 4),
+                           "loads_per_lane": fl["loads"], "us_by_loads": fl["us_by_loads"]},
+            "frac_of_read_floor": round(fl["ms"] / w41["ms"], 4),
             "M4": {"GB/s": round(w4[4]["gbs"], 2), "us": round(w4[4]["ms"] * 1e3, 3),
                    "frac": round(w4[4]["gbs"] / HBM_PEAK_GBS, 4)},
             "M8": {"GB/s": round(w4[8]["gbs"], 2), "us": round(w4[8]["ms"] * 1e3, 3),
@@ -570,10 +700,15 @@ def main():
             "w4a16 32x14336x4096 bl32": {"us": round(w416["ms"] * 1e3, 3),
                                          "GB/s": round(w416["gbs"], 2),
                                          "hbm_frac": round(w416["gbs"] / HBM_PEAK_GBS, 4),
-                                         "TFLOP/s": round(w416["tflops"], 2)},
+                                         "TFLOP/s": round(w416["tflops"], 2),
+                                         "f16_mfma_frac": round(w416["tflops"] / F16_PEAK_TFLOPS, 4),
+                                         "traffic": tr["w4a16"],
+                                         "algorithmic_bytes": w416["bytes"]},
             "igemmcl 8x56x56x128 3x3 OC128": {"us": round(cv["ms"] * 1e3, 3),
                                               "TOPS": round(cv["tops"], 3),
-                                              "mfma_frac": round(cv["tops"] / INT8_PEAK_TOPS, 4)},
+                                              "mfma_frac": round(cv["tops"] / INT8_PEAK_TOPS, 4),
+                                              "traffic": tr["conv"],
+                                              "algorithmic_bytes": cv["bytes"]},
             # packed siblings on the same configurations (operands packed before timing)
             "packed qai8_qai8p_qsi8cxp 512x4096x4096": {
                 "us": round(w8p["ms"] * 1e3, 3), "TOPS": round(w8p["tops"], 3),
@@ -595,11 +730,11 @@ def main():
                       "by the counters of a 256 MB bitwise_not copy kernel",
             "fetch_scale_bytes_per_KiB": traffic["fetch_scale_bytes_per_KiB"],
             "write_scale_bytes_per_KiB": traffic["write_scale_bytes_per_KiB"],
-            "w8a8": {k: round(v) for k, v in traffic["w8a8"].items()},
-            "w4a8": {k: round(v) for k, v in traffic["w4a8"].items()},
         }
+        for leg in TRAFFIC_LEGS:
+            out["traffic_detail"][leg] = {k: round(v) for k, v in traffic[leg].items()}
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(w8)
+        out["cpu_baseline"] = cpu_baseline(w8, w41)
     print(json.dumps(out), flush=True)
 
 
