@@ -17,9 +17,11 @@
 //     sum is shifted right by 4 (exact: |16 * sum| < 2^31 for k <= 65536).
 //   * Activation row `rows` of the 16-row A operand is all ones, so that accumulator row is
 //     16 * sum_k (q - 8), the rsum_b of the reference; rows past it are zero.
-//   * Activations are permuted to the (even k, odd k) byte order of the decoded weights; each
-//     wave stages its own k-slice in LDS when it fits one 16-byte load per lane (decode-sized
-//     m), else they are loaded per step.
+//   * Activations are permuted to the (even k, odd k) byte order of the decoded weights. Each
+//     wave stages the activation rows of its own k-slice in LDS once (up to 8 16-byte loads per
+//     lane, only the chunk's real rows, issued before the weights; row slices XOR-swizzled by
+//     row so the operand reads are conflict-free), with no workgroup barrier: a wave reads back
+//     only what it wrote. Slices too large for that are loaded per step from global memory.
 // The eight waves' partial sums meet in LDS and the reference's f32 epilogue (zero-point
 // correction, two scale multiplies, C, bias, clamp; no FMA) runs per output.
 #include "tqt_hip_common.hpp"
@@ -112,15 +114,24 @@ __device__ __forceinline__ void decode_w16(const u32x4 w, i32x4 &q0, i32x4 &q1)
     q1[3] = static_cast<int32_t>((w[3] & 0xf0f0f0f0u) ^ 0x80808080u);
 }
 
-template <bool kActInLds, int PK, int OUT>
+// Dynamic LDS of the activation-staging path: kWaves slices of act_slice_bytes() bytes.
+constexpr int kMaxActLoads = 8;  // 16-byte activation loads per lane, at most
+
+__host__ __device__ inline int act_slice_bytes(int rows_max, int ppw)
+{
+    return rows_max * ppw * kPairK;
+}
+
+template <int kActLoads, int PK, int OUT>
 __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
 {
     constexpr bool kDirect = (PK & PK_B) != 0;  // weights straight into operand registers
-    __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][kDirect ? 1 : 2 * kPairsPerBatch]
-                                                       [kDirect ? 16 : 1024];
-    // activations of each wave's k-slice (one 16-byte chunk per lane at most)
-    __shared__ __attribute__((aligned(16))) int8_t s_a[kWaves][kActInLds ? 1024 : 16];
-    __shared__ int32_t s_part[kWaves][16][16];
+    constexpr bool kActInLds = kActLoads > 0;
+    // per wave: one pair of staged weights (16 rows x 128 bytes), reused pair after pair; after
+    // the main loop it holds the wave's 16 x 16 int32 partial sums
+    __shared__ __attribute__((aligned(16))) uint8_t s_w[kWaves][2 * 1024];
+    // activations of each wave's k-slice: rows_max rows of ppw * 256 bytes (dynamic size)
+    extern __shared__ __attribute__((aligned(16))) int8_t s_dyn[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -167,25 +178,33 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
     const bool a_ones = fr == rows;
 
     // LDS path: this wave's activation slice, rows x [p_begin, p_end) pairs (row stride
-    // npw * 256 bytes), one 16-byte chunk per lane. It is loaded before the weights, so its
-    // ds_write below waits for this load only (loads complete in order), and no workgroup
-    // barrier is needed: a wave reads back only what it wrote.
+    // npw * 256 bytes), 16-byte chunk q at lane q % 64, load q / 64. Chunk c of row r is stored
+    // at slot c ^ (r & 7) of the row, so the 8 lanes of a ds_read_b128 phase (rows 0-7 or 8-15,
+    // same chunk) hit 8 different 16-byte slots. The loads are issued before the weights, so the
+    // ds_writes below wait for these loads only (loads complete in order).
     const int npw = p_end - p_begin;
     const int a_chunks = rows * npw * 16;
-    i32x4 a_chunk = zero;
+    int8_t *s_a = s_dyn + wave * act_slice_bytes(min(kRowsPerChunk, a.M), ppw);
+    i32x4 a_chunk[kActInLds ? kActLoads : 1];
     if constexpr (kActInLds) {
-        if (lane < a_chunks) {
-            const int r = lane / (npw * 16);
-            const int off = (lane - r * npw * 16) * 16;
-            int mul = 1;  // k multiplier of a packed row (its panel width)
-            long long base;
-            if constexpr ((PK & PK_A) != 0) {
-                base = pack_row(a.pa, m0 + r, mul);
-            } else {
-                base = static_cast<long long>(m0 + r) * a.lda;
+        if (a_chunks > 0) {
+#pragma unroll
+            for (int j = 0; j < kActLoads; ++j) {
+                // unconditional: chunks past the slice reload its last chunk (not stored)
+                const int q = min(lane + 64 * j, a_chunks - 1);
+                const int r = q / (npw * 16);
+                const int off = (q - r * npw * 16) * 16;
+                int mul = 1;  // k multiplier of a packed row (its panel width)
+                long long base;
+                if constexpr ((PK & PK_A) != 0) {
+                    base = pack_row(a.pa, m0 + r, mul);
+                } else {
+                    base = static_cast<long long>(m0 + r) * a.lda;
+                }
+                a_chunk[j] = *reinterpret_cast<const i32x4 *>(
+                    a.A + base +
+                    pack_k<kPackW4A8Chunk, (PK & PK_A) != 0>(p_begin * kPairK + off, mul));
             }
-            a_chunk = *reinterpret_cast<const i32x4 *>(
-                a.A + base + pack_k<kPackW4A8Chunk, (PK & PK_A) != 0>(p_begin * kPairK + off, mul));
         }
     }
     // register path: this lane's activation row (row rows - 1 for the ones/zero lanes) and the
@@ -250,33 +269,44 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         // their uses and serialize the stream); emits no instruction
         asm volatile("" ::: "memory");
         if constexpr (kActInLds) {
-            if (pb == p_begin && lane < a_chunks) {
-                *reinterpret_cast<i32x4 *>(&s_a[wave][lane * 16]) = a_chunk;
+            if (pb == p_begin) {
+#pragma unroll
+                for (int j = 0; j < kActLoads; ++j) {
+                    const int q = lane + 64 * j;
+                    if (q < a_chunks) {
+                        const int r = q / (npw * 16);
+                        const int c = q - r * npw * 16;
+                        *reinterpret_cast<i32x4 *>(&s_a[r * npw * 256 + ((c ^ (r & 7)) << 4)]) =
+                            a_chunk[j];
+                    }
+                }
             }
         }
 #pragma unroll
         for (int pp = 0; pp < kPairsPerBatch; ++pp) {
-            // stage this pair: (row, chunk) at row * 128 + ((chunk ^ (row & 7)) << 4)
-            if constexpr (!kDirect) {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int j = 2 * pp + h;
-                    *reinterpret_cast<u32x4 *>(&s_w[wave][j][r8 * 128 + ((c8 ^ r8) << 4)]) = wr[j];
-                }
-            }
             const int pair = pb + pp;
             if (pair >= p_end) {
                 break;
+            }
+            // stage this pair: (row, chunk) at row * 128 + ((chunk ^ (row & 7)) << 4), rows 8-15
+            // in the second KiB. The buffer is the previous pair's: this wave's LDS accesses run
+            // in program order, so these writes follow its reads of that pair.
+            if constexpr (!kDirect) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    *reinterpret_cast<u32x4 *>(&s_w[wave][h * 1024 + r8 * 128 + ((c8 ^ r8) << 4)]) =
+                        wr[2 * pp + h];
+                }
             }
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 i32x4 v0, v1;
                 if constexpr (kActInLds) {
                     if (a_real) {
-                        const int8_t *p = &s_a[wave][fr * npw * kPairK + (pair - p_begin) * kPairK +
-                                                     h * 128 + fg * 32];
-                        v0 = *reinterpret_cast<const i32x4 *>(p);
-                        v1 = *reinterpret_cast<const i32x4 *>(p + 16);
+                        const int c0 = ((pair - p_begin) * kPairK + h * 128 + fg * 32) >> 4;
+                        const int8_t *row = &s_a[fr * npw * kPairK];
+                        v0 = *reinterpret_cast<const i32x4 *>(row + ((c0 ^ (fr & 7)) << 4));
+                        v1 = *reinterpret_cast<const i32x4 *>(row + (((c0 + 1) ^ (fr & 7)) << 4));
                     } else {
                         v0 = a_ones ? ones : zero;
                         v1 = v0;
@@ -290,11 +320,10 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 if constexpr (kDirect) {
                     decode_w16(wr[2 * pp + h], q0, q1);
                 } else {
-                    const int jj = 2 * pp + (fr >> 3);
                     const int rr = fr & 7;
                     const int c = 4 * h + fg;
                     decode_w16(*reinterpret_cast<const u32x4 *>(
-                                   &s_w[wave][jj][rr * 128 + ((c ^ rr) << 4)]),
+                                   &s_w[wave][(fr >> 3) * 1024 + rr * 128 + ((c ^ rr) << 4)]),
                                q0, q1);
                 }
                 acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, q0, acc0, 0, 0, 0);
@@ -303,18 +332,21 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         }
     }
 
-    // lane holds rows 4 * fg + r, column fr of this wave's 16x16 partial
+    // lane holds rows 4 * fg + r, column fr of this wave's 16x16 partial; it goes to the wave's
+    // own weight buffer (its last reads of it precede these writes in program order)
+    int32_t(*s_part)[16][16] = reinterpret_cast<int32_t(*)[16][16]>(&s_w[0][0]);
+    constexpr int kPartStride = 2 * 1024 / (16 * 16 * 4);  // partial tiles per wave buffer
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        s_part[wave][4 * fg + r][fr] = acc0[r] + acc1[r];
+        s_part[wave * kPartStride][4 * fg + r][fr] = acc0[r] + acc1[r];
     }
     __syncthreads();
     if (out_ok) {
         uint32_t tot = 0, rs = 0;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            tot += static_cast<uint32_t>(s_part[w][orow][ocol]);
-            rs += static_cast<uint32_t>(s_part[w][rows][ocol]);
+            tot += static_cast<uint32_t>(s_part[w * kPartStride][orow][ocol]);
+            rs += static_cast<uint32_t>(s_part[w * kPartStride][rows][ocol]);
         }
         const int gm = m0 + orow, gn = n0 + ocol;
         store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn,
@@ -356,6 +388,16 @@ __global__ __launch_bounds__(256) void w4a8_generic_kernel(W4A8Args a)
                    epilogue_f32(static_cast<int32_t>(acc), static_cast<int32_t>(rsum), a.zp_a[gm],
                                 a.scale_a[gm], a.scale_b[gn], a.C ? &c : nullptr,
                                 a.bias ? &b : nullptr, a.cmin, a.cmax));
+}
+
+template <int kActLoads, int OUT>
+void launch_w4a8(dim3 grid, dim3 block, size_t lds, hipStream_t s, const W4A8Args &a, bool packed)
+{
+    if (packed) {
+        hipLaunchKernelGGL((w4a8_mfma_kernel<kActLoads, PK_AB, OUT>), grid, block, lds, s, a);
+    } else {
+        hipLaunchKernelGGL((w4a8_mfma_kernel<kActLoads, PK_NONE, OUT>), grid, block, lds, s, a);
+    }
 }
 
 // Shared body of the W4A8 runs. `packed`: A and B are in the packed layout (A rows of k bytes,
@@ -419,22 +461,22 @@ void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_
         const size_t npairs = k / kPairK;
         const size_t ppw = (npairs + kWaves - 1) / kWaves;
         const dim3 grid(gx, static_cast<unsigned>(gy));
-        if (rows_max * ppw * 16 <= 64) {  // each wave's activation slice: one chunk per lane
-            if (packed) {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_AB, OUT>), grid, dim3(kWaves * 64), 0,
-                                   s, a);
-            } else {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<true, PK_NONE, OUT>), grid, dim3(kWaves * 64),
-                                   0, s, a);
-            }
+        // activation staging: each wave's slice is rows_max x ppw * 256 bytes, 16 bytes per
+        // lane per load; up to kMaxActLoads loads per lane, else loaded per step
+        const size_t act_loads = (rows_max * ppw * 16 + 63) / 64;
+        const size_t lds = static_cast<size_t>(kWaves) *
+                           act_slice_bytes(static_cast<int>(rows_max), static_cast<int>(ppw));
+        const dim3 block(kWaves * 64);
+        if (act_loads <= 1) {
+            launch_w4a8<1, OUT>(grid, block, lds, s, a, packed);
+        } else if (act_loads <= 2) {
+            launch_w4a8<2, OUT>(grid, block, lds, s, a, packed);
+        } else if (act_loads <= 4) {
+            launch_w4a8<4, OUT>(grid, block, lds, s, a, packed);
+        } else if (act_loads <= static_cast<size_t>(kMaxActLoads)) {
+            launch_w4a8<kMaxActLoads, OUT>(grid, block, lds, s, a, packed);
         } else {
-            if (packed) {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_AB, OUT>), grid, dim3(kWaves * 64),
-                                   0, s, a);
-            } else {
-                hipLaunchKernelGGL((w4a8_mfma_kernel<false, PK_NONE, OUT>), grid, dim3(kWaves * 64),
-                                   0, s, a);
-            }
+            launch_w4a8<0, OUT>(grid, block, 0, s, a, packed);
         }
     } else {
         const long long total = static_cast<long long>(m) * static_cast<long long>(n);
