@@ -10,9 +10,10 @@
 // and their packed siblings.
 //
 // Three kernels, chosen per call:
-//   * int8_stream_kernel (plain A, B = [n, k], k % 128 == 0: W8A8 at its config): a 4-deep
-//     ring of LDS stages filled by direct global->LDS loads, v_mfma_i32_32x32x32_i8, XCD-aware
-//     tile order (described at the kernel);
+//   * int8_stream_kernel (plain A, B = [n, k], k % 128 == 0: W8A8 at its config; igemmcl when
+//     the group channel count is a multiple of 128): 8 wave64s, a 4-deep ring of LDS stages
+//     filled by direct global->LDS loads, v_mfma_i32_32x32x32_i8, XCD-aware tile order
+//     (described at the kernel);
 //   * int8_mfma_kernel (igemmcl, the other 16-byte-aligned shapes, clamp_i32's [k, n] B): 256 threads
 //     (4 wave64s in a 2x2 grid) on a BM x 128 tile, k in steps of 64 bytes through double-buffered
 //     LDS tiles, v_mfma_i32_16x16x64_i8;
@@ -722,8 +723,9 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
 // stage is then 128 channels of one tap, each A row the 128 contiguous input bytes of its output
 // pixel's tap, read through a buffer resource whose range check returns zeros for padding taps.
 //
-// A workgroup of 4 wave64s (2 x 2) owns a BM x 128 output tile (BM = 64 or 128) and walks k in
-// stages of 128 bytes through a 4-deep ring of LDS stages filled by direct global->LDS loads
+// A workgroup of 8 wave64s (2 x 4, each BM/2 x 32) owns a BM x 128 output tile (BM = 64 or
+// 128) and walks k in stages of 128 bytes through a 4-deep ring of LDS stages filled by direct
+// global->LDS loads, every wave issuing an equal share of each stage's loads
 // (global_load_lds_dwordx4: lane i of an instruction writes 16 bytes at LDS base + 16 * i, so
 // no VGPRs carry the tiles). Each LDS row holds 128 k-bytes of one A row or one B row; its eight
 // 16-byte chunks are stored XOR-swizzled with (row >> 1) & 7, which makes both the loads (8 rows
@@ -780,21 +782,39 @@ __device__ __forceinline__ void dma_lds16_buf(i32x4 rsrc, int voffset, int8_t *l
 }
 #pragma clang diagnostic pop
 
+// Streaming kernel layout: kStreamWaves waves per workgroup each issue an equal share of every
+// stage's 1 KiB load blocks and compute a BM/2 x 32 sub-tile (2 x 4 waves). Measured on MI355X
+// (lab kernels, all 256 CUs busy): a CU sustains about 41 B/clk of L2 -> LDS traffic with eight
+// waves issuing a few LDS-DMA loads each, against 24 B/clk with four waves issuing many, and
+// ds_read_b128 reaches about 180 B/clk with eight waves reading against 105 B/clk with four; with
+// two compute waves per SIMD one wave's LDS reads overlap the other's MFMAs.
+constexpr int kStreamWaves = 8;
+constexpr int kStreamWavesN = 4;  // waves along N (each 32 columns of the 128)
+constexpr int kStreamThreads = kStreamWaves * 64;
+
+// LDS ring depth of the streaming kernel (stages of 128 bytes of k for BM + 128 rows). Four
+// stages: a 5- or 6-stage ring (which 64-row tiles would fit) measured no faster at the W8A8
+// configuration (cold operands 17.6-18.0 us with four, 18.2 with six).
+constexpr int kStreamStages = 4;
+
 template <int BM, int EPI, int PK, bool kConv = false>
-__global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int tiles_m, int tiles,
-                                                               int per_xcd)
+__global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a, int tiles_m,
+                                                                     int tiles, int per_xcd)
 {
-    constexpr int WM = BM / 2;             // rows per wave
+    constexpr int WM = BM / (kStreamWaves / kStreamWavesN);  // rows per wave
+    constexpr int WN = kBN / kStreamWavesN;                   // columns per wave
     constexpr int MF = WM / 32;            // 32-row fragments per wave
-    constexpr int NF = 2;                  // 32-column fragments per wave (64 columns)
-    constexpr int A_DMA = BM / 32;         // 1 KB (8-row) load instructions per wave per stage
-    constexpr int B_DMA = kBN / 32;
+    constexpr int NF = WN / 32;            // 32-column fragments per wave
+    constexpr int A_DMA = BM / (8 * kStreamWaves);   // 1 KB (8-row) loads per wave per stage
+    constexpr int B_DMA = kBN / (8 * kStreamWaves);
+    static_assert(A_DMA >= 1 && B_DMA >= 1, "every wave loads A and B blocks");
     constexpr int PER_STAGE = A_DMA + B_DMA;
     constexpr int SA = BM * kSK;
     constexpr int SB = kBN * kSK;
 
-    __shared__ __attribute__((aligned(16))) int8_t sa0[SA], sa1[SA], sa2[SA], sa3[SA];
-    __shared__ __attribute__((aligned(16))) int8_t sb0[SB], sb1[SB], sb2[SB], sb3[SB];
+    // ring of NS stages (A rows then B rows each); NS - 1 stages are in flight while one is read
+    constexpr int NS = kStreamStages;
+    __shared__ __attribute__((aligned(16))) int8_t ring[NS][SA + SB];
     __shared__ int32_t s_mult[kBN];
     __shared__ int32_t s_shift[kBN];
 
@@ -809,8 +829,8 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
+    const int wm = wave / kStreamWavesN;
+    const int wn = wave % kStreamWavesN;
 
     // Epilogue inputs are loaded now and used after the main loop, so their latency hides under
     // it: the multipliers' scale_b (finished into s_mult / s_shift after the loop: computing
@@ -818,7 +838,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     constexpr bool kRow = EPI == EPI_REQUANT_ROW;
     [[maybe_unused]] float pre_sb = 0.f;
     [[maybe_unused]] int32_t pre_rbias = 0;  // per-row bias (EPI_REQUANT_ROW)
-    [[maybe_unused]] uint32_t pre_cbias[2] = {0u, 0u};
+    [[maybe_unused]] uint32_t pre_cbias[NF] = {};
     [[maybe_unused]] const bool mult_lane = kRow ? (tid < BM && m0 + tid < a.M)
                                                  : (tid < kBN && n0 + tid < a.N);
     if constexpr (EPI == EPI_REQUANT_I8 || kRow) {
@@ -833,8 +853,8 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     if constexpr (!is_dyn(EPI) && !kRow) {
         if (a.bias) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int gn = n0 + wn * 64 + 32 * j + (lane & 31);
+            for (int j = 0; j < NF; ++j) {
+                const int gn = n0 + wn * WN + 32 * j + (lane & 31);
                 pre_cbias[j] = gn < a.N ? static_cast<uint32_t>(a.bias[gn]) : 0u;
             }
         }
@@ -985,10 +1005,8 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
     };
     constexpr int KS = kSK / 32;  // MFMA k-steps per stage
     auto compute = [&](const int8_t *sa, const int8_t *sb) {
-        // All operand reads of the stage first, so their LDS latency overlaps.
         i32x4 fa[KS][MF], fb[KS][NF];
-#pragma unroll
-        for (int step = 0; step < KS; ++step) {
+        auto read_step = [&](int step) {
             const int c = 2 * step + h;
 #pragma unroll
             for (int i = 0; i < MF; ++i) {
@@ -997,9 +1015,13 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
             }
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
-                const int row = wn * 64 + 32 * j + r32;
+                const int row = wn * WN + 32 * j + r32;
                 fb[step][j] = *reinterpret_cast<const i32x4 *>(sb + lds_pos(kBP, row, c));
             }
+        };
+#pragma unroll
+        for (int step = 0; step < KS; ++step) {
+            read_step(step);
         }
 #pragma unroll
         for (int step = 0; step < KS; ++step) {
@@ -1024,21 +1046,32 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
                 }
             }
         }
-        // Keep that order through instruction scheduling: DS reads, then MFMAs.
-        __builtin_amdgcn_sched_group_barrier(0x100, KS * (MF + NF), 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, KS * MF * NF, 0);
+        // Instruction order: the operands of k-step 0 first, then the operands of each next
+        // k-step between the MFMAs of the current one, so LDS latency hides under the MFMAs.
+        __builtin_amdgcn_sched_group_barrier(0x100, MF + NF, 0);
+#pragma unroll
+        for (int step = 1; step < KS; ++step) {
+            __builtin_amdgcn_sched_group_barrier(0x100, MF + NF, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, MF * NF, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, MF * NF, 0);
     };
 
     const int nst = a.K / kSK;
     // One pipeline step: wait until this wave's loads of stage st landed (the stages issued after
     // it may stay in flight), meet the other waves, refill the buffer everyone finished reading
-    // in the previous step with stage st + 3, then compute stage st.
-    auto step = [&](int st, const int8_t *ca, const int8_t *cb, int8_t *na, int8_t *nb) {
+    // in the previous step with stage st + NS - 1, then compute stage st.
+    auto step = [&](int st, const int8_t *cur, int8_t *nxt) {
         if (st >= nst) {
             return;
         }
-        const int ahead = min(2, nst - 1 - st);
-        if (ahead == 2) {
+        const int ahead = min(NS - 2, nst - 1 - st);
+        static_assert(NS >= 3 && NS <= 6, "ring depth");
+        if (ahead >= 4) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(4 * PER_STAGE));
+        } else if (ahead == 3) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(3 * PER_STAGE));
+        } else if (ahead == 2) {
             __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * PER_STAGE));
         } else if (ahead == 1) {
             __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PER_STAGE));
@@ -1048,26 +1081,23 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (st + 3 < nst) {
-            issue(st + 3, na, nb);
+        if (st + NS - 1 < nst) {
+            issue(st + NS - 1, nxt, nxt + SA);
         }
-        compute(ca, cb);
+        compute(cur, cur + SA);
     };
 
-    if (nst > 0) {
-        issue(0, sa0, sb0);
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i) {
+        if (nst > i) {
+            issue(i, ring[i], ring[i] + SA);
+        }
     }
-    if (nst > 1) {
-        issue(1, sa1, sb1);
-    }
-    if (nst > 2) {
-        issue(2, sa2, sb2);
-    }
-    for (int st = 0; st < nst; st += 4) {
-        step(st, sa0, sb0, sa3, sb3);
-        step(st + 1, sa1, sb1, sa0, sb0);
-        step(st + 2, sa2, sb2, sa1, sb1);
-        step(st + 3, sa3, sb3, sa2, sb2);
+    for (int st = 0; st < nst; st += NS) {
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            step(st + i, ring[i], ring[(i + NS - 1) % NS]);
+        }
     }
     // Every load of this wave has landed (the last step waits for vmcnt(0)); saying so here lets
     // the compiler's own wait tracking drop the vmcnt(0) it would otherwise place before each
@@ -1108,7 +1138,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         }
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
-            const int gn = n0 + wn * 64 + 32 * j + r32;
+            const int gn = n0 + wn * WN + 32 * j + r32;
             sbc[j] = gn < a.N ? a.scale_b[gn] : 0.0f;
             fbc[j] = gn < a.N ? dyn_bias<EPI>(a, gn) : 0.0f;
         }
@@ -1116,7 +1146,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         if (in_range) {
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
-                const int gn = n0 + wn * 64 + 32 * j + r32;
+                const int gn = n0 + wn * WN + 32 * j + r32;
 #pragma unroll
                 for (int i = 0; i < MF; ++i) {
 #pragma unroll
@@ -1135,7 +1165,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
             // a zero point beyond 16 bits: this lane's outputs summed term by term
             for (int e = 0; e < NF * MF * 16; ++e) {
                 const int j = e / (MF * 16), i = (e / 16) % MF, r = e % 16;
-                const int gn = n0 + wn * 64 + 32 * j + r32;
+                const int gn = n0 + wn * WN + 32 * j + r32;
                 const int gm = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (gm < a.M && gn < a.N) {
                     dyn_finish<EPI>(a, gm, gn, a.d_row0 + gm,
@@ -1155,7 +1185,7 @@ __global__ __launch_bounds__(kThreads) void int8_stream_kernel(Int8Args a, int t
         constexpr bool kChecked = decltype(checked)::value;
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
-            const int lc = wn * 64 + 32 * j + r32;
+            const int lc = wn * WN + 32 * j + r32;
             const int gn = n0 + lc;
             if (gn >= a.N) {
                 continue;
@@ -1353,13 +1383,13 @@ void launch_stream(const Int8Args &a, hipStream_t stream)
     const long long per_xcd = (tiles + 7) / 8;
     TQT_REQUIRE(tiles < (1ll << 30), "grid too large");
     if (big) {
-        hipLaunchKernelGGL((int8_stream_kernel<128, EPI, PK, kConv>), dim3(8 * per_xcd), dim3(kThreads), 0,
-                           stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
-                           static_cast<int>(per_xcd));
+        hipLaunchKernelGGL((int8_stream_kernel<128, EPI, PK, kConv>), dim3(8 * per_xcd),
+                           dim3(kStreamThreads), 0, stream, a, static_cast<int>(tiles_m),
+                           static_cast<int>(tiles), static_cast<int>(per_xcd));
     } else {
-        hipLaunchKernelGGL((int8_stream_kernel<64, EPI, PK, kConv>), dim3(8 * per_xcd), dim3(kThreads), 0,
-                           stream, a, static_cast<int>(tiles_m), static_cast<int>(tiles),
-                           static_cast<int>(per_xcd));
+        hipLaunchKernelGGL((int8_stream_kernel<64, EPI, PK, kConv>), dim3(8 * per_xcd),
+                           dim3(kStreamThreads), 0, stream, a, static_cast<int>(tiles_m),
+                           static_cast<int>(tiles), static_cast<int>(per_xcd));
     }
 }
 
