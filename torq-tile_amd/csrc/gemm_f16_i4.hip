@@ -270,12 +270,14 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Strip kernel (bl == 32, k in {2048, 3072, 4096}, any n): one workgroup of 8 wave64s per CU owns
-// up to four consecutive 16-channel tiles for one group of 32 activation rows. It loads its A
+// Strip kernel (bl == 32, k in {2048, 3072, 4096}, any n): one workgroup of NW wave64s per CU
+// owns up to four consecutive 16-channel tiles for one group of 32 activation rows. It loads its A
 // slice once (into registers, wave w owning k-blocks [w * BPW, (w + 1) * BPW)) and streams the
 // tiles' weights and scales from global memory straight into registers, 16 bytes per lane (one
-// 32-k block of one channel), two tiles in flight; a 4x4 lane-group transpose gives each lane its
-// 8-k slice of four consecutive blocks. Per tile the math is the one of w4a16_mfma_kernel above;
+// 32-k block of one channel); a 4x4 lane-group transpose gives each lane its 8-k slice of four
+// consecutive blocks. NW = 16 (k 2048 or 4096): a 256-k slice per wave, 64 VGPRs of A, four
+// waves per SIMD, one tile's loads in flight; NW = 8 (k 3072): two waves per SIMD, two tiles in
+// flight (measured at k 4096: 20.7 us with 16 waves, 22.4 with 8). Per tile the math is the one of w4a16_mfma_kernel above;
 // the eight waves' f32 partials meet in LDS. The weights do not pass through LDS: on gfx950 a
 // direct-to-LDS stream and the compute's LDS reads do not overlap. The register sets rotate by
 // unrolling, since a register copy would wait for the load still filling it.
@@ -300,13 +302,13 @@ __device__ __forceinline__ f16x8 unpack_q8_sgpr(uint32_t x, uint32_t magic)
     return out;
 }
 
-template <int K, int PK, int OUT>
-__global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
+template <int K, int PK, int OUT, int NW>
+__global__ __launch_bounds__(NW * 64) void w4a16_regs_kernel(W4A16Args a, int nwg)
 {
-    constexpr int BPW = K / 256;  // 32-k blocks per wave (8, 12 or 16)
-    constexpr int NG = BPW / 4;   // 4-block groups per wave
-    static_assert(K % 1024 == 0 && K <= kStripMaxK, "strip kernel k");
-    __shared__ float s_part[kWaves * kMRows * kNTile];
+    constexpr int BPW = K / (32 * NW);  // 32-k blocks per wave
+    constexpr int NG = BPW / 4;         // 4-block groups per wave
+    static_assert(BPW % 4 == 0 && BPW >= 4 && K <= kStripMaxK, "strip kernel k");
+    __shared__ float s_part[NW * kMRows * kNTile];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -353,9 +355,14 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
             r.s[q] = *reinterpret_cast<const uint64_t *>(srow + b0);
         }
     };
+    // register sets in rotation: three (two tiles' loads in flight while one is computed) at
+    // 8 waves; two at 16 waves, where four waves per SIMD hide the latency instead
+    constexpr int kAhead = NW >= 16 ? 1 : 2;
     TileRegs r0, r1, r2;
     load(0, r0);
-    load(1, r1);
+    if constexpr (kAhead == 2) {
+        load(1, r1);
+    }
 
     // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
     f16x8 fa[BPW][2];
@@ -370,7 +377,7 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
     asm volatile("s_mov_b32 %0, 0x64006400" : "=s"(magic));
 
     auto tile = [&](int tl, const TileRegs &cur, TileRegs &nxt) {
-        load(tl + 2, nxt);
+        load(tl + kAhead, nxt);
         f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int q = 0; q < NG; ++q) {
@@ -378,25 +385,31 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
             if constexpr ((PK & PK_B) == 0) {
                 transpose_lane_groups(p);  // packed weights are stored transposed already
             }
-            f32x4 part[4][2];
+            // 8 waves: all four blocks' MFMAs first, then their scale FMAs (latency hidden in
+            // the wave); 16 waves: block by block (fewer registers; other waves hide it)
+            constexpr int JB = NW >= 16 ? 1 : 4;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f16x8 wq = unpack_q8_sgpr(p[j], magic);
+            for (int j0 = 0; j0 < 4; j0 += JB) {
+                f32x4 part[JB][2];
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
-                    part[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        fa[4 * q + j][mt], wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                for (int jj = 0; jj < JB; ++jj) {
+                    const f16x8 wq = unpack_q8_sgpr(p[j0 + jj], magic);
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) {
+                        part[jj][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            fa[4 * q + j0 + jj][mt], wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    }
                 }
-            }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint16_t sbits = static_cast<uint16_t>(cur.s[q] >> (16 * j));
-                const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sbits));
+                for (int jj = 0; jj < JB; ++jj) {
+                    const uint16_t sbits = static_cast<uint16_t>(cur.s[q] >> (16 * (j0 + jj)));
+                    const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sbits));
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
+                    for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        acc[mt][r] = __builtin_fmaf(part[j][mt][r], sf, acc[mt][r]);
+                        for (int r = 0; r < 4; ++r) {
+                            acc[mt][r] = __builtin_fmaf(part[jj][mt][r], sf, acc[mt][r]);
+                        }
                     }
                 }
             }
@@ -413,10 +426,10 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
         const int ocol = tid & 15;
         const int gm = mg0 + orow;
         const int gn = (t_begin + tl) * kNTile + ocol;
-        if (gm < a.M && gn < a.N) {
+        if (orow < kMRows && gm < a.M && gn < a.N) {
             float v = 0.f;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
+            for (int w = 0; w < NW; ++w) {
                 v += s_part[(w * kMRows + orow) * kNTile + ocol];
             }
             if (a.C) {
@@ -431,15 +444,28 @@ __global__ __launch_bounds__(512) void w4a16_regs_kernel(W4A16Args a, int nwg)
         }
         __syncthreads();  // s_part is rewritten by the next tile
     };
-    tile(0, r0, r2);
-    if (ntl > 1) {
-        tile(1, r1, r0);
-    }
-    if (ntl > 2) {
-        tile(2, r2, r1);
-    }
-    if (ntl > 3) {
-        tile(3, r0, r2);
+    if constexpr (kAhead == 2) {
+        tile(0, r0, r2);
+        if (ntl > 1) {
+            tile(1, r1, r0);
+        }
+        if (ntl > 2) {
+            tile(2, r2, r1);
+        }
+        if (ntl > 3) {
+            tile(3, r0, r2);
+        }
+    } else {
+        tile(0, r0, r1);
+        if (ntl > 1) {
+            tile(1, r1, r0);
+        }
+        if (ntl > 2) {
+            tile(2, r0, r1);
+        }
+        if (ntl > 3) {
+            tile(3, r1, r0);
+        }
     }
 }
 
@@ -556,21 +582,22 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
         TQT_REQUIRE(gy < 65536 && nwg < (1ll << 31), "grid too large");
         const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(gy));
         const int nw = static_cast<int>(nwg);
+        // 16 waves (a 256-k slice each) where the k-slices allow, else 8
         if (packed) {
             if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_AB, OUT>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_AB, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
             } else if (k == 3072) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_AB, OUT>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_AB, OUT, 8>), grid, dim3(512), 0, s, a, nw);
             } else {
-                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_AB, OUT>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_AB, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
             }
         } else {
             if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_NONE, OUT>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_NONE, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
             } else if (k == 3072) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_NONE, OUT>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_NONE, OUT, 8>), grid, dim3(512), 0, s, a, nw);
             } else {
-                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_NONE, OUT>), grid, dim3(512), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_NONE, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
             }
         }
     } else if (fast) {
