@@ -19,6 +19,8 @@
 //     bias are f32 too).
 // A generic one-thread-per-output kernel covers every other shape with the reference test
 // oracle's exact operation order (reference test/common/reference_gemm.cpp:132-179).
+#include <type_traits>
+
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f16_f16p_qsi4c2p_mfma_gfx950.h"
@@ -34,6 +36,13 @@ constexpr int kMRows = 32;            // activation rows per workgroup (two 16-r
 constexpr int kNTile = 16;
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// s_waitcnt immediate waiting for vmcnt <= vm only (gfx9: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] << 14; expcnt and lgkmcnt at their maximum: no wait).
+__host__ __device__ constexpr int waitcnt_vm0(int vm)
+{
+    return (vm & 15) | (7 << 4) | (15 << 8) | ((vm >> 4) << 14);
+}
 
 struct W4A16Args
 {
@@ -126,6 +135,73 @@ __device__ __forceinline__ f16x8 permute_a(u32x4 v)
     o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
     o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
     return __builtin_bit_cast(f16x8, o);
+}
+
+// A slice of a strip kernel's wave: 2 * BPW 16-byte loads per lane covering 32 rows x BPW 32-k
+// blocks. Plain A is loaded in whole cache lines -- load j = 2 * jp + rh of row tile mt gives lane
+// L row mt * 16 + rh * 8 + L / 8, 16-byte chunk L % 8 of block pair jp -- because 16 rows x 64 B
+// per instruction (the MFMA layout) runs at well under half the rate when every row is a separate
+// line. Packed A is loaded straight in the MFMA layout (lane (r, g): row mt * 16 + r, chunk g of
+// block j), which its chunk-major panels already make whole lines. Rows past m read row m - 1.
+template <int BPW, int PK>
+__device__ __forceinline__ const uint8_t *a_slice_addr(const W4A16Args &a, int mg0, int wave,
+                                                       int lane, int j, int mt)
+{
+    int row, k;
+    if constexpr ((PK & PK_A) != 0) {
+        row = mg0 + mt * 16 + (lane & 15);
+        k = (wave * BPW + j) * 32 + (lane >> 4) * 8;
+    } else {
+        row = mg0 + mt * 16 + (j & 1) * 8 + (lane >> 3);
+        k = (wave * BPW + (j & ~1)) * 32 + (lane & 7) * 8;
+    }
+    int mul;
+    const uint8_t *arow = a_row_ptr<PK>(a, min(row, a.M - 1), mul);
+    return arow + 2ll * k * mul;
+}
+
+// The slice as a_slice_addr loaded it -> MFMA A fragments (k in permute_a's slot order). Plain A
+// passes through `stage`, 2 KiB of LDS private to the wave: per (jp, mt) 16 rows x 128 B written
+// as loaded (chunk c of row r at 16-byte slot c ^ (r & 7): conflict-free both ways) and read back
+// as block 2 jp + jj, lane (r, g) taking chunk 4 jj + g of row r. Blocks [J0, J1) only (even
+// bounds).
+template <int BPW, int PK, int J0 = 0, int J1 = BPW>
+__device__ __forceinline__ void a_slice_to_mfma(const u32x4 (&ra)[BPW][2], f16x8 (&fa)[BPW][2],
+                                                int8_t *stage, int lane)
+{
+    static_assert(J0 % 2 == 0 && J1 % 2 == 0 && 0 <= J0 && J0 < J1 && J1 <= BPW, "block range");
+    if constexpr ((PK & PK_A) != 0) {
+#pragma unroll
+        for (int j = J0; j < J1; ++j) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                fa[j][mt] = permute_a(ra[j][mt]);
+            }
+        }
+    } else {
+        const int wr = lane >> 3;
+        const int wc = lane & 7;
+        const int fr = lane & 15;
+        const int fg = lane >> 4;
+#pragma unroll
+        for (int jp = J0 / 2; jp < J1 / 2; ++jp) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                for (int rh = 0; rh < 2; ++rh) {
+                    const int r = rh * 8 + wr;
+                    *reinterpret_cast<u32x4 *>(stage + r * 128 + ((wc ^ (r & 7)) << 4)) =
+                        ra[2 * jp + rh][mt];
+                }
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(
+                        stage + fr * 128 + (((4 * jj + fg) ^ (fr & 7)) << 4));
+                    fa[2 * jp + jj][mt] = permute_a(v);
+                }
+            }
+        }
+    }
 }
 
 template <int PK, int OUT>
@@ -270,17 +346,16 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Strip kernel (bl == 32, k in {2048, 3072, 4096}, any n): one workgroup of NW wave64s per CU
-// owns up to four consecutive 16-channel tiles for one group of 32 activation rows. It loads its A
-// slice once (into registers, wave w owning k-blocks [w * BPW, (w + 1) * BPW)) and streams the
-// tiles' weights and scales from global memory straight into registers, 16 bytes per lane (one
-// 32-k block of one channel); a 4x4 lane-group transpose gives each lane its 8-k slice of four
-// consecutive blocks. NW = 16 (k 2048 or 4096): a 256-k slice per wave, 64 VGPRs of A, four
-// waves per SIMD, one tile's loads in flight; NW = 8 (k 3072): two waves per SIMD, two tiles in
-// flight (measured at k 4096: 20.7 us with 16 waves, 22.4 with 8). Per tile the math is the one of w4a16_mfma_kernel above;
-// the eight waves' f32 partials meet in LDS. The weights do not pass through LDS: on gfx950 a
-// direct-to-LDS stream and the compute's LDS reads do not overlap. The register sets rotate by
-// unrolling, since a register copy would wait for the load still filling it.
+// Strip kernel (bl == 32, k 3072 here; any n): one workgroup of NW wave64s per CU owns up to four
+// consecutive 16-channel tiles for one group of 32 activation rows. It loads its A slice once
+// (into registers, wave w owning k-blocks [w * BPW, (w + 1) * BPW)) and streams the tiles'
+// weights and scales from global memory straight into registers, 16 bytes per lane (one 32-k
+// block of one channel); a 4x4 lane-group transpose gives each lane its 8-k slice of four
+// consecutive blocks. NW = 8 at k 3072: two waves per SIMD, two tiles in flight (k 2048 and 4096
+// take the LDS-staged kernel below: 19.3 us at the bench's k 4096 against 20.7 for this kernel
+// with 16 waves, 22.4 with 8). Per tile the math is the one of w4a16_mfma_kernel above; the
+// waves' f32 partials meet in LDS. The register sets rotate by unrolling, since a register copy
+// would wait for the load still filling it.
 // ---------------------------------------------------------------------------------------------
 constexpr int kStripTiles = 4;
 constexpr int kStripMaxK = 4096;
@@ -327,11 +402,8 @@ __global__ __launch_bounds__(NW * 64) void w4a16_regs_kernel(W4A16Args a, int nw
     for (int j = 0; j < BPW; ++j) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            const int row = min(mg0 + mt * 16 + fr, a.M - 1);
-            const int k = (wave * BPW + j) * 32 + fg * 8;
-            int mul;
-            const uint8_t *arow = a_row_ptr<PK>(a, row, mul);
-            ra[j][mt] = *reinterpret_cast<const u32x4 *>(arow + 2ll * k * mul);
+            ra[j][mt] = *reinterpret_cast<const u32x4 *>(
+                a_slice_addr<BPW, PK>(a, mg0, wave, lane, j, mt));
         }
     }
 
@@ -365,14 +437,10 @@ __global__ __launch_bounds__(NW * 64) void w4a16_regs_kernel(W4A16Args a, int nw
     }
 
     // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
+    // The wave's own partials area of s_part stages its A (no other wave touches it).
     f16x8 fa[BPW][2];
-#pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            fa[j][mt] = permute_a(ra[j][mt]);
-        }
-    }
+    a_slice_to_mfma<BPW, PK>(ra, fa, reinterpret_cast<int8_t *>(&s_part[wave * kMRows * kNTile]),
+                             lane);
     uint32_t magic;
     asm volatile("s_mov_b32 %0, 0x64006400" : "=s"(magic));
 
@@ -467,6 +535,361 @@ __global__ __launch_bounds__(NW * 64) void w4a16_regs_kernel(W4A16Args a, int nw
             tile(3, r1, r0);
         }
     }
+}
+
+// One C / bias element loaded by asm (no compiler-placed wait; the caller waits with s_waitcnt and
+// ties the register with an empty asm): 32 bits for f32 outputs, the 16-bit pattern otherwise.
+template <int OUT>
+__device__ __forceinline__ uint32_t load_out_bits_async(const void *p, long long i)
+{
+    uint32_t v;
+    if constexpr (OUT == OUT_F32) {
+        asm volatile("global_load_dword %0, %1, off"
+                     : "=v"(v)
+                     : "v"(static_cast<const float *>(p) + i)
+                     : "memory");
+    } else {
+        asm volatile("global_load_ushort %0, %1, off"
+                     : "=v"(v)
+                     : "v"(static_cast<const uint16_t *>(p) + i)
+                     : "memory");
+    }
+    return v;
+}
+
+template <int OUT>
+__device__ __forceinline__ float out_bits_to_f32(uint32_t v)
+{
+    if constexpr (OUT == OUT_F32) {
+        return __builtin_bit_cast(float, v);
+    } else if constexpr (OUT == OUT_F16) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v)));
+    } else {
+        return bf16_bits_to_f32(static_cast<uint16_t>(v));
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// LDS-staged strip kernel (bl == 32, k 2048 or 4096): the strip kernel's math with the weight
+// stream moved off the registers. One workgroup of 16 wave64s per CU owns up to four consecutive
+// 16-channel tiles for one group of 32 activation rows; wave w keeps its k-slice of A (BPW 32-k
+// blocks) in registers and streams that same k-slice of every tile -- 16 channels x BPW blocks of
+// weights, 16 x BPW f16 scales -- into a three-slot LDS ring of its own with direct global -> LDS
+// loads, three tiles ahead. No wave reads another wave's ring, so a wave starts a tile as soon as
+// its own loads of it have landed and refills the slot as soon as it has read it.
+// What bounds it: every CU takes in all of A (256 KiB at k 4096) besides its tiles, at some
+// 90 B/ns, and the CU serves its waves' requests about in issue order. So the first half of every
+// wave's A slice is requested first (all waves, then a meeting), then tile 0, then the second
+// halves: tile 0's first four blocks are computed while the second halves stream in.
+// Plain weights: one load instruction takes 8 channels x 128 B (whole lines), lane i fetching
+// block (i & 7) ^ (c & 7) of channel c = i / 8, so block b of channel c lies at 16-byte slot
+// b ^ (c & 7) of the channel's 128 bytes and a wave's ds_read_b128 of one block for 16 channels
+// hits distinct slots; a whole packed panel's k-slice is contiguous (2 KiB) and is copied as it
+// lies. Per tile: the strip kernel's decode, v_mfma_f32_16x16x32_f16 per block and scale FMA;
+// then the 16 partials (ds_write_b128) meet in LDS and every thread sums 8 of one output's 16,
+// paired with its neighbour lane.
+// ---------------------------------------------------------------------------------------------
+
+// unpack_q8_sgpr with one shift instead of three: nibbles 1, 3 (5, 7) are inserted at bits 4-7
+// (20-23), giving 1024 + 16 q, and scaled back by an exact fma (h / 16 - 72 = q - 8).
+__device__ __forceinline__ f16x8 unpack_q8_lds(uint32_t x, uint32_t magic)
+{
+    const f16x2 bias = f16x2{static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+    const f16x2 sixteenth = f16x2{static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    const f16x2 bias16 = f16x2{static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+    const uint32_t y = x >> 8;
+    const f16x2 h0 = __builtin_bit_cast(f16x2, (x & 0x000f000fu) | (magic & ~0x000f000fu)) + bias;
+    const f16x2 h1 = __builtin_elementwise_fma(
+        __builtin_bit_cast(f16x2, (x & 0x00f000f0u) | (magic & ~0x00f000f0u)), sixteenth, bias16);
+    const f16x2 h2 = __builtin_bit_cast(f16x2, (y & 0x000f000fu) | (magic & ~0x000f000fu)) + bias;
+    const f16x2 h3 = __builtin_elementwise_fma(
+        __builtin_bit_cast(f16x2, (y & 0x00f000f0u) | (magic & ~0x00f000f0u)), sixteenth, bias16);
+    return f16x8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+}
+
+// s_waitcnt until at most n (wave-uniform, 0 .. 23) of the wave's vector memory operations are
+// pending (vmcnt counts loads, LDS-DMA loads and stores in issue order).
+__device__ __forceinline__ void wait_vm_upto(int n)
+{
+    switch (n) {
+#define TQT_VM_CASE(v)                                                                             \
+    case v: __builtin_amdgcn_s_waitcnt(waitcnt_vm0(v)); break;
+        TQT_VM_CASE(0) TQT_VM_CASE(1) TQT_VM_CASE(2) TQT_VM_CASE(3) TQT_VM_CASE(4) TQT_VM_CASE(5)
+        TQT_VM_CASE(6) TQT_VM_CASE(7) TQT_VM_CASE(8) TQT_VM_CASE(9) TQT_VM_CASE(10) TQT_VM_CASE(11)
+        TQT_VM_CASE(12) TQT_VM_CASE(13) TQT_VM_CASE(14) TQT_VM_CASE(15) TQT_VM_CASE(16)
+        TQT_VM_CASE(17) TQT_VM_CASE(18) TQT_VM_CASE(19) TQT_VM_CASE(20) TQT_VM_CASE(21)
+        TQT_VM_CASE(22)
+#undef TQT_VM_CASE
+    default: __builtin_amdgcn_s_waitcnt(waitcnt_vm0(23)); break;
+    }
+    asm volatile("" ::: "memory");
+}
+
+template <int K, int PK, int OUT>
+__global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
+{
+    constexpr int NW = 16;
+    constexpr int BPW = K / (32 * NW);        // 32-k blocks per wave (8 or 4)
+    constexpr int NG = BPW / 4;               // 4-block groups per wave
+    constexpr int HB = BPW / 2;               // blocks per half of the A slice
+    constexpr int CB = BPW * 16;              // weight bytes of one channel's k-slice
+    constexpr int WSLOT = kNTile * CB;        // weight bytes per wave per tile
+    constexpr int SSLOT = 256;                // scale bytes per wave per tile (one dword load)
+    constexpr int SLOT = WSLOT + SSLOT;
+    constexpr int NSLOT = 3;
+    constexpr int NDW = WSLOT / 1024 + 1;     // loads per wave per tile
+    constexpr int OUTS = kMRows * kNTile;     // outputs per tile
+    static_assert(K == 2048 || K == 4096, "LDS strip kernel k");
+    static_assert(kPackW4A16NStep == kNTile, "a packed weight panel is one tile");
+    static_assert(kMRows == 32 && kNTile == 16 && OUTS * 2 == NW * 64, "epilogue thread map");
+    static_assert(kStripTiles * kNTile == 64, "one bias per lane of wave 0");
+    static_assert(NSLOT * NDW + BPW <= 23, "wait counts");
+    __shared__ __attribute__((aligned(16))) int8_t s_ring[NW][NSLOT][SLOT];
+    __shared__ __attribute__((aligned(16))) float s_part[NW * OUTS];
+    __shared__ float s_bias[kStripTiles * kNTile];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int fr = lane & 15;
+    const int fg = lane >> 4;
+    const int mg0 = blockIdx.y * kMRows;
+
+    const int t_begin = static_cast<int>((static_cast<long long>(blockIdx.x) * a.ntiles) / nwg);
+    const int t_end = static_cast<int>((static_cast<long long>(blockIdx.x + 1) * a.ntiles) / nwg);
+    const int ntl = t_end - t_begin;  // 1 .. kStripTiles
+    const int npro = min(ntl, NSLOT);
+
+    // A slice of this wave, loaded by asm so that the compiler adds no wait for it: the waits
+    // below count these loads with the ring's (all of them in issue order).
+    u32x4 ra[BPW][2];
+    auto load_a = [&](int j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            asm volatile("global_load_dwordx4 %0, %1, off"
+                         : "=v"(ra[j][mt])
+                         : "v"(a_slice_addr<BPW, PK>(a, mg0, wave, lane, j, mt))
+                         : "memory");
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < HB; ++j) {
+        load_a(j);
+    }
+    // The bias of every tile's 16 channels, loaded by wave 0 with A for the same reason as A (a
+    // compiler-placed wait for a load issued later would drain the whole ring; C, when given, is
+    // read that way in the epilogue, at that cost) and parked in LDS.
+    uint32_t rb = 0;
+    if (wave == 0 && a.bias) {
+        const int gn = (t_begin + (lane >> 4)) * kNTile + (lane & 15);
+        if ((lane >> 4) < ntl && gn < a.N) {
+            rb = load_out_bits_async<OUT>(a.bias, gn);
+        }
+    }
+
+    // Tiles whose weights are one whole packed panel (16 channels); a narrower last panel is
+    // gathered channel by channel like plain rows, into the plain slot layout.
+    auto packed_tile = [&](int t) { return (PK & PK_B) != 0 && (t + 1) * kNTile <= a.N; };
+    // This wave's k-slice of tile tl into its slot sl: NDW loads.
+    auto issue = [&](int tl, int sl) {
+        const int t = t_begin + tl;
+        int8_t *slot = &s_ring[wave][sl][0];
+#pragma unroll
+        for (int h = 0; h < WSLOT / 1024; ++h) {
+            const uint8_t *src;
+            if (packed_tile(t)) {
+                int wmul;
+                src = b_row_ptr<PK>(a, t * kNTile, wmul) + wave * (kNTile * CB) + h * 1024 +
+                      lane * 16;
+            } else {
+                int c, b;
+                if constexpr (BPW == 8) {
+                    c = 8 * h + (lane >> 3);
+                    b = (lane & 7) ^ (c & 7);
+                } else {
+                    c = lane >> 2;
+                    b = (lane & 3) ^ (c & 3);
+                }
+                const int n = min(t * kNTile + c, a.N - 1);
+                int wmul;
+                src = b_row_ptr<PK>(a, n, wmul) + static_cast<long long>(wave * BPW + b) * 16 * wmul;
+            }
+            dma_lds16(reinterpret_cast<const int8_t *>(src), slot + h * 1024);
+        }
+        // scales: channel c's BPW f16 at c * 2 BPW (lanes past the 16 channels repeat them)
+        constexpr int LPC = BPW / 2;  // lanes (dwords) per channel
+        const int c = (lane / LPC) & 15;
+        const int n = min(t * kNTile + c, a.N - 1);
+        dma_lds4(a.scale_b + static_cast<long long>(n) * a.ldsb + wave * BPW + (lane % LPC) * 2,
+                 slot + WSLOT);
+    };
+
+    // every wave's first half of A is requested before anyone's tile or second half
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(0, 0);
+#pragma unroll
+    for (int j = HB; j < BPW; ++j) {
+        load_a(j);
+    }
+    for (int i = 1; i < npro; ++i) {
+        issue(i, i);
+    }
+    // In flight, oldest first: A[0, HB) + bias, tile 0 (NDW), A[HB, BPW) (BPW loads), tiles
+    // 1 .. npro - 1. First half of A in:
+    wait_vm_upto(npro * NDW + BPW);
+#pragma unroll
+    for (int j = 0; j < HB; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            asm volatile("" : "+v"(ra[j][mt]));
+        }
+    }
+    asm volatile("" : "+v"(rb));
+    if (wave == 0) {
+        s_bias[lane] = out_bits_to_f32<OUT>(rb);  // read after the first tile's meeting
+    }
+    // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
+    // The wave's own partials area of s_part stages its A (no other wave touches it). The empty
+    // asm keeps the fragments as computed (no re-permutation inside the tile loop).
+    int8_t *stage = reinterpret_cast<int8_t *>(&s_part[wave * OUTS]);
+    f16x8 fa[BPW][2];
+    a_slice_to_mfma<BPW, PK, 0, HB>(ra, fa, stage, lane);
+#pragma unroll
+    for (int j = 0; j < HB; ++j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            asm volatile("" : "+v"(fa[j][mt]));
+        }
+    }
+    // the second half, once it is in (tile 0 only)
+    auto second_half = [&]() {
+        wait_vm_upto((npro - 1) * NDW);
+#pragma unroll
+        for (int j = HB; j < BPW; ++j) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                asm volatile("" : "+v"(ra[j][mt]));
+            }
+        }
+        a_slice_to_mfma<BPW, PK, HB, BPW>(ra, fa, stage, lane);
+#pragma unroll
+        for (int j = HB; j < BPW; ++j) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                asm volatile("" : "+v"(fa[j][mt]));
+            }
+        }
+    };
+    uint32_t magic;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+
+    // Epilogue map: thread pair (2 p, 2 p + 1) owns output p = row * 16 + col of each tile, the
+    // even thread summing waves 0-7's partials and the odd one waves 8-15's.
+    const int half = tid & 1;
+    const int orow = tid >> 5;
+    const int ocol = (tid >> 1) & 15;
+    const int gm = mg0 + orow;
+    // the output's place in a wave's partials: (mt, lane fg * 16 + col, r) of the MFMA result
+    const int pidx = (orow >> 4) * 256 + (((orow >> 2) & 3) * 16 + ocol) * 4 + (orow & 3);
+
+    // One tile; tile 0 (FIRST, peeled off the loop) brings in the second half of A on the way.
+    auto tile = [&](int tl, auto first) {
+        constexpr bool FIRST = decltype(first)::value;
+        const int sl = tl % NSLOT;
+        // this wave's loads of tile tl have landed (later ones may still be in flight; for tile
+        // 0, the second half of A too)
+        wait_vm_upto(FIRST ? BPW + (npro - 1) * NDW : min(ntl - 1 - tl, NSLOT - 1) * NDW);
+        const int8_t *slot = &s_ring[wave][sl][0];
+        const bool panel = packed_tile(t_begin + tl);
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int q = 0; q < NG; ++q) {
+            if constexpr (FIRST) {
+                if (q == NG / 2) {
+                    second_half();  // before the first group that uses it
+                }
+            }
+            const int j = 4 * q + fg;
+            int off;
+            if constexpr (BPW == 8) {
+                off = panel ? j * 256 + fr * 16 : fr * CB + ((j ^ (fr & 7)) << 4);
+            } else {
+                off = panel ? j * 256 + fr * 16 : fr * CB + ((j ^ (fr & 3)) << 4);
+            }
+            const u32x4 wv = *reinterpret_cast<const u32x4 *>(slot + off);
+            const uint64_t sc =
+                *reinterpret_cast<const uint64_t *>(slot + WSLOT + fr * (2 * BPW) + q * 8);
+            uint32_t p[4] = {wv[0], wv[1], wv[2], wv[3]};
+            if constexpr ((PK & PK_B) == 0) {
+                transpose_lane_groups(p);  // packed weights are stored transposed already
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                f16x8 wq = unpack_q8_lds(p[jj], magic);
+                // this block's MFMAs after the previous block's FMAs: one block's partials live
+                // at a time (four waves per SIMD hide the MFMA -> FMA latency instead)
+                asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(wq));
+                const uint16_t sbits = static_cast<uint16_t>(sc >> (16 * jj));
+                const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sbits));
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        fa[4 * q + jj][mt], wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        acc[mt][r] = __builtin_fmaf(part[r], sf, acc[mt][r]);
+                    }
+                }
+            }
+        }
+        // this wave has read its slot (the MFMAs consumed it): refill it with the tile NSLOT
+        // ahead before meeting the other waves
+        if (tl + NSLOT < ntl) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(tl + NSLOT, sl);
+        }
+        if constexpr (!FIRST) {
+            // every thread has read the previous tile's partials
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            *reinterpret_cast<f32x4 *>(&s_part[wave * OUTS + mt * 256 + lane * 4]) = acc[mt];
+        }
+        // partials written (LDS only: the ring's loads stay in flight across this barrier)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW / 2; ++w) {
+            v += s_part[(half * (NW / 2) + w) * OUTS + pidx];
+        }
+        // the pair's other half (lane ^ 1), added in the order half 0 + half 1 on both lanes
+        const float o = __builtin_bit_cast(
+            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
+        v = half == 0 ? v + o : o + v;
+        const int gn = (t_begin + tl) * kNTile + ocol;
+        if (half == 0 && gm < a.M && gn < a.N) {
+            if (a.C) {
+                v += load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
+            }
+            if (a.bias) {
+                v += s_bias[tl * kNTile + ocol];
+            }
+            v = fmaxf(v, a.cmin);
+            v = fminf(v, a.cmax);
+            store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn, v);
+        }
+    };
+    tile(0, std::true_type{});
+#pragma unroll 1
+    for (int tl = 1; tl < ntl; ++tl) {
+        tile(tl, std::false_type{});
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm0(0));
 }
 
 // Generic path: the reference test oracle's operation order, one thread per output
@@ -582,22 +1005,22 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
         TQT_REQUIRE(gy < 65536 && nwg < (1ll << 31), "grid too large");
         const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(gy));
         const int nw = static_cast<int>(nwg);
-        // 16 waves (a 256-k slice each) where the k-slices allow, else 8
+        // k 2048 / 4096: weights staged through LDS; k 3072: the register strip kernel (8 waves)
         if (packed) {
             if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_AB, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_lds_kernel<4096, PK_AB, OUT>), grid, dim3(1024), 0, s, a, nw);
             } else if (k == 3072) {
                 hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_AB, OUT, 8>), grid, dim3(512), 0, s, a, nw);
             } else {
-                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_AB, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_lds_kernel<2048, PK_AB, OUT>), grid, dim3(1024), 0, s, a, nw);
             }
         } else {
             if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<4096, PK_NONE, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_lds_kernel<4096, PK_NONE, OUT>), grid, dim3(1024), 0, s, a, nw);
             } else if (k == 3072) {
                 hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_NONE, OUT, 8>), grid, dim3(512), 0, s, a, nw);
             } else {
-                hipLaunchKernelGGL((w4a16_regs_kernel<2048, PK_NONE, OUT, 16>), grid, dim3(1024), 0, s, a, nw);
+                hipLaunchKernelGGL((w4a16_lds_kernel<2048, PK_NONE, OUT>), grid, dim3(1024), 0, s, a, nw);
             }
         }
     } else if (fast) {

@@ -48,6 +48,63 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
+// One global -> LDS load of 16 bytes per lane (lane i writes lds + 16 * i; lds is wave-uniform).
+// It is inline asm rather than __builtin_amdgcn_global_load_lds on purpose: the compiler tracks
+// the builtin's LDS write and, where its alias tracking of the ring stages is lost (the pipelined
+// loop's back edge), guards the next LDS reads with vmcnt(0), which drains every stage in flight
+// and serializes the stream (measured: 22.9 us -> 16 us per W8A8 M512 launch without it). The
+// kernels order these writes themselves with explicit vmcnt waits and s_barrier; the "memory"
+// clobber keeps the compiler's own LDS accesses on their side of each load. M0 carries the LDS
+// base (the low 32 bits of a flat LDS address are its LDS offset); nothing else in these kernels
+// uses M0. gfx9 needs one wait state between an SALU write of M0 and an LDS-DMA load that reads
+// it; the compiler cannot insert it inside an asm block, so the asm carries its own s_nop 0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_lds16(const int8_t *src, int8_t *lds)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t base =
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base)
+                 : "memory", "m0");
+#else
+    (void)src;
+    (void)lds;
+#endif
+}
+
+// 4 bytes per lane (lane i's dword at lds + 4 i): small rows such as per-block scales.
+__device__ __forceinline__ void dma_lds4(const void *src, int8_t *lds)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t base =
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(base)
+                 : "memory", "m0");
+#else
+    (void)src;
+    (void)lds;
+#endif
+}
+
+// The same load through a buffer resource: voffset is a byte offset from the resource's base,
+// and an offset at or past its num_records reads zeros (the implicit convolution's padding taps).
+__device__ __forceinline__ void dma_lds16_buf(i32x4 rsrc, int voffset, int8_t *lds)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t base =
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset),
+                 "s"(rsrc), "s"(base)
+                 : "memory", "m0");
+#else
+    (void)rsrc;
+    (void)voffset;
+    (void)lds;
+#endif
+}
+#pragma clang diagnostic pop
+
 inline bool aligned16(const void *p)
 {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
