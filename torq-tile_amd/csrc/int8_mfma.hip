@@ -1135,16 +1135,31 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
         return;
     }
 
-    // Epilogue: lane holds D[8 * (r / 4) + 4 * h + r % 4][r32] of each 32 x 32 fragment. A
-    // lane's output rows are row_l plus compile-time offsets, so their addresses are one
-    // per-lane base plus multiples of the uniform ldd (scalar arithmetic); whole row tiles skip
-    // the per-output row check.
-    const int row_l = m0 + wm * WM + 4 * h;
+    // Epilogue: lane holds D[8 * (r / 4) + 4 * h + r % 4][r32] of each 32 x 32 fragment. Every
+    // output's address is a wave-uniform base -- the wave's first row plus a compile-time row
+    // offset, times the row stride, plus the fragment's first column: scalar arithmetic -- plus
+    // the lane's 32-bit offset 4 h ld + r32, so stores and C loads take the SGPR-base form with
+    // no per-output 64-bit VALU arithmetic (the launcher checks 4 ld + 32 < 2^31). Whole row
+    // tiles skip the per-output row check.
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int wm_u = wave_u / kStreamWavesN;
+    const int wn_u = wave_u % kStreamWavesN;
+    const int row_w = m0 + wm_u * WM;                   // the wave's first row (A / C rows)
+    const long long drow_w = a.d_row0 + row_w;          // the same row of D
+    constexpr int kES = EPI == EPI_CLAMP_I32 ? 4 : 1;   // bytes per D element
+    const int ldd32 = static_cast<int>(a.ldd);          // 136 ldd kES < 2^31 (launch_stream)
+    const uint32_t voff_d = (static_cast<uint32_t>(4 * h) * static_cast<uint32_t>(ldd32) + r32) * kES;
+    const uint32_t voff_c = static_cast<uint32_t>(4 * h) * static_cast<uint32_t>(a.ldc) + r32;
+    // D through a buffer resource based at the wave's first row and the tile's first column:
+    // each store is the lane's offset plus a scalar offset (row and fragment column)
+    const __amdgpu_buffer_rsrc_t d_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<int8_t *>(a.D) + (drow_w * a.ldd + n0) * kES, 0, 0x7fffffff, 0x00020000);
     auto epilogue = [&](auto checked) {
         constexpr bool kChecked = decltype(checked)::value;
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
-            const int lc = wn * WN + 32 * j + r32;
+            const int lc0 = wn_u * WN + 32 * j;  // the fragment's first column (uniform)
+            const int lc = lc0 + r32;
             const int gn = n0 + lc;
             if (gn >= a.N) {
                 continue;
@@ -1159,26 +1174,26 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
             // them once rather than between stores
             uint32_t cv[MF][16] = {};
             if (a.C) {
-                const long long c0 = static_cast<long long>(row_l) * a.ldc + gn;
 #pragma unroll
                 for (int i = 0; i < MF; ++i) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
-                        if (!kChecked || row_l + dr < a.M) {
-                            cv[i][r] = static_cast<uint32_t>(a.C[c0 + dr * a.ldc]);
+                        if (!kChecked || row_w + 4 * h + dr < a.M) {
+                            const int32_t *cp =
+                                a.C + (static_cast<long long>(row_w + dr) * a.ldc + n0 + lc0);
+                            cv[i][r] = static_cast<uint32_t>(cp[voff_c]);
                         }
                     }
                 }
                 __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // no compiler waits below
             }
-            const long long d0 = (a.d_row0 + row_l) * a.ldd + gn;
 #pragma unroll
             for (int i = 0; i < MF; ++i) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
-                    const int gm = row_l + dr;
+                    const int gm = row_w + 4 * h + dr;
                     if (kChecked && gm >= a.M) {
                         continue;
                     }
@@ -1188,15 +1203,18 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
                         shift = s_shift[gm - m0];
                         v += static_cast<uint32_t>(s_rbias[gm - m0]);  // 0 without a bias
                     }
-                    const long long e = d0 + dr * a.ldd;
+                    const int soff = (dr * ldd32 + lc0) * kES;
                     if constexpr (EPI == EPI_CLAMP_I32) {
                         int32_t x = static_cast<int32_t>(v);
                         x = x < a.cmin ? a.cmin : x;
                         x = x > a.cmax ? a.cmax : x;
-                        static_cast<int32_t *>(a.D)[e] = x;
+                        __builtin_amdgcn_raw_buffer_store_b32(x, d_rsrc, static_cast<int>(voff_d),
+                                                              soff, 0);
                     } else {
-                        static_cast<int8_t *>(a.D)[e] = requant_dev(static_cast<int32_t>(v), mult,
-                                                                    shift, a.zp_d, a.cmin, a.cmax);
+                        const int8_t q = requant_dev(static_cast<int32_t>(v), mult, shift, a.zp_d,
+                                                     a.cmin, a.cmax);
+                        __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(q), d_rsrc,
+                                                             static_cast<int>(voff_d), soff, 0);
                     }
                 }
             }
@@ -1329,6 +1347,13 @@ __global__ __launch_bounds__(256) void int8_generic_kernel(Int8Args a)
     }
 }
 
+// The streaming kernel's epilogue addresses D (and C) with 32-bit offsets from a tile's first row:
+// 136 rows of either must span less than 2 GiB.
+inline bool stream_offsets_fit(const Int8Args &a, int d_bytes)
+{
+    return 136ll * a.ldd * d_bytes < (1ll << 31) && (a.C == nullptr || 136ll * a.ldc * 4 < (1ll << 31));
+}
+
 template <int EPI, int PK, bool kConv = false>
 void launch_stream(const Int8Args &a, hipStream_t stream)
 {
@@ -1362,14 +1387,14 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
     // group channel count is a multiple of its 128-byte stage (conv_bytes > 0, set by the
     // convolution's run when its geometry allows).
     if constexpr (BMd == B_NK && AM == A_MATRIX) {
-        if (fast && a.K % kSK == 0) {
+        if (fast && a.K % kSK == 0 && stream_offsets_fit(a, EPI == EPI_CLAMP_I32 ? 4 : 1)) {
             launch_stream<EPI, PK>(a, stream);
             check_launch(where);
             return;
         }
     }
     if constexpr (BMd == B_NK && AM == A_CONV_CL && EPI == EPI_REQUANT_I8) {
-        if (fast && a.conv_bytes > 0 && a.cv.ICg % kSK == 0) {
+        if (fast && a.conv_bytes > 0 && a.cv.ICg % kSK == 0 && stream_offsets_fit(a, 1)) {
             launch_stream<EPI, PK, true>(a, stream);
             check_launch(where);
             return;

@@ -465,8 +465,13 @@ __device__ __forceinline__ int8_t requant_dev(int32_t acc, int32_t mult, int32_t
     int32_t y = __mulhi(acc, mult);  // high 32 bits of the signed 64-bit product
     y = y >> (shift & 31);
     y = static_cast<int32_t>(static_cast<uint32_t>(y) + static_cast<uint32_t>(zp));
-    y = max(y, min(cmin, cmax));
-    y = min(y, cmax);
+    // max(y, min(cmin, cmax)) then min(., cmax): with lo <= cmax that is the median of the three
+    const int32_t lo = min(cmin, cmax);
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(y), "v"(lo), "v"(cmax));
+#else
+    y = min(max(y, lo), cmax);
+#endif
     return static_cast<int8_t>(y);
 }
 
