@@ -184,6 +184,14 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
     // ds_writes below wait for these loads only (loads complete in order).
     const int npw = p_end - p_begin;
     const int a_chunks = rows * npw * 16;
+    // row of chunk q (rows of npw * 16 chunks) without an integer division. On the LDS path
+    // q < 64 kActLoads <= 512, so x = q / 16 < 32 and npw <= 32: (x + 0.5) / npw sits at least
+    // 1/64 from the next integer while the float error is below 2^-18, and the truncation is
+    // exact
+    const float inv_npw = 1.0f / static_cast<float>(npw > 0 ? npw : 1);
+    auto chunk_row = [&](int q) {
+        return static_cast<int>((static_cast<float>(q >> 4) + 0.5f) * inv_npw);
+    };
     int8_t *s_a = s_dyn + wave * act_slice_bytes(min(kRowsPerChunk, a.M), ppw);
     i32x4 a_chunk[kActInLds ? kActLoads : 1];
     if constexpr (kActInLds) {
@@ -192,7 +200,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
             for (int j = 0; j < kActLoads; ++j) {
                 // unconditional: chunks past the slice reload its last chunk (not stored)
                 const int q = min(lane + 64 * j, a_chunks - 1);
-                const int r = q / (npw * 16);
+                const int r = chunk_row(q);
                 const int off = (q - r * npw * 16) * 16;
                 int mul = 1;  // k multiplier of a packed row (its panel width)
                 long long base;
@@ -274,7 +282,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 for (int j = 0; j < kActLoads; ++j) {
                     const int q = lane + 64 * j;
                     if (q < a_chunks) {
-                        const int r = q / (npw * 16);
+                        const int r = chunk_row(q);
                         const int c = q - r * npw * 16;
                         *reinterpret_cast<i32x4 *>(&s_a[r * npw * 256 + ((c ^ (r & 7)) << 4)]) =
                             a_chunk[j];
