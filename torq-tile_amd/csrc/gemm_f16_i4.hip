@@ -71,7 +71,7 @@ __device__ __forceinline__ const uint8_t *a_row_ptr(const W4A16Args &a, int row,
 {
     const uint8_t *base = reinterpret_cast<const uint8_t *>(a.A);
     if constexpr ((PK & PK_A) != 0) {
-        return base + pack_row(a.pa, row, mul);
+        return base + pack_row_fixed<kPackW4A16MStep>(a.pa, row, mul);
     } else {
         mul = 1;
         return base + static_cast<long long>(row) * a.lda * 2;
@@ -84,7 +84,7 @@ template <int PK>
 __device__ __forceinline__ const uint8_t *b_row_ptr(const W4A16Args &a, int n, int &mul)
 {
     if constexpr ((PK & PK_B) != 0) {
-        return a.B + pack_row(a.pb, n, mul);
+        return a.B + pack_row_fixed<kPackW4A16NStep>(a.pb, n, mul);
     } else {
         mul = 1;
         return a.B + static_cast<long long>(n) * a.bstride;
@@ -587,7 +587,7 @@ __device__ __forceinline__ float out_bits_to_f32(uint32_t v)
 // hits distinct slots; a whole packed panel's k-slice is contiguous (2 KiB) and is copied as it
 // lies. Per tile: the strip kernel's decode, v_mfma_f32_16x16x32_f16 per block and scale FMA;
 // then the 16 partials (ds_write_b128) meet in LDS and every thread sums 8 of one output's 16,
-// paired with its neighbour lane.
+// paired with the lane 32 above or below it.
 // ---------------------------------------------------------------------------------------------
 
 // unpack_q8_sgpr with one shift instead of three: nibbles 1, 3 (5, 7) are inserted at bits 4-7
@@ -639,13 +639,15 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     constexpr int NSLOT = 3;
     constexpr int NDW = WSLOT / 1024 + 1;     // loads per wave per tile
     constexpr int OUTS = kMRows * kNTile;     // outputs per tile
+    // floats per wave's partials: 4 past OUTS puts waves w and w + 8 32 banks apart
+    constexpr int PSTRIDE = OUTS + 4;
     static_assert(K == 2048 || K == 4096, "LDS strip kernel k");
     static_assert(kPackW4A16NStep == kNTile, "a packed weight panel is one tile");
     static_assert(kMRows == 32 && kNTile == 16 && OUTS * 2 == NW * 64, "epilogue thread map");
     static_assert(kStripTiles * kNTile == 64, "one bias per lane of wave 0");
     static_assert(NSLOT * NDW + BPW <= 23, "wait counts");
     __shared__ __attribute__((aligned(16))) int8_t s_ring[NW][NSLOT][SLOT];
-    __shared__ __attribute__((aligned(16))) float s_part[NW * OUTS];
+    __shared__ __attribute__((aligned(16))) float s_part[NW * PSTRIDE];
     __shared__ float s_bias[kStripTiles * kNTile];
 
     const int tid = threadIdx.x;
@@ -752,7 +754,7 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
     // The wave's own partials area of s_part stages its A (no other wave touches it). The empty
     // asm keeps the fragments as computed (no re-permutation inside the tile loop).
-    int8_t *stage = reinterpret_cast<int8_t *>(&s_part[wave * OUTS]);
+    int8_t *stage = reinterpret_cast<int8_t *>(&s_part[wave * PSTRIDE]);
     f16x8 fa[BPW][2];
     a_slice_to_mfma<BPW, PK, 0, HB>(ra, fa, stage, lane);
 #pragma unroll
@@ -784,11 +786,13 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
 
-    // Epilogue map: thread pair (2 p, 2 p + 1) owns output p = row * 16 + col of each tile, the
-    // even thread summing waves 0-7's partials and the odd one waves 8-15's.
-    const int half = tid & 1;
-    const int orow = tid >> 5;
-    const int ocol = (tid >> 1) & 15;
+    // Epilogue map: lanes i and i + 32 (i < 32) of wave w own output row (w / 2) * 4 + i % 4,
+    // column (w % 2) * 8 + i / 4 of each tile, the lower lane summing waves 0-7's partials and the
+    // upper one waves 8-15's. A half-wave thus reads 32 consecutive floats of one wave's partials
+    // and the two halves' reads are 32 banks apart: no bank conflicts.
+    const int half = lane >> 5;
+    const int orow = (wave >> 1) * 4 + (lane & 3);
+    const int ocol = (wave & 1) * 8 + ((lane & 31) >> 2);
     const int gm = mg0 + orow;
     // the output's place in a wave's partials: (mt, lane fg * 16 + col, r) of the MFMA result
     const int pidx = (orow >> 4) * 256 + (((orow >> 2) & 3) * 16 + ocol) * 4 + (orow & 3);
@@ -856,7 +860,7 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
         }
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            *reinterpret_cast<f32x4 *>(&s_part[wave * OUTS + mt * 256 + lane * 4]) = acc[mt];
+            *reinterpret_cast<f32x4 *>(&s_part[wave * PSTRIDE + mt * 256 + lane * 4]) = acc[mt];
         }
         // partials written (LDS only: the ring's loads stay in flight across this barrier)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -865,12 +869,16 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < NW / 2; ++w) {
-            v += s_part[(half * (NW / 2) + w) * OUTS + pidx];
+            v += s_part[(half * (NW / 2) + w) * PSTRIDE + pidx];
         }
-        // the pair's other half (lane ^ 1), added in the order half 0 + half 1 on both lanes
-        const float o = __builtin_bit_cast(
-            float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));
-        v = half == 0 ? v + o : o + v;
+        // half 0 + half 1: v_permlane32_swap on two copies of v leaves the lower half's sums in
+        // every lane of one register and the upper half's in the other (an f32 add gives the
+        // same bits either way round). Written as asm: the builtin with equal operands is folded
+        // as if its two results were equal.
+        uint32_t x0 = __builtin_bit_cast(uint32_t, v);
+        uint32_t x1 = x0;
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x0), "+v"(x1));
+        v = __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
         const int gn = (t_begin + tl) * kNTile + ocol;
         if (half == 0 && gm < a.M && gn < a.N) {
             if (a.C) {

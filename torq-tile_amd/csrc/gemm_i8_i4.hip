@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 int mul = 1;  // k multiplier of a packed row (its panel width)
                 long long base;
                 if constexpr ((PK & PK_A) != 0) {
-                    base = pack_row(a.pa, m0 + r, mul);
+                    base = pack_row_fixed<kPackW4A8MStep>(a.pa, m0 + r, mul);
                 } else {
                     base = static_cast<long long>(m0 + r) * a.lda;
                 }
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
     if constexpr (!kActInLds) {
         const int r = m0 + min(fr, rows - 1);
         if constexpr ((PK & PK_A) != 0) {
-            a_rowp = a.A + pack_row(a.pa, r, a_mul);
+            a_rowp = a.A + pack_row_fixed<kPackW4A8MStep>(a.pa, r, a_mul);
         } else {
             a_rowp = a.A + static_cast<long long>(r) * a.lda;
         }
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         const int grow = n0 + row < a.N ? n0 + row : n0;
         w_mul[h] = 1;
         if constexpr ((PK & PK_B) != 0) {
-            w_rowp[h] = a.B + pack_row(a.pb, grow, w_mul[h]);
+            w_rowp[h] = a.B + pack_row_fixed<kPackW4A8NStep>(a.pb, grow, w_mul[h]);
         } else {
             w_rowp[h] = a.B + static_cast<long long>(grow) * a.bstride;
         }

@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             const int r = a_ok[j] ? gm : 0;
             long long base;
             if constexpr ((PK & PK_A) != 0) {
-                base = pack_row(a.pa, r, a_mul[j]);
+                base = pack_row_fixed<kPackI8MStep>(a.pa, r, a_mul[j]);
             } else {
                 base = static_cast<long long>(r) * a.lda;
             }
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void int8_mfma_kernel(Int8Args a)
             long long base;
             b_mul[j] = 1;
             if constexpr ((PK & PK_B) != 0) {
-                base = pack_row(a.pb, r, b_mul[j]);
+                base = pack_row_fixed<kPackI8NStep>(a.pb, r, b_mul[j]);
             } else {
                 base = static_cast<long long>(r) * a.ldb;
             }
@@ -863,7 +863,7 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
                 chunk * 16u);
             base = 0;
         } else if constexpr (kAP) {
-            base = pack_row(a.pa, gm, a_mul[j]);
+            base = pack_row_fixed<kPackI8MStep>(a.pa, gm, a_mul[j]);
         } else {
             base = static_cast<long long>(gm) * a.lda;
         }
@@ -889,7 +889,7 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
         long long base;
         b_mul[j] = 1;
         if constexpr (kBP) {
-            base = pack_row(a.pb, gn, b_mul[j]);
+            base = pack_row_fixed<kPackI8NStep>(a.pb, gn, b_mul[j]);
         } else {
             base = static_cast<long long>(gn) * a.ldb;
         }

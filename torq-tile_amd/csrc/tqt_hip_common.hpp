@@ -315,6 +315,24 @@ __host__ __device__ inline long long pack_row(const PackDesc &d, int r, int &mul
     return pack_panel_base(d, p, w) + static_cast<long long>(d.kc) * (r - p * d.step);
 }
 
+// pack_row of a packed descriptor whose step is the compile-time STEP (a power of two; r >= 0):
+// shifts and masks where pack_row divides by the run-time step.
+template <int STEP>
+__device__ __forceinline__ long long pack_row_fixed(const PackDesc &d, int r, int &mul)
+{
+    static_assert(STEP > 0 && (STEP & (STEP - 1)) == 0, "panel step");
+    const int p = static_cast<int>(static_cast<unsigned>(r) / STEP);
+    const int rl = static_cast<int>(static_cast<unsigned>(r) % STEP);
+    const int left = d.rows - p * STEP;
+    const int w = left < STEP ? left : STEP;
+    mul = w;
+    long long b = static_cast<long long>(p) * STEP * d.ld + static_cast<long long>(d.kc) * rl;
+    if (p > 0 && w < STEP) {
+        b -= d.shift * (STEP - w);
+    }
+    return b;
+}
+
 // Offset of byte kb from the row base pack_row returned (a plain row: kb itself). For a packed
 // row kb < 2^24 and mul <= 2^7 (the launchers of the packed fast paths check kbytes < 2^24; panel
 // heights are at most 128), so one 24-bit multiply gives it.
