@@ -1,19 +1,24 @@
 """ctypes binding of the gfx950 TORQ-Tile C ABI (libtorq_tile_gfx950.so).
 
-This is the Python-side stub a framework maintainer would add to call the library: it declares
-every exported symbol with its exact C signature (include/*.h) and mirrors the parameter
-structs field for field. Buffers are passed as raw device addresses (int); torch tensors on a
-ROCm device provide them via ``tensor.data_ptr()``.
+This is the Python-side stub a framework maintainer would add to call the library. The function
+signatures are not restated here: they are read from the C declarations in include/*.h, so the
+headers stay the one definition of the ABI, and every declared function must be exported by the
+library or loading fails. The parameter structs are mirrored field for field. Buffers are passed
+as raw device addresses (int); torch tensors on a ROCm device provide them via
+``tensor.data_ptr()``.
 
 Loading fails loudly: there is no CPU fallback. ``load()`` raises if the shared library has not
 been built (``make -C torq-tile_amd``).
 """
 
 import ctypes
+import glob
 import os
+import re
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libtorq_tile_gfx950.so")
+INCLUDE_DIR = os.path.join(os.path.dirname(_HERE), "include")
 
 c_size = ctypes.c_size_t
 c_vp = ctypes.c_void_p
@@ -143,259 +148,51 @@ def _sym(kind, action):
     return "tqt_%s_%s_%s" % (action, name, VARIANT)
 
 
-# (action, restype, argtypes) per kernel type; float16 / bfloat16 clamps are not callable from
-# ctypes and those runs are reached through the test shim instead.
-_GEMM_I8_ARGS = [c_size, c_size, c_size, c_vp, c_size, c_size, c_vp, c_size, c_size, c_vp,
-                 c_size, c_vp, c_size]
-_SIGS = {
-    "clamp": {
-        "get_m_step": (c_size, []),
-        "get_n_step": (c_size, []),
-        "get_a_offset": (c_size, [c_size] * 3),
-        "get_b_offset": (c_size, [c_size] * 3),
-        "get_c_offset": (c_size, [c_size] * 3),
-        "get_d_offset": (c_size, [c_size] * 3),
-        "get_d_size": (c_size, [c_size] * 2),
-        "run": (None, _GEMM_I8_ARGS + [ctypes.c_int32, ctypes.c_int32]),
-        "run_async": (None, _GEMM_I8_ARGS + [ctypes.c_int32, ctypes.c_int32, c_vp]),
-    },
-    "w8a8": {
-        "get_m_step": (c_size, []),
-        "get_n_step": (c_size, []),
-        "get_a_offset": (c_size, [c_size] * 3),
-        "get_b_offset": (c_size, [c_size] * 3),
-        "get_c_offset": (c_size, [c_size] * 3),
-        "get_bias_offset": (c_size, [c_size]),
-        "get_d_offset": (c_size, [c_size] * 3),
-        "get_d_size": (c_size, [c_size] * 2),
-        "run": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_int8, ctypes.c_int8,
-                                       ctypes.POINTER(QAI8QSI8CXParams)]),
-        "run_async": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_int8, ctypes.c_int8,
-                                             ctypes.POINTER(QAI8QSI8CXParams), c_vp]),
-    },
-    "w4a8": {
-        "get_m_step": (c_size, []),
-        "get_n_step": (c_size, []),
-        "get_a_offset": (c_size, [c_size] * 3),
-        "get_b_offset": (c_size, [c_size] * 3),
-        "get_c_offset": (c_size, [c_size] * 3),
-        "get_bias_offset": (c_size, [c_size]),
-        "get_d_offset": (c_size, [c_size] * 3),
-        "get_d_size": (c_size, [c_size] * 2),
-        "run": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float,
-                                       ctypes.POINTER(QAI8DXQSI4CXParams)]),
-        "run_async": (None, _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float,
-                                             ctypes.POINTER(QAI8DXQSI4CXParams), c_vp]),
-    },
-    "w4a16": {
-        "get_m_step": (c_size, []),
-        "get_n_step": (c_size, []),
-        "get_a_offset": (c_size, [c_size] * 4),
-        "get_b_offset": (c_size, [c_size] * 4),
-        "get_scale_b_offset": (c_size, [c_size] * 3),
-        "get_c_offset": (c_size, [c_size] * 3),
-        "get_bias_offset": (c_size, [c_size]),
-        "get_d_offset": (c_size, [c_size] * 3),
-        "get_d_size": (c_size, [c_size] * 2),
-    },
-    "igemmcl": {
-        "get_m_step": (c_size, []),
-        "get_n_step": (c_size, []),
-        "get_b_offset": (c_size, [c_size] * 3),
-        "get_c_offset": (c_size, [c_size] * 3),
-        "get_bias_offset": (c_size, [c_size]),
-        "get_d_offset": (c_size, [c_size] * 3),
-        "get_d_size": (c_size, [c_size] * 2),
-        "run": (None, [c_size, c_size, c_size, c_vp, c_size, c_size, c_size, c_vp, c_size, c_size,
-                       c_vp, c_size, c_vp, c_size, c_vp, ctypes.c_int8, ctypes.c_int8,
-                       ctypes.POINTER(ConvParams), ctypes.POINTER(QAI8QSI8CXParams)]),
-        "run_async": (None, [c_size, c_size, c_size, c_vp, c_size, c_size, c_size, c_vp, c_size,
-                             c_size, c_vp, c_size, c_vp, c_size, c_vp, ctypes.c_int8,
-                             ctypes.c_int8, ctypes.POINTER(ConvParams),
-                             ctypes.POINTER(QAI8QSI8CXParams), c_vp]),
-    },
+# C type (as written in include/*.h, parameter name dropped) -> ctypes type.
+_CTYPES = {
+    "size_t": c_size,
+    "int32_t": ctypes.c_int32,
+    "int8_t": ctypes.c_int8,
+    "float": ctypes.c_float,
+    "const void *": c_vp,
+    "void *": c_vp,
+    "const float *": c_vp,
+    "float *": c_vp,
+    "int8_t *": c_vp,
+    "int32_t *": c_vp,
+    "const char *": ctypes.c_char_p,
+    "const tqt_conv_params *": ctypes.POINTER(ConvParams),
+    "const struct tqt_conv_params *": ctypes.POINTER(ConvParams),
+    "const struct tqt_qai8_qai8_qsi8cx_params *": ctypes.POINTER(QAI8QSI8CXParams),
+    "const struct tqt_qai8dx_qsi4cx_params *": ctypes.POINTER(QAI8DXQSI4CXParams),
+    "const struct tqt_qai8dxp_qsi8cxp_params *": ctypes.POINTER(QAI8DXPQSI8CXPParams),
+    "const struct tqt_qai8_qsi8dx_qai8_params *": ctypes.POINTER(QAI8QSI8DXQAI8Params),
 }
+# f16 / bf16 values are passed in SSE registers on x86-64, which ctypes cannot fill: functions
+# taking them are checked for export but not bound (the test shim in tests/abi_shim calls them).
+_UNBOUND = ("float16_t", "bfloat16_t")
+_DECL = re.compile(r"^(size_t|void|const char \*)\s*(tqt_\w+)\s*\(([^;]*?)\)\s*;", re.M)
 
 
-_PACK = [c_size] * 5 + [c_vp, c_vp]  # (rows, k, ld, ld_packed, k_idx, src, dst)
-_OFFP = [c_size] * 4                  # (idx, k_idx, ld, actual)
-
-
-def _packed_sigs(base, packers, run_args, offsets):
-    sig = {
-        "get_m_step": (c_size, []),
-        "get_n_step": (c_size, []),
-        "get_c_offset": (c_size, [c_size] * 3),
-        "get_d_offset": (c_size, [c_size] * 3),
-        "get_d_size": (c_size, [c_size] * 2),
-    }
-    for what in offsets:
-        sig[what] = (c_size, _OFFP if "packed_offset" in what else
-                     ([c_size] * 3 if what == "get_a_offset" else [c_size] * 2))
-    if base != "clamp":
-        sig["get_bias_offset"] = (c_size, [c_size])
-    for pk in packers:
-        sig[pk] = (None, _PACK)
-        sig[pk + "_async"] = (None, _PACK + [c_vp])
-    if run_args is not None:
-        sig["run"] = (None, run_args)
-        sig["run_async"] = (None, run_args + [c_vp])
-    return sig
-
-
-_I8_REQ = [c_vp, ctypes.c_int8, ctypes.c_int8, ctypes.POINTER(QAI8QSI8CXParams)]
-_SIGS["clampp"] = _packed_sigs(
-    "clamp", ["run_a_pack", "run_b_pack", "run_bt_pack"],
-    _GEMM_I8_ARGS + [ctypes.c_int32, ctypes.c_int32],
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_SIGS["w8a8pb"] = _packed_sigs(
-    "w8a8", ["run_b_pack", "run_bt_pack"], _GEMM_I8_ARGS + _I8_REQ,
-    ["get_a_offset", "get_b_packed_offset", "get_b_packed_size"])
-_SIGS["w8a8p"] = _packed_sigs(
-    "w8a8", ["run_a_pack", "run_b_pack", "run_bt_pack"], _GEMM_I8_ARGS + _I8_REQ,
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_SIGS["w4a8p"] = _packed_sigs(
-    "w4a8", ["run_a_pack", "run_bt_pack"],
-    _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float, ctypes.POINTER(QAI8DXQSI4CXParams)],
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-# float16 clamps: the run is reached through the test shim (tqts_run_w4a16p)
-_SIGS["w4a16p"] = _packed_sigs(
-    "w4a16", ["run_a_pack", "run_bt_pack"], None,
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_SIGS["w4a16p"]["get_scale_b_offset"] = (c_size, [c_size] * 3)
-_SIGS["igemmclp"] = _packed_sigs(
-    "igemmcl", ["run_bt_pack"], _SIGS["igemmcl"]["run"][1],
-    ["get_b_packed_offset", "get_b_packed_size"])
-# f16 / bf16 clamps: the runs are reached through the test shim (tqts_run_w4a8h)
-for _kind in ("w4a8h", "w4a8b"):
-    _SIGS[_kind] = {a: v for a, v in _SIGS["w4a8"].items() if not a.startswith("run")}
-for _kind in ("w4a8hp", "w4a8bp"):
-    _SIGS[_kind] = _packed_sigs(
-        "w4a8", ["run_a_pack", "run_bt_pack"], None,
-        ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_W4A16F_RUN = ([c_size] * 4 + [c_vp, c_size, c_size] * 2 +
-               [c_vp, c_size, c_vp, c_size, c_vp, c_size, c_vp, ctypes.c_float, ctypes.c_float])
-_SIGS["w4a16f"] = dict(_SIGS["w4a16"], run=(None, _W4A16F_RUN),
-                       run_async=(None, _W4A16F_RUN + [c_vp]))
-_SIGS["w4a16fp"] = _packed_sigs(
-    "w4a16", ["run_a_pack", "run_bt_pack"], _W4A16F_RUN,
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_SIGS["w4a16fp"]["get_scale_b_offset"] = (c_size, [c_size] * 3)
-_DYN_RUN = _GEMM_I8_ARGS + [c_vp, ctypes.c_float, ctypes.c_float,
-                            ctypes.POINTER(QAI8DXPQSI8CXPParams)]
-_SIGS["w8dyn"] = {a: v for a, v in _SIGS["w4a8"].items() if not a.startswith("run")}
-_SIGS["w8dyn"].update(run=(None, _DYN_RUN), run_async=(None, _DYN_RUN + [c_vp]))
-_SIGS["w8dynh"] = {a: v for a, v in _SIGS["w4a8"].items() if not a.startswith("run")}
-_SIGS["w8dynp"] = _packed_sigs(
-    "w8dyn", ["run_a_pack", "run_b_pack", "run_bt_pack"], _DYN_RUN,
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_SIGS["w8dynhp"] = _packed_sigs(
-    "w8dyn", ["run_a_pack", "run_b_pack", "run_bt_pack"], None,
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_IM2COL = [c_size, c_vp, c_vp, ctypes.POINTER(ConvParams)]
-_IM2COLPACK = [c_size, c_vp, c_size, c_size, c_vp, ctypes.POINTER(ConvParams)]
-_SIGS["convcl"] = {
-    "get_m_step": (c_size, []),
-    "get_n_step": (c_size, []),
-    "get_b_offset": (c_size, [c_size] * 3),
-    "get_c_offset": (c_size, [c_size] * 3),
-    "get_bias_offset": (c_size, [c_size]),
-    "get_d_offset": (c_size, [c_size] * 3),
-    "get_d_size": (c_size, [c_size] * 2),
-    "get_a_im2col_size": (c_size, [c_size] * 2),
-    "get_a_im2col_offset": (c_size, [c_size] * 3),
-    "run_im2col": (None, _IM2COL),
-    "run_im2col_async": (None, _IM2COL + [c_vp]),
-    "run_conv": _SIGS["w8a8"]["run"],
-    "run_conv_async": _SIGS["w8a8"]["run_async"],
-}
-_SIGS["convclp"] = {
-    "get_m_step": (c_size, []),
-    "get_n_step": (c_size, []),
-    "get_a_im2colpack_offset": (c_size, _OFFP),
-    "get_b_packed_offset": (c_size, _OFFP),
-    "get_c_offset": (c_size, [c_size] * 3),
-    "get_bias_offset": (c_size, [c_size]),
-    "get_d_offset": (c_size, [c_size] * 3),
-    "get_d_size": (c_size, [c_size] * 2),
-    "get_a_im2colpack_size": (c_size, [c_size] * 2),
-    "get_b_packed_size": (c_size, [c_size] * 2),
-    "run_bt_pack": (None, _PACK),
-    "run_bt_pack_async": (None, _PACK + [c_vp]),
-    "run_a_im2colpack": (None, _IM2COLPACK),
-    "run_a_im2colpack_async": (None, _IM2COLPACK + [c_vp]),
-    "run_conv": _SIGS["w8a8p"]["run"],
-    "run_conv_async": _SIGS["w8a8p"]["run_async"],
-}
-_MX1_REQ = [c_vp, ctypes.c_int8, ctypes.c_int8, ctypes.POINTER(QAI8QSI8DXQAI8Params)]
-_SIGS["mx1"] = {a: v for a, v in _SIGS["w8a8"].items() if not a.startswith("run")}
-_SIGS["mx1"].update(run=(None, _GEMM_I8_ARGS + _MX1_REQ),
-                    run_async=(None, _GEMM_I8_ARGS + _MX1_REQ + [c_vp]))
-_SIGS["mx1p"] = _packed_sigs(
-    "mx1", ["run_a_pack", "run_b_pack", "run_bt_pack"], _GEMM_I8_ARGS + _MX1_REQ,
-    ["get_a_packed_offset", "get_b_packed_offset", "get_a_packed_size", "get_b_packed_size"])
-_SIGS["convcf"] = {
-    "get_m_step": (c_size, []),
-    "get_n_step": (c_size, []),
-    "get_a_offset": (c_size, [c_size] * 3),
-    "get_c_offset": (c_size, [c_size] * 3),
-    "get_bias_offset": (c_size, [c_size]),
-    "get_d_offset": (c_size, [c_size] * 3),
-    "get_d_size": (c_size, [c_size] * 2),
-    "get_b_im2col_size": (c_size, [c_size] * 2),
-    "get_b_im2col_offset": (c_size, [c_size] * 3),
-    "run_im2col": (None, _IM2COL),
-    "run_im2col_async": (None, _IM2COL + [c_vp]),
-    "run_conv": _SIGS["mx1"]["run"],
-    "run_conv_async": _SIGS["mx1"]["run_async"],
-}
-_SIGS["convcfp"] = {
-    "get_m_step": (c_size, []),
-    "get_n_step": (c_size, []),
-    "get_a_packed_offset": (c_size, _OFFP),
-    "get_b_im2colpack_offset": (c_size, _OFFP),
-    "get_c_offset": (c_size, [c_size] * 3),
-    "get_bias_offset": (c_size, [c_size]),
-    "get_d_offset": (c_size, [c_size] * 3),
-    "get_d_size": (c_size, [c_size] * 2),
-    "get_a_packed_size": (c_size, [c_size] * 2),
-    "get_b_im2colpack_size": (c_size, [c_size] * 2),
-    "run_a_pack": (None, _PACK),
-    "run_a_pack_async": (None, _PACK + [c_vp]),
-    "run_b_im2colpack": (None, _IM2COLPACK),
-    "run_b_im2colpack_async": (None, _IM2COLPACK + [c_vp]),
-    "run_conv": _SIGS["mx1p"]["run"],
-    "run_conv_async": _SIGS["mx1p"]["run_async"],
-}
-_IGEMMCF = ([c_size] * 3 + [c_vp, c_size, c_size, c_size, c_vp, c_size, c_size, c_vp, c_size, c_vp,
-                            c_size, c_vp, ctypes.c_int8, ctypes.c_int8,
-                            ctypes.POINTER(ConvParams), ctypes.POINTER(QAI8QSI8DXQAI8Params)])
-_SIGS["igemmcf"] = {
-    "get_m_step": (c_size, []),
-    "get_n_step": (c_size, []),
-    "get_a_offset": (c_size, [c_size] * 3),
-    "get_c_offset": (c_size, [c_size] * 3),
-    "get_bias_offset": (c_size, [c_size]),
-    "get_d_offset": (c_size, [c_size] * 3),
-    "get_d_size": (c_size, [c_size] * 2),
-    "run_igemm": (None, _IGEMMCF),
-    "run_igemm_async": (None, _IGEMMCF + [c_vp]),
-}
-_SIGS["igemmcfp"] = {
-    "get_m_step": (c_size, []),
-    "get_n_step": (c_size, []),
-    "get_a_packed_offset": (c_size, _OFFP),
-    "get_c_offset": (c_size, [c_size] * 3),
-    "get_bias_offset": (c_size, [c_size]),
-    "get_d_offset": (c_size, [c_size] * 3),
-    "get_d_size": (c_size, [c_size] * 2),
-    "get_a_packed_size": (c_size, [c_size] * 2),
-    "run_a_pack": (None, _PACK),
-    "run_a_pack_async": (None, _PACK + [c_vp]),
-    "run_igemm": (None, _IGEMMCF),
-    "run_igemm_async": (None, _IGEMMCF + [c_vp]),
-}
-_SHIM_RUNS = ("w4a16", "w4a16p", "w4a8h", "w4a8b", "w4a8hp", "w4a8bp", "w8dynh", "w8dynhp")
+def declarations(include_dir=INCLUDE_DIR):
+    """{symbol: (restype, argtypes)} for every function include/*.h declares; argtypes is None
+    for a function with an argument ctypes cannot pass."""
+    decls = {}
+    for header in sorted(glob.glob(os.path.join(include_dir, "*.h"))):
+        with open(header) as fh:
+            text = re.sub(r"/\*.*?\*/", " ", fh.read(), flags=re.S)
+        for ret, name, args in _DECL.findall(text):
+            args = " ".join(args.split())
+            params = [] if args in ("", "void") else [p.strip() for p in args.split(",")]
+            types = [re.sub(r"\s*\b\w+$", "", p) for p in params]
+            restype = None if ret == "void" else _CTYPES[ret]
+            if any(t in _UNBOUND for t in types):
+                decls[name] = (restype, None)
+            else:
+                decls[name] = (restype, [_CTYPES[t] for t in types])
+    if not decls:
+        raise RuntimeError("no tqt_ declarations found under %s" % include_dir)
+    return decls
 
 
 class Lib:
@@ -407,34 +204,24 @@ class Lib:
                 "gfx950 library not built: %s missing (run make -C torq-tile_amd)" % path)
         self.path = path
         self.dll = ctypes.CDLL(path)
+        self._decls = declarations()
         self._fns = {}
-        for kind, actions in _SIGS.items():
-            for action, (res, args) in actions.items():
-                f = getattr(self.dll, _sym(kind, action))
-                f.restype = res
-                f.argtypes = args
-                self._fns[(kind, action)] = f
-        self.dll.tqt_gfx950_target.restype = ctypes.c_char_p
-        self.dll.tqt_gfx950_target.argtypes = []
+        for name, (res, args) in self._decls.items():
+            f = getattr(self.dll, name)  # AttributeError: declared but not exported
+            if args is None:
+                continue
+            f.restype = res
+            f.argtypes = args
+            self._fns[name] = f
         # dynamic per-row activation quantization (include/tqt_quantize_qai8dx_gfx950.h)
-        qargs = [c_size, c_size, c_vp, c_size, c_vp, c_size, c_vp, c_vp]
-        self.quantize = self.dll.tqt_run_quantize_qai8dx_f32_gfx950
-        self.quantize.restype = None
-        self.quantize.argtypes = qargs
-        self.quantize_async = self.dll.tqt_run_quantize_qai8dx_f32_gfx950_async
-        self.quantize_async.restype = None
-        self.quantize_async.argtypes = qargs + [c_vp]
+        self.quantize = self._fns["tqt_run_quantize_qai8dx_f32_gfx950"]
+        self.quantize_async = self._fns["tqt_run_quantize_qai8dx_f32_gfx950_async"]
 
     def fn(self, kind, action):
-        return self._fns[(kind, action)]
+        return self._fns[_sym(kind, action)]
 
     def symbol_names(self):
-        names = [_sym(k, a) for (k, a) in self._fns]
-        for kind in _SHIM_RUNS:
-            names += [_sym(kind, "run"), _sym(kind, "run_async")]
-        names += ["tqt_gfx950_target", "tqt_run_quantize_qai8dx_f32_gfx950",
-                  "tqt_run_quantize_qai8dx_f32_gfx950_async"]
-        return sorted(set(names))
+        return sorted(self._decls)
 
 
 _LIB = None
