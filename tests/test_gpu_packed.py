@@ -256,7 +256,8 @@ def test_w4a8_packed_run(gpu, m, n, k):
 
 
 W4A16_SHAPES = [(32, 96, 2048, 32), (32, 14336 // 64, 4096, 32), (33, 40, 3072, 32),
-                (32, 48, 384, 32), (7, 20, 64, 16), (5, 18, 96, 32)]
+                (32, 48, 384, 32), (7, 20, 64, 16), (5, 18, 96, 32),
+                (33, 8200, 2048, 32), (20, 4104, 4096, 32)]
 
 
 def run_w4a16p(shim, d, lda_extra=0):

@@ -225,7 +225,12 @@ W4A16_REF_SHAPES = [(8, 8, 4, 2, {}), (16, 16, 8, 2, {}), (32, 32, 32, 2, {}), (
                     (32, 32, 32, 4, dict(c=True, bias=True, clamp=(-0.5, 0.5)))]
 W4A16_FAST_SHAPES = [(32, 256, 4096, 32, dict(bias=True)), (1, 48, 128, 32, dict(bias=True)),
                      (33, 40, 512, 32, dict(c=True, bias=True)),
-                     (64, 160, 1152, 32, dict(clamp=(-0.5, 0.5)))]
+                     (64, 160, 1152, 32, dict(clamp=(-0.5, 0.5))),
+                     # LDS strip kernel with 2-3 tiles per workgroup, a partial last tile and
+                     # rows past m (k 2048), and 1-2 tiles per workgroup ending in a partial
+                     # tile (k 4096)
+                     (33, 8200, 2048, 32, dict(c=True, bias=True)),
+                     (20, 4104, 4096, 32, dict(bias=True, clamp=(-0.5, 0.5)))]
 
 
 @pytest.mark.parametrize("m,n,k,bl,opt", W4A16_REF_SHAPES + W4A16_FAST_SHAPES)

@@ -117,7 +117,8 @@ def gen(m, n, k, bl, seed, with_c, with_bias=True):
 # (m, n, k, bl): the strip kernel (k 2048/3072/4096, bl 32), the block kernel (other k % 128,
 # bl 32) and the generic kernel (bl 16, k not a multiple of 128)
 SHAPES = [(32, 96, 4096, 32), (33, 40, 2048, 32), (7, 50, 3072, 32), (32, 48, 1024, 32),
-          (5, 18, 384, 32), (9, 20, 64, 16), (6, 17, 96, 32), (3, 5, 10, 2)]
+          (5, 18, 384, 32), (9, 20, 64, 16), (6, 17, 96, 32), (3, 5, 10, 2),
+          (33, 8200, 2048, 32)]
 
 
 @pytest.mark.parametrize("m,n,k,bl", SHAPES)
