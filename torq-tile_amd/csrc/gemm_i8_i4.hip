@@ -84,6 +84,16 @@ __device__ __forceinline__ float epilogue_f32(int32_t acc, int32_t rsum, int32_t
     return f;
 }
 
+// 16 activation bytes -> the byte order of the decoded weights within each 8-byte group:
+// (even k of bytes 0-7, odd k of bytes 0-7, even k of bytes 8-15, odd k of bytes 8-15).
+__device__ __forceinline__ i32x4 permute_act16(const i32x4 v)
+{
+    return i32x4{static_cast<int32_t>(__builtin_amdgcn_perm(v[1], v[0], 0x06040200u)),
+                 static_cast<int32_t>(__builtin_amdgcn_perm(v[1], v[0], 0x07050301u)),
+                 static_cast<int32_t>(__builtin_amdgcn_perm(v[3], v[2], 0x06040200u)),
+                 static_cast<int32_t>(__builtin_amdgcn_perm(v[3], v[2], 0x07050301u))};
+}
+
 // 32 activation bytes (k = 0..31 of this lane's slice) -> two MFMA operands in the byte order
 // of the decoded weights: (even k of bytes 0-7, odd k of bytes 0-7, even k 8-15, odd k 8-15).
 __device__ __forceinline__ void permute_act(const i32x4 v0, const i32x4 v1, i32x4 &x0, i32x4 &x1)
@@ -154,6 +164,8 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
     const bool out_ok = tid < 256 && orow < rows && n0 + ocol < a.N;
     float p_sb = 0.f, p_sa = 0.f, p_bias = 0.f, p_c = 0.f;
     int32_t p_za = 0;
+    // output rows are addressed as the workgroup's first row (uniform, 64-bit) plus a 24-bit
+    // per-thread offset (the launcher keeps ldc, ldd, lda and the weight row stride < 2^24)
     if (out_ok) {
         const int gm = m0 + orow, gn = n0 + ocol;
         p_sb = a.scale_b[gn];
@@ -163,7 +175,8 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
             p_bias = load_out<OUT>(a.bias, gn);
         }
         if (a.C) {
-            p_c = load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
+            p_c = load_out<OUT>(a.C, static_cast<long long>(m0) * a.ldc +
+                                         __umul24(orow, static_cast<uint32_t>(a.ldc)) + gn);
         }
     }
 
@@ -201,13 +214,14 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 // unconditional: chunks past the slice reload its last chunk (not stored)
                 const int q = min(lane + 64 * j, a_chunks - 1);
                 const int r = chunk_row(q);
-                const int off = (q - r * npw * 16) * 16;
+                const int off = (q - static_cast<int>(__umul24(r, npw)) * 16) * 16;
                 int mul = 1;  // k multiplier of a packed row (its panel width)
                 long long base;
                 if constexpr ((PK & PK_A) != 0) {
                     base = pack_row_fixed<kPackW4A8MStep>(a.pa, m0 + r, mul);
                 } else {
-                    base = static_cast<long long>(m0 + r) * a.lda;
+                    base = static_cast<long long>(m0) * a.lda +
+                           __umul24(r, static_cast<uint32_t>(a.lda));
                 }
                 a_chunk[j] = *reinterpret_cast<const i32x4 *>(
                     a.A + base +
@@ -238,7 +252,8 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
         if constexpr ((PK & PK_B) != 0) {
             w_rowp[h] = a.B + pack_row_fixed<kPackW4A8NStep>(a.pb, grow, w_mul[h]);
         } else {
-            w_rowp[h] = a.B + static_cast<long long>(grow) * a.bstride;
+            w_rowp[h] = a.B + static_cast<long long>(n0) * a.bstride +
+                        __umul24(grow - n0, static_cast<uint32_t>(a.bstride));
         }
     }
 
@@ -283,9 +298,11 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                     const int q = lane + 64 * j;
                     if (q < a_chunks) {
                         const int r = chunk_row(q);
-                        const int c = q - r * npw * 16;
-                        *reinterpret_cast<i32x4 *>(&s_a[r * npw * 256 + ((c ^ (r & 7)) << 4)]) =
-                            a_chunk[j];
+                        const int rn = static_cast<int>(__umul24(r, npw));
+                        const int c = q - rn * 16;
+                        // stored in the decoded weights' byte order (the MFMA operand as is)
+                        *reinterpret_cast<i32x4 *>(&s_a[rn * 256 + ((c ^ (r & 7)) << 4)]) =
+                            permute_act16(a_chunk[j]);
                     }
                 }
             }
@@ -312,7 +329,7 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                 if constexpr (kActInLds) {
                     if (a_real) {
                         const int c0 = ((pair - p_begin) * kPairK + h * 128 + fg * 32) >> 4;
-                        const int8_t *row = &s_a[fr * npw * kPairK];
+                        const int8_t *row = &s_a[__umul24(fr, npw) * kPairK];
                         v0 = *reinterpret_cast<const i32x4 *>(row + ((c0 ^ (fr & 7)) << 4));
                         v1 = *reinterpret_cast<const i32x4 *>(row + (((c0 + 1) ^ (fr & 7)) << 4));
                     } else {
@@ -324,7 +341,12 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
                     v1 = av[2 * pp + h][1];
                 }
                 i32x4 x0, x1, q0, q1;
-                permute_act(v0, v1, x0, x1);
+                if constexpr (kActInLds) {
+                    x0 = v0;  // staged in operand order already
+                    x1 = v1;
+                } else {
+                    permute_act(v0, v1, x0, x1);
+                }
                 if constexpr (kDirect) {
                     decode_w16(wr[2 * pp + h], q0, q1);
                 } else {
@@ -356,8 +378,9 @@ __global__ __launch_bounds__(kWaves * 64) void w4a8_mfma_kernel(W4A8Args a)
             tot += static_cast<uint32_t>(s_part[w * kPartStride][orow][ocol]);
             rs += static_cast<uint32_t>(s_part[w * kPartStride][rows][ocol]);
         }
-        const int gm = m0 + orow, gn = n0 + ocol;
-        store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn,
+        const int gn = n0 + ocol;
+        store_out<OUT>(a.D, static_cast<long long>(m0) * a.ldd +
+                                __umul24(orow, static_cast<uint32_t>(a.ldd)) + gn,
                        epilogue_f32(static_cast<int32_t>(tot) >> 4, static_cast<int32_t>(rs) >> 4,
                                     p_za, p_sa, p_sb, a.C ? &p_c : nullptr,
                                     a.bias ? &p_bias : nullptr, a.cmin, a.cmax));
@@ -460,8 +483,11 @@ void w4a8_run(size_t m, size_t n, size_t k, const void *A, size_t lda, size_t k_
         a.pb = make_pack(0, kPackW4A8Chunk, n, ldb / 2, k / 2, 0);
         layout_fast = (lda % 16 == 0) && ((ldb / 2) % 16 == 0);
     }
+    // (the fast kernel forms row offsets with 24-bit multiplies)
     const bool fast = (k % kPairK == 0) && k <= 65536 && layout_fast && aligned16(A) &&
-                      aligned16(B) && (m + kRowsPerChunk - 1) / kRowsPerChunk < 65536;
+                      aligned16(B) && (m + kRowsPerChunk - 1) / kRowsPerChunk < 65536 &&
+                      lda < (1u << 24) && ldb / 2 < (1u << 24) && ldc < (1u << 24) &&
+                      ldd < (1u << 24);
     if (fast) {
         const unsigned gx = static_cast<unsigned>((n + kNTile - 1) / kNTile);
         const unsigned long long gy = (m + kRowsPerChunk - 1) / kRowsPerChunk;
