@@ -577,17 +577,20 @@ __device__ __forceinline__ float out_bits_to_f32(uint32_t v)
 // weights, 16 x BPW f16 scales -- into a three-slot LDS ring of its own with direct global -> LDS
 // loads, three tiles ahead. No wave reads another wave's ring, so a wave starts a tile as soon as
 // its own loads of it have landed and refills the slot as soon as it has read it.
-// What bounds it: every CU takes in all of A (256 KiB at k 4096) besides its tiles, at some
-// 90 B/ns, and the CU serves its waves' requests about in issue order. So the first half of every
-// wave's A slice is requested first (all waves, then a meeting), then tile 0, then the second
-// halves: tile 0's first four blocks are computed while the second halves stream in.
+// What bounds it: every CU takes in all of A (256 KiB at k 4096) besides its tiles, and the CU
+// serves its waves' requests about group by group (four waves at a time), so the four wave
+// groups get their A slices microseconds apart. No wave therefore waits for another: each adds
+// its partials of a tile into that tile's f64 sums in LDS (ds_add_f64; the sum of 16 f32
+// partials is exact in f64, so the order of arrival does not change it) and counts itself in,
+// and goes on to its next tile; wave t finishes tile t (the f32 rounding of the sums, C, bias,
+// clamp, store) once all 16 have counted in. Waves 0-3 get their A first and finish their own
+// tiles first, so those epilogues overlap the slower waves' math. Every wave requests all of its
+// A before its tiles.
 // Plain weights: one load instruction takes 8 channels x 128 B (whole lines), lane i fetching
 // block (i & 7) ^ (c & 7) of channel c = i / 8, so block b of channel c lies at 16-byte slot
 // b ^ (c & 7) of the channel's 128 bytes and a wave's ds_read_b128 of one block for 16 channels
 // hits distinct slots; a whole packed panel's k-slice is contiguous (2 KiB) and is copied as it
-// lies. Per tile: the strip kernel's decode, v_mfma_f32_16x16x32_f16 per block and scale FMA;
-// then the 16 partials (ds_write_b128) meet in LDS and every thread sums 8 of one output's 16,
-// paired with the lane 32 above or below it.
+// lies. Per tile: the strip kernel's decode, v_mfma_f32_16x16x32_f16 per block and scale FMA.
 // ---------------------------------------------------------------------------------------------
 
 // unpack_q8_sgpr with one shift instead of three: nibbles 1, 3 (5, 7) are inserted at bits 4-7
@@ -639,15 +642,18 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     constexpr int NSLOT = 3;
     constexpr int NDW = WSLOT / 1024 + 1;     // loads per wave per tile
     constexpr int OUTS = kMRows * kNTile;     // outputs per tile
-    // floats per wave's partials: 4 past OUTS puts waves w and w + 8 32 banks apart
-    constexpr int PSTRIDE = OUTS + 4;
     static_assert(K == 2048 || K == 4096, "LDS strip kernel k");
     static_assert(kPackW4A16NStep == kNTile, "a packed weight panel is one tile");
-    static_assert(kMRows == 32 && kNTile == 16 && OUTS * 2 == NW * 64, "epilogue thread map");
+    static_assert(kMRows == 32 && kNTile == 16 && OUTS == 8 * 64, "8 outputs per lane per tile");
     static_assert(kStripTiles * kNTile == 64, "one bias per lane of wave 0");
     static_assert(NSLOT * NDW + BPW <= 23, "wait counts");
     __shared__ __attribute__((aligned(16))) int8_t s_ring[NW][NSLOT][SLOT];
-    __shared__ __attribute__((aligned(16))) float s_part[NW * PSTRIDE];
+    // A staging area of each wave (2 KiB, private)
+    __shared__ __attribute__((aligned(16))) int8_t s_stage[NW][2048];
+    // per tile of the strip: the 16 waves' partials summed in f64 (output (mt, r) of lane L at
+    // (4 mt + r) 64 + L: consecutive lanes, consecutive words) and how many waves added theirs
+    __shared__ __attribute__((aligned(16))) double s_acc[kStripTiles][OUTS];
+    __shared__ uint32_t s_arrived[kStripTiles];
     __shared__ float s_bias[kStripTiles * kNTile];
 
     const int tid = threadIdx.x;
@@ -661,6 +667,20 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     const int t_end = static_cast<int>((static_cast<long long>(blockIdx.x + 1) * a.ntiles) / nwg);
     const int ntl = t_end - t_begin;  // 1 .. kStripTiles
     const int npro = min(ntl, NSLOT);
+
+    // Zero the tiles' sums and arrival counts before any wave can add to them. The meeting comes
+    // before any load is issued: placed after them it would wait for the last wave's last issue,
+    // which the CU's address unit delays by microseconds while it takes every wave's loads.
+#pragma unroll
+    for (int i = tid; i < kStripTiles * OUTS; i += NW * 64) {
+        (&s_acc[0][0])[i] = 0.0;
+    }
+    if (tid < kStripTiles) {
+        s_arrived[tid] = 0u;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
     // A slice of this wave, loaded by asm so that the compiler adds no wait for it: the waits
     // below count these loads with the ring's (all of them in issue order).
@@ -726,19 +746,17 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
                  slot + WSLOT);
     };
 
-    // every wave's first half of A is requested before anyone's tile or second half
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    issue(0, 0);
+    // all of A before any tile: with no wave waiting for another, the last wave group's A is
+    // what the launch waits for
 #pragma unroll
     for (int j = HB; j < BPW; ++j) {
         load_a(j);
     }
-    for (int i = 1; i < npro; ++i) {
+    for (int i = 0; i < npro; ++i) {
         issue(i, i);
     }
-    // In flight, oldest first: A[0, HB) + bias, tile 0 (NDW), A[HB, BPW) (BPW loads), tiles
-    // 1 .. npro - 1. First half of A in:
+    // In flight, oldest first: A[0, HB) + bias, A[HB, BPW) (BPW loads), tiles 0 .. npro - 1.
+    // First half of A in:
     wait_vm_upto(npro * NDW + BPW);
 #pragma unroll
     for (int j = 0; j < HB; ++j) {
@@ -749,12 +767,12 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     }
     asm volatile("" : "+v"(rb));
     if (wave == 0) {
-        s_bias[lane] = out_bits_to_f32<OUT>(rb);  // read after the first tile's meeting
+        // read by the wave that finishes a tile, which counts itself in after wave 0 did
+        s_bias[lane] = out_bits_to_f32<OUT>(rb);
     }
     // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
-    // The wave's own partials area of s_part stages its A (no other wave touches it). The empty
-    // asm keeps the fragments as computed (no re-permutation inside the tile loop).
-    int8_t *stage = reinterpret_cast<int8_t *>(&s_part[wave * PSTRIDE]);
+    // The empty asm keeps the fragments as computed (no re-permutation inside the tile loop).
+    int8_t *stage = &s_stage[wave][0];
     f16x8 fa[BPW][2];
     a_slice_to_mfma<BPW, PK, 0, HB>(ra, fa, stage, lane);
 #pragma unroll
@@ -766,7 +784,7 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     }
     // the second half, once it is in (tile 0 only)
     auto second_half = [&]() {
-        wait_vm_upto((npro - 1) * NDW);
+        wait_vm_upto(npro * NDW);
 #pragma unroll
         for (int j = HB; j < BPW; ++j) {
 #pragma unroll
@@ -786,16 +804,25 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
 
-    // Epilogue map: lanes i and i + 32 (i < 32) of wave w own output row (w / 2) * 4 + i % 4,
-    // column (w % 2) * 8 + i / 4 of each tile, the lower lane summing waves 0-7's partials and the
-    // upper one waves 8-15's. A half-wave thus reads 32 consecutive floats of one wave's partials
-    // and the two halves' reads are 32 banks apart: no bank conflicts.
-    const int half = lane >> 5;
-    const int orow = (wave >> 1) * 4 + (lane & 3);
-    const int ocol = (wave & 1) * 8 + ((lane & 31) >> 2);
-    const int gm = mg0 + orow;
-    // the output's place in a wave's partials: (mt, lane fg * 16 + col, r) of the MFMA result
-    const int pidx = (orow >> 4) * 256 + (((orow >> 2) & 3) * 16 + ocol) * 4 + (orow & 3);
+    // This lane's outputs of a tile (MFMA layout): rows mt * 16 + fg * 4 + r, column fr. D and C
+    // are addressed through buffer resources based at this workgroup's first row and ending at
+    // its last row (the launcher keeps 32 rows of either under 2^31 bytes): a lane's offset is
+    // (fg * 4 * ld + column) elements, each output row adds a wave-uniform offset, and rows past
+    // m fall outside the resource (columns past n get an offset past it), so no output is
+    // guarded by a branch.
+    constexpr uint32_t kOutBytes = OUT == OUT_F32 ? 4u : 2u;
+    const uint32_t rows_here = static_cast<uint32_t>(min(kMRows, a.M - mg0));
+    const uint32_t d_bytes = rows_here * static_cast<uint32_t>(a.ldd) * kOutBytes;
+    const uint32_t c_bytes = rows_here * static_cast<uint32_t>(a.ldc) * kOutBytes;
+    const __amdgpu_buffer_rsrc_t d_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<uint8_t *>(a.D) + static_cast<long long>(mg0) * a.ldd * kOutBytes, 0,
+        static_cast<int>(d_bytes), 0x00020000);
+    const __amdgpu_buffer_rsrc_t c_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(a.C) == nullptr
+            ? static_cast<void *>(a.D)
+            : static_cast<uint8_t *>(const_cast<void *>(a.C)) +
+                  static_cast<long long>(mg0) * a.ldc * kOutBytes,
+        0, static_cast<int>(a.C ? c_bytes : 0u), 0x00020000);
 
     // One tile; tile 0 (FIRST, peeled off the loop) brings in the second half of A on the way.
     auto tile = [&](int tl, auto first) {
@@ -803,7 +830,7 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
         const int sl = tl % NSLOT;
         // this wave's loads of tile tl have landed (later ones may still be in flight; for tile
         // 0, the second half of A too)
-        wait_vm_upto(FIRST ? BPW + (npro - 1) * NDW : min(ntl - 1 - tl, NSLOT - 1) * NDW);
+        wait_vm_upto(FIRST ? (npro - 1) * NDW : min(ntl - 1 - tl, NSLOT - 1) * NDW);
         const int8_t *slot = &s_ring[wave][sl][0];
         const bool panel = packed_tile(t_begin + tl);
         f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -848,54 +875,86 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
             }
         }
         // this wave has read its slot (the MFMAs consumed it): refill it with the tile NSLOT
-        // ahead before meeting the other waves
+        // ahead
         if (tl + NSLOT < ntl) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             issue(tl + NSLOT, sl);
         }
-        if constexpr (!FIRST) {
-            // every thread has read the previous tile's partials
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-        }
+        // Add this wave's partials into the tile's f64 sums and count the wave in; no wave waits
+        // for another. The sums of the 16 f32 partials are exact in f64 (unless their exponents
+        // span more than 25 binades), so the order in which the waves add does not change them.
+        double *sum = &s_acc[tl][0];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            *reinterpret_cast<f32x4 *>(&s_part[wave * PSTRIDE + mt * 256 + lane * 4]) = acc[mt];
-        }
-        // partials written (LDS only: the ring's loads stay in flight across this barrier)
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        float v = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW / 2; ++w) {
-            v += s_part[(half * (NW / 2) + w) * PSTRIDE + pidx];
+            for (int r = 0; r < 4; ++r) {
+                __hip_atomic_fetch_add(&sum[(mt * 4 + r) * 64 + lane],
+                                       static_cast<double>(acc[mt][r]), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
         }
-        // half 0 + half 1: v_permlane32_swap on two copies of v leaves the lower half's sums in
-        // every lane of one register and the upper half's in the other (an f32 add gives the
-        // same bits either way round). Written as asm: the builtin with equal operands is folded
-        // as if its two results were equal.
-        uint32_t x0 = __builtin_bit_cast(uint32_t, v);
-        uint32_t x1 = x0;
-        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x0), "+v"(x1));
-        v = __builtin_bit_cast(float, x0) + __builtin_bit_cast(float, x1);
-        const int gn = (t_begin + tl) * kNTile + ocol;
-        if (half == 0 && gm < a.M && gn < a.N) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) {
+            __hip_atomic_fetch_add(&s_arrived[tl], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+    };
+    // Tile tl's outputs, once all 16 waves have added their partials: the sums rounded to f32
+    // once, then C, bias, clamp.
+    auto finish = [&](int tl) {
+        const double *sum = &s_acc[tl][0];
+        const int gn = (t_begin + tl) * kNTile + fr;
+        const float bias = a.bias ? s_bias[tl * kNTile + fr] : 0.f;
+        const bool col_ok = gn < a.N;
+        const uint32_t d_off = col_ok ? (static_cast<uint32_t>(fg * 4) * static_cast<uint32_t>(a.ldd) +
+                                         static_cast<uint32_t>(gn)) * kOutBytes
+                                      : d_bytes;
+        const uint32_t c_off = col_ok ? (static_cast<uint32_t>(fg * 4) * static_cast<uint32_t>(a.ldc) +
+                                         static_cast<uint32_t>(gn)) * kOutBytes
+                                      : c_bytes;
+        // all eight sums read at once (one LDS round trip), rounded to f32
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[e] = static_cast<float>(sum[e * 64 + lane]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t row = (e >> 2) * 16 + (e & 3);  // plus fg * 4 (in the lane offsets)
+            float x = v[e];
             if (a.C) {
-                v += load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
+                x += load_out_buf<OUT>(c_rsrc, c_off, row * static_cast<uint32_t>(a.ldc) * kOutBytes);
             }
             if (a.bias) {
-                v += s_bias[tl * kNTile + ocol];
+                x += bias;
             }
-            v = fmaxf(v, a.cmin);
-            v = fminf(v, a.cmax);
-            store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn, v);
+            x = fmaxf(x, a.cmin);
+            x = fminf(x, a.cmax);
+            store_out_buf<OUT>(d_rsrc, d_off, row * static_cast<uint32_t>(a.ldd) * kOutBytes, x);
         }
     };
     tile(0, std::true_type{});
 #pragma unroll 1
     for (int tl = 1; tl < ntl; ++tl) {
         tile(tl, std::false_type{});
+    }
+    // Wave w < ntl finishes tile w once the last wave has counted itself in. Waves 0-3 get their
+    // A first and finish their own tiles first, so the tiles' epilogues overlap the slower
+    // waves' math; only the last tile's stays on the path. Every wave counts itself in for every
+    // tile without waiting for anyone, so the wait ends; the iteration cap only bounds it.
+    if (wave < ntl) {
+        uint32_t in = 0;
+        for (int it = 0; it < (1 << 24); ++it) {
+            in = __hip_atomic_load(&s_arrived[wave], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (in == NW) {
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (in == NW) {
+            asm volatile("" ::: "memory");
+            finish(wave);
+        }
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_vm0(0));
 }
@@ -1003,8 +1062,10 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
     const bool fast = bl == 32 && k % 128 == 0 && k <= 128u * kWaves * kMaxGroupsPerWave &&
                       layout_fast && ldsb % 4 == 0 && aligned16(A) && aligned16(B) &&
                       (reinterpret_cast<uintptr_t>(scale_b) & 7u) == 0;
+    // (the strip kernels address 32 rows of D and C through 32-bit buffer offsets)
     const bool strip = bl == 32 && (k == 2048 || k == 3072 || k == 4096) && layout_fast &&
-                       ldsb % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(scale_b);
+                       ldsb % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(scale_b) &&
+                       ldd < (1ull << 24) && ldc < (1ull << 24);
     if (strip) {
         static int cus = device_cu_count();
         const long long need = (a.ntiles + kStripTiles - 1) / kStripTiles;

@@ -440,6 +440,46 @@ __device__ __forceinline__ void store_out(void *p, long long i, float v)
     }
 }
 
+// The same conversions through a raw buffer resource: element at byte offset voff + soff (soff
+// wave-uniform); an offset at or past the resource's num_records reads 0 / writes nothing.
+template <int OUT>
+__device__ __forceinline__ float load_out_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+{
+    if constexpr (OUT == OUT_F32) {
+        return __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff),
+                                                        static_cast<int>(soff), 0));
+    } else {
+        const uint16_t bits = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(voff),
+                                                                   static_cast<int>(soff), 0);
+        if constexpr (OUT == OUT_F16) {
+            return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+        } else {
+            return bf16_bits_to_f32(bits);
+        }
+    }
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_out_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                              float v)
+{
+    if constexpr (OUT == OUT_F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r,
+                                              static_cast<int>(voff), static_cast<int>(soff), 0);
+    } else {
+        uint16_t bits;
+        if constexpr (OUT == OUT_F16) {
+            const _Float16 h = static_cast<_Float16>(v);
+            bits = v != v ? static_cast<uint16_t>(0x7e00) : __builtin_bit_cast(uint16_t, h);
+        } else {
+            bits = f32_to_bf16_bits(v);
+        }
+        __builtin_amdgcn_raw_buffer_store_b16(bits, r, static_cast<int>(voff),
+                                              static_cast<int>(soff), 0);
+    }
+}
+
 // RISC-V vfmax / vfmin on f32 (IEEE 754-2019 maximumNumber / minimumNumber): a NaN operand
 // yields the other one (the canonical quiet NaN when both are NaN), and -0 orders below +0.
 __device__ __forceinline__ float rv_fmaxf(float a, float b)
