@@ -1,8 +1,10 @@
 // gemm_1xnbias_clamp_f16_f16_qsi4c2t (W4A16, block-quantized int4 weights) on gfx950.
 //
-// Two MFMA kernels share the math below: w4a16_regs_kernel (the strip kernel, for k in {2048,
-// 3072, 4096}: whole CUs, at most four tiles each, two tiles in flight) and w4a16_mfma_kernel
-// (any other k % 128 == 0, k <= 4096). In w4a16_mfma_kernel a workgroup of 8 wave64s owns a strip of
+// Three MFMA kernels share the math below: w4a16_lds_kernel (k 2048 and 4096: 16 waves per CU,
+// weights streamed through per-wave LDS rings, no per-tile meeting of the waves; see its own
+// comment), w4a16_regs_kernel (k 3072: whole CUs, at most four tiles each, two tiles in flight)
+// and w4a16_mfma_kernel (any other k % 128 == 0, k <= 4096). In w4a16_mfma_kernel a workgroup of
+// 8 wave64s owns a strip of
 // 16-channel weight tiles for one group of 32 activation rows. Wave w owns a fixed slice of k
 // (a run of 32-wide scale blocks) and keeps its slice of A (32 rows, f16) in registers for the
 // whole strip, so A is read from memory once per workgroup. For each 16-channel tile:
