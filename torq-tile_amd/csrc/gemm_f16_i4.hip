@@ -586,8 +586,8 @@ __device__ __forceinline__ float out_bits_to_f32(uint32_t v)
 // partials is exact in f64, so the order of arrival does not change it) and counts itself in,
 // and goes on to its next tile; wave t finishes tile t (the f32 rounding of the sums, C, bias,
 // clamp, store) once all 16 have counted in. Waves 0-3 get their A first and finish their own
-// tiles first, so those epilogues overlap the slower waves' math. Every wave requests all of its
-// A before its tiles.
+// tiles first, so those epilogues overlap the slower waves' math. Every wave requests the first
+// half of its A, tile 0, the second half, then its next tiles.
 // Plain weights: one load instruction takes 8 channels x 128 B (whole lines), lane i fetching
 // block (i & 7) ^ (c & 7) of channel c = i / 8, so block b of channel c lies at 16-byte slot
 // b ^ (c & 7) of the channel's 128 bytes and a wave's ds_read_b128 of one block for 16 channels
@@ -748,17 +748,18 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
                  slot + WSLOT);
     };
 
-    // all of A before any tile: with no wave waiting for another, the last wave group's A is
-    // what the launch waits for
+    // the first half of A, tile 0, the second half, then the next tiles: tile 0's first blocks
+    // compute while the second half lands
+    issue(0, 0);
 #pragma unroll
     for (int j = HB; j < BPW; ++j) {
         load_a(j);
     }
-    for (int i = 0; i < npro; ++i) {
+    for (int i = 1; i < npro; ++i) {
         issue(i, i);
     }
-    // In flight, oldest first: A[0, HB) + bias, A[HB, BPW) (BPW loads), tiles 0 .. npro - 1.
-    // First half of A in:
+    // In flight, oldest first: A[0, HB) + bias, tile 0 (NDW), A[HB, BPW) (BPW loads), tiles
+    // 1 .. npro - 1. First half of A in:
     wait_vm_upto(npro * NDW + BPW);
 #pragma unroll
     for (int j = 0; j < HB; ++j) {
@@ -786,7 +787,7 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     }
     // the second half, once it is in (tile 0 only)
     auto second_half = [&]() {
-        wait_vm_upto(npro * NDW);
+        wait_vm_upto((npro - 1) * NDW);
 #pragma unroll
         for (int j = HB; j < BPW; ++j) {
 #pragma unroll
@@ -832,7 +833,7 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
         const int sl = tl % NSLOT;
         // this wave's loads of tile tl have landed (later ones may still be in flight; for tile
         // 0, the second half of A too)
-        wait_vm_upto(FIRST ? (npro - 1) * NDW : min(ntl - 1 - tl, NSLOT - 1) * NDW);
+        wait_vm_upto(FIRST ? BPW + (npro - 1) * NDW : min(ntl - 1 - tl, NSLOT - 1) * NDW);
         const int8_t *slot = &s_ring[wave][sl][0];
         const bool panel = packed_tile(t_begin + tl);
         f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
