@@ -5,7 +5,10 @@ of the reference igemmcl (tqto_igemmcl_qsi8cxt, pinned in test_oracle.py as im2c
 
 Cases: strides, paddings and dilations in every dimension, a 3-D kernel, partial row and
 column tiles, two groups with the second group selected, the reference's m_step tiling with
-m_idx (a ragged last tile), and plain and packed weights."""
+m_idx (a ragged last tile), and plain and packed weights. The plain-weight 3 x 3 stride-1
+"same" cases with 128 channels per group (case 0, the grouped case, the tiled calls, cfg 5
+plain) are served by the halo kernel instead (test_gpu_conv_halo.py); their packed twins still
+take the streaming kernel."""
 
 import ctypes
 

@@ -9,17 +9,20 @@
 //   igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8   (B gathered from an NCDHW image)
 // and their packed siblings.
 //
-// Three kernels, chosen per call:
-//   * int8_stream_kernel (plain A, B = [n, k], k % 128 == 0: W8A8 at its config; igemmcl when
-//     the group channel count is a multiple of 128): 8 wave64s, a 4-deep ring of LDS stages
-//     filled by direct global->LDS loads, v_mfma_i32_32x32x32_i8, XCD-aware tile order
-//     (described at the kernel);
+// Four kernels, chosen per call:
+//   * conv_halo_kernel (igemmcl, plain weights, 3 x 3 "same" convolution with stride 1 and 128
+//     channels per group: the benchmark's): each workgroup loads the input rows its 256 output
+//     pixels touch into LDS once and forms the nine taps from them (described at the kernel);
+//   * int8_stream_kernel (plain A, B = [n, k], k % 128 == 0: W8A8 at its config; the other
+//     igemmcl geometries whose group channel count is a multiple of 128): 8 wave64s, a 4-deep
+//     ring of LDS stages filled by direct global->LDS loads, v_mfma_i32_32x32x32_i8, XCD-aware
+//     tile order (described at the kernel);
 //   * int8_mfma_kernel (igemmcl, the other 16-byte-aligned shapes, clamp_i32's [k, n] B): 256 threads
 //     (4 wave64s in a 2x2 grid) on a BM x 128 tile, k in steps of 64 bytes through double-buffered
 //     LDS tiles, v_mfma_i32_16x16x64_i8;
 //   * int8_generic_kernel: one thread per output for unaligned pointers or strides, k not a
 //     multiple of 16, or channel counts not a multiple of 16.
-// All three accumulate exactly in int32 and fuse the epilogue (C, bias, requantization,
+// All four accumulate exactly in int32 and fuse the epilogue (C, bias, requantization,
 // saturation, clamp) into the store.
 #include <type_traits>
 
@@ -1377,6 +1380,411 @@ void launch_stream(const Int8Args &a, hipStream_t stream)
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Implicit convolution through an LDS input halo (igemmcl with plain weights; 2-D: one depth tap,
+// depth stride 1, no depth padding; 3 x 3 taps, stride 1, dilation 1, padding 1 in h and w, so
+// OH = IH and OW = IW; 128 channels per group).
+//
+// Output pixels are numbered row by row through the depth (batch) axis. With these geometries
+// "stacked" output row R = od * OH + oh reads stacked input rows R - 1 .. R + 1 (input row
+// od * IH + ih), so a tile of 256 consecutive pixels spanning stacked output rows R0 .. R1 reads
+// stacked input rows R0 - 1 .. R1 + 1 only: the tile's halo, NR rows of IW + 2 pixels (the two
+// border columns, and rows outside the input, zero) at a row pitch HC >= IW + 2 (below). A tap
+// whose input row belongs to the previous or next image (the padding row between images) reads
+// a zero line instead of the halo row. Every input byte a tile needs is loaded into LDS once: at
+// the benchmark geometry (56 x 56 x 128, 256 x 64 tiles) 58 KiB of halo and 72 KiB of weights per
+// workgroup, against 288 KiB of per-tap rows and weights for the streaming kernel's 128 x 128
+// tiles.
+//
+// Every load moves whole 128-byte lines (a pixel's 128 channels, or one tap's 128 channels of a
+// weight row): the memory system moves whole lines, so a split of each line over several stages
+// would fetch it once per stage. The k loop therefore runs tap by tap, in stages of one kernel
+// row (3 taps). The epilogue inputs and the whole halo are requested first, then each tap's
+// weights (64 rows x 128 bytes: one 1 KiB block per wave), kHaloAhead stages ahead of the compute:
+// every wave has the same loads outstanding behind each stage, so each stage's wait is a constant
+// vmcnt (runtime counts would need a compare-and-branch tree of waits per stage: measured 3x
+// slower), and stage 0 waits for the halo as well. Everything stays resident (no buffer is
+// reused): no barrier other than each stage's arrival. A tap is 4 MFMA k-steps (32 channels
+// each); a stage's 12 k-steps run as one software pipeline.
+//
+// MFMA operands: the weights are the 32-row operand and the pixels the 32-column operand, so the
+// accumulator of a lane is one pixel (its column) and 16 channels in four runs of four consecutive
+// channels (rows 8 g + 4 h + e): the epilogue writes 4 requantized channels per dword store.
+//
+// LDS: a pixel (or weight row) is 8 units of 16 bytes; chunk c of pixel q sits in unit
+// 8 q + (c ^ ((q >> 1) & 7)), so any 16 consecutive pixels (or weight rows) a ds_read_b128 pass
+// reads fall in 16 distinct 16-byte slots modulo 256 bytes: no bank conflicts (the halo pitch
+// keeps consecutive output pixels consecutive modulo 16 across a row change where the halo still
+// fits that way; counters: 416 conflict cycles per launch against 190 K). Loads are LDS-DMA:
+// a load block fills 1 KiB (64 lanes x 16 bytes, 8 pixels) in lane order, each lane fetching the
+// global chunk its position holds; 8 consecutive lanes read one pixel's 128 bytes.
+constexpr int kHaloPix = 256;               // output pixels per workgroup
+constexpr int kHaloCh = 64;                 // output channels per workgroup
+constexpr int kHaloTaps = 9;                // 3 x 3
+constexpr int kHaloWBlocks = 8;             // 1 KiB weight load blocks per tap (64 x 128 B)
+constexpr int kHaloLdsBytes = 152 * 1024;   // halo + weights + a zero line
+constexpr int kHaloTPS = 3;                 // taps per stage (one kernel row)
+constexpr int kHaloStages = kHaloTaps / kHaloTPS;
+constexpr int kHaloAhead = 2;               // stages in flight ahead of the one computed
+constexpr int kHaloReadAhead = 2;           // k-steps of operands read ahead of the MFMAs
+
+struct HaloPlan
+{
+    int HC;       // halo row pitch in pixels (>= IW + 2; the pixels past IW + 1 zero)
+    int NRHC;     // halo pixels (NR rows)
+    int HB;       // halo blocks
+    int b_bytes;  // bytes of B from its base through the last weight byte
+    int tiles_c;  // 64-channel tiles
+    int tiles;    // workgroups with work
+    int per_xcd;  // tiles per XCD (grid = 8 per_xcd)
+};
+
+// Raw buffer resource (stride 0, 32-bit dwords format): offsets at or past num_records read zeros.
+__device__ __forceinline__ i32x4 raw_rsrc(const void *base, int num_records)
+{
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    i32x4 r;
+    r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(b & 0xffffffffu));
+    r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((b >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane(num_records);
+    r[3] = 0x00020000;
+    return r;
+}
+
+__global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, HaloPlan hp)
+{
+    __shared__ __attribute__((aligned(128))) int8_t lds[kHaloLdsBytes];
+    __shared__ __attribute__((aligned(16))) int32_t s_mult[kHaloCh];
+    __shared__ __attribute__((aligned(16))) int32_t s_shift[kHaloCh];
+    __shared__ __attribute__((aligned(16))) int32_t s_bias[kHaloCh];
+    __shared__ __attribute__((aligned(16))) float s_sb[kHaloCh];
+
+    const int t = (blockIdx.x & 7) * hp.per_xcd + (blockIdx.x >> 3);
+    if (t >= hp.tiles) {
+        return;
+    }
+    // the two channel tiles of a pixel tile are neighbours in t, so they run on one XCD and
+    // share the halo through its L2
+    const int tile_c = t % hp.tiles_c;
+    const int m0 = (t / hp.tiles_c) * kHaloPix;
+    const int n0 = tile_c * kHaloCh;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const ConvGeom &g = a.cv;
+    const int w_base = hp.HB * 1024;                     // weights: 9 taps x 8 blocks
+    const int zero_base = w_base + kHaloTaps * kHaloWBlocks * 1024;  // 128 zero bytes
+
+    // Epilogue inputs (the 64 channels' weight scales and biases; channels past N repeat the
+    // last, and are not stored) by LDS-DMA ahead of everything else: the first stage's wait
+    // covers them, and the compiler places no wait of its own for them.
+    if (wave == 0) {
+        const int ch = min(n0 + lane, a.N - 1);
+        dma_lds4(a.scale_b + (a.quant_channel_b == 1 ? 0 : ch), reinterpret_cast<int8_t *>(s_sb));
+        if (a.bias) {
+            dma_lds4(a.bias + ch, reinterpret_cast<int8_t *>(s_bias));
+        } else {
+            s_bias[lane] = 0;
+        }
+    }
+    if (tid < 8) {
+        *reinterpret_cast<i32x4 *>(lds + zero_base + 16 * tid) = i32x4{0, 0, 0, 0};
+    }
+
+    // p0 + M < 2^31 on this path (launcher): 32-bit unsigned divisions
+    const uint32_t OW = static_cast<uint32_t>(g.OW);
+    const uint32_t IH = static_cast<uint32_t>(g.IH);
+    const int R0 = static_cast<int>((static_cast<uint32_t>(a.p0) + static_cast<uint32_t>(m0)) / OW);
+    const int nrows = g.ID * g.IH;  // stacked input rows
+    const i32x4 a_rsrc = raw_rsrc(a.A, a.conv_bytes);
+    const i32x4 b_rsrc = raw_rsrc(a.B, hp.b_bytes);
+    const int slot = lane & 7;
+    const int sub = lane >> 3;  // pixel (weight row) of a block this lane's 8-lane group reads
+
+    // The halo: blocks wave, wave + 8, ... (8 pixels each); pixels past the halo's NR rows,
+    // border columns and rows outside the input read zeros (offset past the resource). A lane's
+    // pixel advances by 64 per block: its halo row, column and input offset step by uniform
+    // amounts (one wrap at most: 64 mod HC < HC), so the loop needs no division or multiply.
+    {
+        const int q0 = wave * 8 + sub;
+        int jr = q0 / hp.HC;
+        int col = q0 - jr * hp.HC;
+        const int djr = 64 / hp.HC;
+        const int dcol = 64 - djr * hp.HC;
+        // input offset of (row R0 - 1 + jr, column col - 1): row-major pixels, IC bytes each
+        int off = ((R0 - 1 + jr) * g.IW + col - 1) * g.IC + (slot ^ ((q0 >> 1) & 7)) * 16;
+        const int doff = (djr * g.IW + dcol) * g.IC;
+        const int wrap = (g.IW - hp.HC) * g.IC;  // a row wrap: HC pixels back, IW forward
+        for (int hb = wave; hb < hp.HB; hb += 8) {
+            const int G = R0 - 1 + jr;
+            const bool in = hb * 8 + sub < hp.NRHC && G >= 0 && G < nrows && col >= 1 &&
+                            col <= g.IW;
+            dma_lds16_buf(a_rsrc, in ? off : a.conv_bytes, lds + hb * 1024);
+            jr += djr;
+            col += dcol;
+            off += doff;
+            if (col >= hp.HC) {
+                col -= hp.HC;
+                ++jr;
+                off += wrap;
+            }
+        }
+    }
+    // Weights: block `wave` of tap t is rows 8 wave .. 8 wave + 7 of the tile's 64, tap t's 128
+    // channels (bytes 128 t of the row).
+    const int w_nr = wave * 8 + sub;
+    const int w_off = min(n0 + w_nr, a.N - 1) * static_cast<int>(a.ldb) +
+                      (slot ^ ((w_nr >> 1) & 7)) * 16;
+    auto issue_w = [&](int tp) {
+        dma_lds16_buf(b_rsrc, w_off + tp * g.ICg, lds + w_base + (tp * kHaloWBlocks + wave) * 1024);
+    };
+    auto issue_stage = [&](int st) {
+#pragma unroll
+        for (int tt = 0; tt < kHaloTPS; ++tt) {
+            issue_w(st * kHaloTPS + tt);
+        }
+    };
+
+    // Compute roles: wave (wc = wave >> 2, wp = wave & 3) computes channels 32 wc .. 32 wc + 31
+    // x pixels 64 wp .. 64 wp + 63 of the tile (1 x 2 fragments) over the four k-steps of every
+    // tap; the two waves of a SIMD (w and w + 4) hold the two channel halves. Lane (r32, h)
+    // supplies row / column r32 and channel half h of each 32-channel k-step (chunk 2 k + h of
+    // the 8).
+    constexpr int KPW = 4;  // k-steps per tap
+    constexpr int RW = 1;   // 32-channel fragments per wave
+    constexpr int RP = 2;   // 32-pixel fragments per wave
+    const int wp = wave & 3;
+    const int jbase = wave >> 2;
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+    // the lane's unit of k-step k is (address ^ 32 k): the XOR touches chunk bits 5..6 only
+    int w_addr[RW];  // + 8192 tap
+#pragma unroll
+    for (int jj = 0; jj < RW; ++jj) {
+        const int nr = (jbase + jj) * 32 + r32;
+        w_addr[jj] = w_base + nr * 128 + ((16 * h) ^ (16 * ((nr >> 1) & 7)));
+    }
+    // per fragment: the halo pixel of tap (0, 0), and whether the top / bottom kernel rows lie in
+    // this pixel's image
+    int qb[RP];
+    bool ok_top[RP], ok_bot[RP];
+#pragma unroll
+    for (int i = 0; i < RP; ++i) {
+        const int pl = min(m0 + wp * 64 + 32 * i + r32, a.M - 1);  // rows past M: any valid pixel
+        const uint32_t p = static_cast<uint32_t>(a.p0) + static_cast<uint32_t>(pl);
+        const uint32_t R = p / OW;
+        const int ow = static_cast<int>(p - R * OW);
+        const int oh = static_cast<int>(R % IH);
+        qb[i] = (static_cast<int>(R) - R0) * hp.HC + ow;
+        ok_top[i] = oh > 0;
+        ok_bot[i] = oh + 1 < g.IH;
+    }
+
+    i32x16 acc[RW][RP];  // [channel fragment][pixel fragment]
+#pragma unroll
+    for (int jj = 0; jj < RW; ++jj) {
+#pragma unroll
+        for (int i = 0; i < RP; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[jj][i][r] = 0;
+            }
+        }
+    }
+#pragma unroll
+    for (int st = 0; st < kHaloAhead; ++st) {
+        issue_stage(st);
+    }
+#pragma unroll
+    for (int st = 0; st < kHaloStages; ++st) {
+        // this wave's loads up to stage st's weights have landed once at most the weight blocks
+        // issued after them are outstanding (the epilogue inputs and the halo were requested
+        // first); then every wave's have, after the barrier (the LDS stores of the zero line
+        // and of a null bias too: lgkmcnt(0))
+        const int later = kHaloTPS * min(kHaloAhead - 1, kHaloStages - 1 - st);
+        static_assert(kHaloTPS * (kHaloAhead - 1) <= 8, "wait counts below");
+        if (later == 8) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(8));
+        } else if (later == 6) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(6));
+        } else if (later == 4) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(4));
+        } else if (later == 3) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(3));
+        } else if (later == 2) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2));
+        } else if (later == 1) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(1));
+        } else {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (st + kHaloAhead < kHaloStages) {
+            issue_stage(st + kHaloAhead);
+        }
+        // pixel operand addresses of the stage's taps (a padding-row tap reads the zero line)
+        int pa[kHaloTPS][RP];
+#pragma unroll
+        for (int tt = 0; tt < kHaloTPS; ++tt) {
+            const int s = st * kHaloTPS + tt;
+            const int kh = s / 3;
+            const int tap_q = kh * hp.HC + (s - 3 * kh);
+#pragma unroll
+            for (int i = 0; i < RP; ++i) {
+                const int q = qb[i] + tap_q;
+                const bool ok = kh == 0 ? ok_top[i] : kh == 2 ? ok_bot[i] : true;
+                pa[tt][i] = ok ? q * 128 + ((16 * h) ^ (16 * ((q >> 1) & 7))) : zero_base + 16 * h;
+            }
+        }
+        // the stage's k-steps (its taps' KPW steps each) as one pipeline: the operands of step
+        // u + 1 are read between the MFMAs of step u
+        constexpr int NSTEP = kHaloTPS * KPW;
+        i32x4 fw[NSTEP][RW], fp[NSTEP][RP];
+#pragma unroll
+        for (int u = 0; u < NSTEP; ++u) {
+            const int tt = u / KPW;
+            const int kx = 32 * (u % KPW);
+#pragma unroll
+            for (int jj = 0; jj < RW; ++jj) {
+                fw[u][jj] = *reinterpret_cast<const i32x4 *>(
+                    lds + ((w_addr[jj] + (st * kHaloTPS + tt) * 8192) ^ kx));
+            }
+#pragma unroll
+            for (int i = 0; i < RP; ++i) {
+                fp[u][i] = *reinterpret_cast<const i32x4 *>(lds + (pa[tt][i] ^ kx));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NSTEP; ++u) {
+#pragma unroll
+            for (int jj = 0; jj < RW; ++jj) {
+#pragma unroll
+                for (int i = 0; i < RP; ++i) {
+                    acc[jj][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[u][jj], fp[u][i],
+                                                                       acc[jj][i], 0, 0, 0);
+                }
+            }
+        }
+        // reads run kHaloReadAhead steps ahead of the MFMAs: one step's MFMAs of the two waves of
+        // a SIMD (128 cycles) are shorter than an LDS read's latency under this load
+        __builtin_amdgcn_sched_group_barrier(0x100, (RW + RP) * kHaloReadAhead, 0);
+#pragma unroll
+        for (int u = 0; u < NSTEP; ++u) {
+            if (u + kHaloReadAhead < NSTEP) {
+                __builtin_amdgcn_sched_group_barrier(0x100, RW + RP, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, RW * RP, 0);
+        }
+        if (st == 1 && wave == 0) {
+            // the channels' requantization multipliers, while this stage's MFMAs run
+            int32_t mult, shift;
+            column_multiplier_val(a.scale_a, s_sb[lane], a.scale_d, mult, shift);
+            s_mult[lane] = mult;
+            s_shift[lane] = shift;
+        }
+    }
+
+    static_assert(kHaloStages >= 2, "the multipliers are computed in stage 1");
+    __syncthreads();  // the multipliers in LDS
+
+    // Epilogue: lane holds pixel m0 + 64 wp + 32 i + r32 and channels n0 + cb + 8 g + e.
+    const int cb = jbase * 32 + 4 * h;
+    i32x4 em[4], es[4], eb[4];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+        em[gq] = *reinterpret_cast<const i32x4 *>(&s_mult[cb + 8 * gq]);
+        es[gq] = *reinterpret_cast<const i32x4 *>(&s_shift[cb + 8 * gq]);
+        eb[gq] = *reinterpret_cast<const i32x4 *>(&s_bias[cb + 8 * gq]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int pl = m0 + wp * 64 + 32 * i + r32;
+        if (pl >= a.M) {
+            continue;
+        }
+        int8_t *drow = static_cast<int8_t *>(a.D) + (a.d_row0 + pl) * a.ldd + n0 + cb;
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t v =
+                    static_cast<uint32_t>(acc[0][i][4 * gq + e]) + static_cast<uint32_t>(eb[gq][e]);
+                const int8_t q = requant_dev(static_cast<int32_t>(v), em[gq][e], es[gq][e], a.zp_d,
+                                             a.cmin, a.cmax);
+                packed |= static_cast<uint32_t>(static_cast<uint8_t>(q)) << (8 * e);
+            }
+            const int ch = n0 + cb + 8 * gq;
+            if (ch + 3 < a.N) {
+                *reinterpret_cast<uint32_t *>(drow + 8 * gq) = packed;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (ch + e < a.N) {
+                        drow[8 * gq + e] = static_cast<int8_t>(packed >> (8 * e));
+                    }
+                }
+            }
+        }
+    }
+}
+
+// The halo kernel's plan for this call, or false when its geometry or sizes do not fit it.
+bool halo_plan(const Int8Args &a, HaloPlan &hp)
+{
+    const ConvGeom &g = a.cv;
+    if (g.KD != 1 || g.PD != 0 || g.SD != 1 || g.KH != 3 || g.KW != 3 || g.SH != 1 || g.SW != 1 ||
+        g.DH != 1 || g.DW != 1 || g.PH != 1 || g.PW != 1 || g.OH != g.IH || g.OW != g.IW) {
+        return false;
+    }
+    if (g.ICg != 128 || a.conv_bytes <= 0) {
+        return false;
+    }
+    // dword stores of 4 channels; pixel offsets of a tile and the B offsets fit 31 bits
+    if ((reinterpret_cast<uintptr_t>(a.D) & 3u) != 0 || a.ldd % 4 != 0 ||
+        static_cast<long long>(kHaloPix) * a.ldd >= (1ll << 31)) {
+        return false;
+    }
+    const long long b_bytes = static_cast<long long>(a.N - 1) * a.ldb + a.K;
+    if (a.ldb < a.K || b_bytes >= (1ll << 31)) {
+        return false;
+    }
+    const long long RS = (g.OW - 1 + kHaloPix - 1) / g.OW + 1;  // most output rows per tile
+    // Row pitch: with pitch = OW modulo 16, the 16 consecutive output pixels of a ds_read_b128
+    // pass sit at 16 consecutive halo pixels modulo 16 across a change of output row too (no
+    // bank conflict; with pitch IW + 2 such a pass puts two pairs of lanes on one slot). Taken
+    // when the halo still fits; IW + 2 otherwise.
+    const long long HCmin = static_cast<long long>(g.IW) + 2;
+    const long long HCcf = HCmin + ((g.OW - HCmin) & 15);
+    auto fits = [&](long long hc) {
+        return ((RS + 2) * hc + 7) / 8 + kHaloTaps * kHaloWBlocks <= (kHaloLdsBytes - 128) / 1024;
+    };
+    const long long HC = fits(HCcf) ? HCcf : HCmin;
+    if (!fits(HC)) {
+        return false;
+    }
+    const long long NRHC = (RS + 2) * HC;
+    const long long HB = (NRHC + 7) / 8;
+    // stacked row indices and halo offsets in 32 bits
+    if (static_cast<long long>(g.ID) * g.IH >= (1ll << 30) || a.p0 + a.M >= (1ll << 31)) {
+        return false;
+    }
+    hp.HC = static_cast<int>(HC);
+    hp.NRHC = static_cast<int>(NRHC);
+    hp.HB = static_cast<int>(HB);
+    hp.b_bytes = static_cast<int>(b_bytes);
+    hp.tiles_c = (a.N + kHaloCh - 1) / kHaloCh;
+    const long long tiles = static_cast<long long>((a.M + kHaloPix - 1) / kHaloPix) * hp.tiles_c;
+    if (tiles >= (1ll << 30)) {
+        return false;
+    }
+    hp.tiles = static_cast<int>(tiles);
+    hp.per_xcd = static_cast<int>((tiles + 7) / 8);
+    return true;
+}
+
 template <int AM, int BMd, int EPI, int PK = PK_NONE>
 void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *where)
 {
@@ -1389,6 +1797,15 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
     if constexpr (BMd == B_NK && AM == A_MATRIX) {
         if (fast && a.K % kSK == 0 && stream_offsets_fit(a, EPI == EPI_CLAMP_I32 ? 4 : 1)) {
             launch_stream<EPI, PK>(a, stream);
+            check_launch(where);
+            return;
+        }
+    }
+    if constexpr (BMd == B_NK && AM == A_CONV_CL && EPI == EPI_REQUANT_I8 && PK == PK_NONE) {
+        HaloPlan hp;
+        if (fast && halo_plan(a, hp)) {
+            hipLaunchKernelGGL(conv_halo_kernel, dim3(8 * hp.per_xcd), dim3(kStreamThreads), 0,
+                               stream, a, hp);
             check_launch(where);
             return;
         }
