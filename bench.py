@@ -420,6 +420,8 @@ def leg_of_kernel(name):
         return "w4a8"
     if "w4a16_" in name:
         return "w4a16"
+    if "conv_halo_kernel" in name:
+        return "conv"
     if "int8_stream_kernel<" in name or "igemm" in name:
         # int8_stream_kernel<BM, EPI, PK, conv>: the convolution mode has conv = true
         head = name.split(">")[0].rstrip()

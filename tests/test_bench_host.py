@@ -1,0 +1,26 @@
+"""Host logic of bench.py that needs no GPU: which bench leg each product kernel's counters are
+attributed to (the HBM traffic and counter summaries sum per leg by demangled kernel name)."""
+
+import os
+import sys
+
+import pytest
+
+sys.path.insert(0, os.path.join(os.path.dirname(__file__), ".."))
+import bench  # noqa: E402
+
+NS = "tqt::(anonymous namespace)::"
+
+
+@pytest.mark.parametrize("name,leg", [
+    ("void %sconv_halo_kernel(%sInt8Args, %sHaloPlan)" % (NS, NS, NS), "conv"),
+    ("void %sint8_stream_kernel<128, 1, 0, true>(%sInt8Args, int, int, int)" % (NS, NS), "conv"),
+    ("void %sint8_stream_kernel<64, 1, 0, false>(%sInt8Args, int, int, int)" % (NS, NS), "w8a8"),
+    ("void %sw4a8_mfma_kernel<1, 0, 0>(%sW4A8Args)" % (NS, NS), "w4a8"),
+    ("void %sw4a16_lds_kernel<4096, 0, 1>(%sW4A16Args, int)" % (NS, NS), "w4a16"),
+    ("void at::native::vectorized_elementwise_kernel<4, at::native::bitwise_not_kernel_cuda>",
+     "copy"),
+    ("void %squantize_qai8dx_kernel(float const*)" % NS, None),
+])
+def test_leg_of_kernel(name, leg):
+    assert bench.leg_of_kernel(name) == leg
