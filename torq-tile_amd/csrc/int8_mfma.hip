@@ -1698,6 +1698,8 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
         es[gq] = *reinterpret_cast<const i32x4 *>(&s_shift[cb + 8 * gq]);
         eb[gq] = *reinterpret_cast<const i32x4 *>(&s_bias[cb + 8 * gq]);
     }
+    // Four requantized channels go into one dword with two byte permutes and an OR.
+    const int32_t lo = min(a.cmin, a.cmax);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int pl = m0 + wp * 64 + 32 * i + r32;
@@ -1707,15 +1709,17 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
         int8_t *drow = static_cast<int8_t *>(a.D) + (a.d_row0 + pl) * a.ldd + n0 + cb;
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
-            uint32_t packed = 0;
+            uint32_t y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t v =
-                    static_cast<uint32_t>(acc[0][i][4 * gq + e]) + static_cast<uint32_t>(eb[gq][e]);
-                const int8_t q = requant_dev(static_cast<int32_t>(v), em[gq][e], es[gq][e], a.zp_d,
-                                             a.cmin, a.cmax);
-                packed |= static_cast<uint32_t>(static_cast<uint8_t>(q)) << (8 * e);
+                const uint32_t v = static_cast<uint32_t>(acc[0][i][4 * gq + e]) +
+                                   static_cast<uint32_t>(eb[gq][e]);
+                y[e] = static_cast<uint32_t>(requant_clamped_dev(
+                    static_cast<int32_t>(v), em[gq][e], es[gq][e], a.zp_d, lo, a.cmax));
             }
+            // v_perm_b32 byte k of {S0, S1} (S1 bytes 0-3): low bytes of y0, y1 | y2, y3
+            const uint32_t packed = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u) |
+                                    __builtin_amdgcn_perm(y[3], y[2], 0x04000c0cu);
             const int ch = n0 + cb + 8 * gq;
             if (ch + 3 < a.N) {
                 *reinterpret_cast<uint32_t *>(drow + 8 * gq) = packed;

@@ -517,20 +517,26 @@ __device__ __forceinline__ float rv_fminf(float a, float b)
 // [-128, 127] followed by max(., cmin) and min(., cmax) equals max(., min(cmin, cmax)) followed
 // by min(., cmax), which also covers cmin > cmax (every output is cmax); the first of those is
 // uniform, so two operations per output remain.
-__device__ __forceinline__ int8_t requant_dev(int32_t acc, int32_t mult, int32_t shift,
-                                              int32_t zp, int32_t cmin, int32_t cmax)
+// The same output before its int8 truncation: an int32 in [lo, cmax], lo = min(cmin, cmax).
+__device__ __forceinline__ int32_t requant_clamped_dev(int32_t acc, int32_t mult, int32_t shift,
+                                                       int32_t zp, int32_t lo, int32_t cmax)
 {
     int32_t y = __mulhi(acc, mult);  // high 32 bits of the signed 64-bit product
     y = y >> (shift & 31);
     y = static_cast<int32_t>(static_cast<uint32_t>(y) + static_cast<uint32_t>(zp));
-    // max(y, min(cmin, cmax)) then min(., cmax): with lo <= cmax that is the median of the three
-    const int32_t lo = min(cmin, cmax);
+    // max(y, lo) then min(., cmax): with lo <= cmax that is the median of the three
 #if defined(__HIP_DEVICE_COMPILE__)
     asm("v_med3_i32 %0, %1, %2, %3" : "=v"(y) : "v"(y), "v"(lo), "v"(cmax));
 #else
     y = min(max(y, lo), cmax);
 #endif
-    return static_cast<int8_t>(y);
+    return y;
+}
+
+__device__ __forceinline__ int8_t requant_dev(int32_t acc, int32_t mult, int32_t shift,
+                                              int32_t zp, int32_t cmin, int32_t cmax)
+{
+    return static_cast<int8_t>(requant_clamped_dev(acc, mult, shift, zp, min(cmin, cmax), cmax));
 }
 
 }  // namespace tqt
