@@ -1511,15 +1511,19 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
         int col = q0 - jr * hp.HC;
         const int djr = 64 / hp.HC;
         const int dcol = 64 - djr * hp.HC;
-        // input offset of (row R0 - 1 + jr, column col - 1): row-major pixels, IC bytes each
-        int off = ((R0 - 1 + jr) * g.IW + col - 1) * g.IC + (slot ^ ((q0 >> 1) & 7)) * 16;
-        const int doff = (djr * g.IW + dcol) * g.IC;
-        const int wrap = (g.IW - hp.HC) * g.IC;  // a row wrap: HC pixels back, IW forward
+        // input offset of (row R0 - 1 + jr, column col - 1): row-major pixels, IC bytes each;
+        // unsigned (wrapping) arithmetic: outside the input (row -1, rows past the last, the
+        // border columns) the value is not used, and where it is used it is below 2^31
+        uint32_t off = static_cast<uint32_t>(((R0 - 1 + jr) * g.IW + col - 1) * g.IC) +
+                       static_cast<uint32_t>((slot ^ ((q0 >> 1) & 7)) * 16);
+        const uint32_t doff = static_cast<uint32_t>((djr * g.IW + dcol) * g.IC);
+        // a row wrap: HC pixels back, IW forward
+        const uint32_t wrap = static_cast<uint32_t>((g.IW - hp.HC) * g.IC);
         for (int hb = wave; hb < hp.HB; hb += 8) {
             const int G = R0 - 1 + jr;
             const bool in = hb * 8 + sub < hp.NRHC && G >= 0 && G < nrows && col >= 1 &&
                             col <= g.IW;
-            dma_lds16_buf(a_rsrc, in ? off : a.conv_bytes, lds + hb * 1024);
+            dma_lds16_buf(a_rsrc, in ? static_cast<int>(off) : a.conv_bytes, lds + hb * 1024);
             jr += djr;
             col += dcol;
             off += doff;
