@@ -4,6 +4,9 @@ its 256 output pixels touch once into LDS and forms the nine taps from them), bi
 oracle's restatement of the reference igemmcl (tqto_igemmcl_qsi8cxt, pinned in test_oracle.py as
 im2col + GEMM).
 
+Plain weights and the packed sibling (igemmcl...qsi8cxp: 128-row panels, 16-byte chunks
+chunk-major; a partial last panel in the tiled-call test) through the same cases.
+
 Cases: the bank-conflict-free halo row pitch (rows long enough for it to fit) and the plain pitch
 IW + 2; images smaller than a tile, so one tile crosses many image boundaries (the padding rows
 between images), down to one-row images; a wide image near the halo's size limit, and one too wide
@@ -54,8 +57,9 @@ def m_all(conv):
 
 
 def run(d, group_idx=0, m=None, m_idx=0, ldd=None, bias=True, qcb=None, zp_d=0, cmin=-128,
-        cmax=127, D=None):
-    """One igemmcl run on the GPU into D (M_all x ldd, sentinel-filled unless given)."""
+        cmax=127, D=None, packed=False):
+    """One igemmcl run on the GPU into D (M_all x ldd, sentinel-filled unless given); packed:
+    the qsi8cxp sibling, weights packed on the GPU first."""
     import torch
 
     g = _g()
@@ -65,12 +69,18 @@ def run(d, group_idx=0, m=None, m_idx=0, ldd=None, bias=True, qcb=None, zp_d=0, 
     m = m_all(conv) - m_idx if m is None else m
     if D is None:
         D = np.full((m_all(conv), ldd), SENTINEL, np.int8)
-    din, dW, dD = g.dev(d["inp"]), g.dev(W), g.dev(D)
+    din, dD = g.dev(d["inp"]), g.dev(D)
+    if packed:
+        dWs = g.dev(W)
+        dW = torch.empty(n * K, dtype=torch.int8, device="cuda:0")
+        g.lib().fn("igemmclp", "run_bt_pack")(n, K, K, K, 0, dWs.data_ptr(), dW.data_ptr())
+    else:
+        dW = g.dev(W)
     dbias, dsb = g.dev(d["bias"]), g.dev(d["scale_b"])
     p = g.w8a8_params(dict(d, B=W, zp_d=zp_d, qcb=n if qcb is None else qcb), dsb)
     cp = g._mod.ConvParams()
     ctypes.memmove(ctypes.byref(cp), ctypes.byref(conv), ctypes.sizeof(cp))
-    g.lib().fn("igemmcl", "run")(
+    g.lib().fn("igemmclp" if packed else "igemmcl", "run")(
         m, n, K, din.data_ptr(), group_idx, m_idx, 0, dW.data_ptr(), K, 0, None, 0,
         dD.data_ptr(), ldd, dbias.data_ptr() if bias else None, cmin, cmax, ctypes.byref(cp),
         ctypes.byref(p))
@@ -110,25 +120,28 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
 @pytest.mark.parametrize("case", range(len(CASES)), ids=[
     "x".join(map(str, c[0])) + "_ic%d_oc%d_g%d" % c[1:] for c in CASES])
-def test_conv_halo_matches_oracle(gpu, case):
+def test_conv_halo_matches_oracle(gpu, case, packed):
     in_shape, ic, oc, groups = CASES[case]
     d = gen(in_shape, ic, oc, groups, seed=100 + case)
     for gi in range(groups):
-        np.testing.assert_array_equal(run(d, group_idx=gi), expected(d, group_idx=gi))
+        np.testing.assert_array_equal(run(d, group_idx=gi, packed=packed),
+                                      expected(d, group_idx=gi))
 
 
-def test_conv_halo_tiled_calls(gpu):
+@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
+def test_conv_halo_tiled_calls(gpu, packed):
     """The reference caller pattern with tiles of 200 pixels: no call starts on a 256-pixel
     boundary of the image, and the last one is ragged; D is addressed absolutely."""
-    d = gen((3, 17, 19), 128, 64, 1, seed=7)
+    d = gen((3, 17, 19), 128, 200, 1, seed=7)
     M = m_all(d["conv"])
-    D = np.full((M, 64), SENTINEL, np.int8)
+    D = np.full((M, 200), SENTINEL, np.int8)
     E = D.copy()
     for m_idx in range(0, M, 200):
         m = min(200, M - m_idx)
-        D = run(d, m=m, m_idx=m_idx, D=D)
+        D = run(d, m=m, m_idx=m_idx, D=D, packed=packed)
         E = expected(d, m=m, m_idx=m_idx, D=E)
     np.testing.assert_array_equal(D, E)
     assert not (D == SENTINEL).all(axis=1).any()

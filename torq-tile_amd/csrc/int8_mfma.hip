@@ -10,9 +10,10 @@
 // and their packed siblings.
 //
 // Four kernels, chosen per call:
-//   * conv_halo_kernel (igemmcl, plain weights, 3 x 3 "same" convolution with stride 1 and 128
-//     channels per group: the benchmark's): each workgroup loads the input rows its 256 output
-//     pixels touch into LDS once and forms the nine taps from them (described at the kernel);
+//   * conv_halo_kernel (igemmcl, plain or packed weights, 3 x 3 "same" convolution with stride 1
+//     and 128 channels per group: the benchmark's): each workgroup loads the input rows its 256
+//     output pixels touch into LDS once and forms the nine taps from them (described at the
+//     kernel);
 //   * int8_stream_kernel (plain A, B = [n, k], k % 128 == 0: W8A8 at its config; the other
 //     igemmcl geometries whose group channel count is a multiple of 128): 8 wave64s, a 4-deep
 //     ring of LDS stages filled by direct global->LDS loads, v_mfma_i32_32x32x32_i8, XCD-aware
@@ -1381,9 +1382,9 @@ void launch_stream(const Int8Args &a, hipStream_t stream)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Implicit convolution through an LDS input halo (igemmcl with plain weights; 2-D: one depth tap,
-// depth stride 1, no depth padding; 3 x 3 taps, stride 1, dilation 1, padding 1 in h and w, so
-// OH = IH and OW = IW; 128 channels per group).
+// Implicit convolution through an LDS input halo (igemmcl, plain or packed weights; 2-D: one
+// depth tap, depth stride 1, no depth padding; 3 x 3 taps, stride 1, dilation 1, padding 1 in h
+// and w, so OH = IH and OW = IW; 128 channels per group).
 //
 // Output pixels are numbered row by row through the depth (batch) axis. With these geometries
 // "stacked" output row R = od * OH + oh reads stacked input rows R - 1 .. R + 1 (input row
@@ -1451,8 +1452,10 @@ __device__ __forceinline__ i32x4 raw_rsrc(const void *base, int num_records)
     return r;
 }
 
+template <int PK>
 __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, HaloPlan hp)
 {
+    static_assert(PK == PK_NONE || PK == PK_B, "plain or packed weights");
     __shared__ __attribute__((aligned(128))) int8_t lds[kHaloLdsBytes];
     __shared__ __attribute__((aligned(16))) int32_t s_mult[kHaloCh];
     __shared__ __attribute__((aligned(16))) int32_t s_shift[kHaloCh];
@@ -1535,12 +1538,24 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
         }
     }
     // Weights: block `wave` of tap t is rows 8 wave .. 8 wave + 7 of the tile's 64, tap t's 128
-    // channels (bytes 128 t of the row).
+    // channels (bytes 128 t of the row). Packed weights (panels of 128 rows, 16-byte chunks
+    // chunk-major): chunk c of row r at the row's base plus 16 c w (w = the panel's height; the
+    // tile's 64 rows lie in one panel), so a block still reads 8 whole 128-byte lines (one per
+    // chunk, the 8 rows' chunks side by side) and a tap steps by 128 w.
     const int w_nr = wave * 8 + sub;
-    const int w_off = min(n0 + w_nr, a.N - 1) * static_cast<int>(a.ldb) +
-                      (slot ^ ((w_nr >> 1) & 7)) * 16;
+    const int w_row = min(n0 + w_nr, a.N - 1);
+    const int w_c16 = (slot ^ ((w_nr >> 1) & 7)) * 16;
+    int w_off, w_tap;
+    if constexpr (PK == PK_B) {
+        int mul;
+        w_off = static_cast<int>(pack_row_fixed<kPackI8NStep>(a.pb, w_row, mul)) + w_c16 * mul;
+        w_tap = g.ICg * mul;
+    } else {
+        w_off = w_row * static_cast<int>(a.ldb) + w_c16;
+        w_tap = g.ICg;
+    }
     auto issue_w = [&](int tp) {
-        dma_lds16_buf(b_rsrc, w_off + tp * g.ICg, lds + w_base + (tp * kHaloWBlocks + wave) * 1024);
+        dma_lds16_buf(b_rsrc, w_off + tp * w_tap, lds + w_base + (tp * kHaloWBlocks + wave) * 1024);
     };
     auto issue_stage = [&](int st) {
 #pragma unroll
@@ -1740,7 +1755,7 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
 }
 
 // The halo kernel's plan for this call, or false when its geometry or sizes do not fit it.
-bool halo_plan(const Int8Args &a, HaloPlan &hp)
+bool halo_plan(const Int8Args &a, bool packed, HaloPlan &hp)
 {
     const ConvGeom &g = a.cv;
     if (g.KD != 1 || g.PD != 0 || g.SD != 1 || g.KH != 3 || g.KW != 3 || g.SH != 1 || g.SW != 1 ||
@@ -1755,7 +1770,10 @@ bool halo_plan(const Int8Args &a, HaloPlan &hp)
         static_cast<long long>(kHaloPix) * a.ldd >= (1ll << 31)) {
         return false;
     }
-    const long long b_bytes = static_cast<long long>(a.N - 1) * a.ldb + a.K;
+    // bytes of B the loads may address: plain rows, or whole 128-row panels when packed
+    const long long b_bytes =
+        packed ? static_cast<long long>((a.N + kPackI8NStep - 1) / kPackI8NStep) * kPackI8NStep * a.ldb
+               : static_cast<long long>(a.N - 1) * a.ldb + a.K;
     if (a.ldb < a.K || b_bytes >= (1ll << 31)) {
         return false;
     }
@@ -1809,11 +1827,12 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
             return;
         }
     }
-    if constexpr (BMd == B_NK && AM == A_CONV_CL && EPI == EPI_REQUANT_I8 && PK == PK_NONE) {
+    if constexpr (BMd == B_NK && AM == A_CONV_CL && EPI == EPI_REQUANT_I8 &&
+                  (PK == PK_NONE || PK == PK_B)) {
         HaloPlan hp;
-        if (fast && halo_plan(a, hp)) {
-            hipLaunchKernelGGL(conv_halo_kernel, dim3(8 * hp.per_xcd), dim3(kStreamThreads), 0,
-                               stream, a, hp);
+        if (fast && halo_plan(a, PK == PK_B, hp)) {
+            hipLaunchKernelGGL(conv_halo_kernel<PK>, dim3(8 * hp.per_xcd), dim3(kStreamThreads),
+                               0, stream, a, hp);
             check_launch(where);
             return;
         }
