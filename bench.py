@@ -8,7 +8,7 @@ Headline (BASELINE.json metric "W4A8 GEMV HBM GB/s (M=1) + W8A8 GEMM int8 TOPS (
   * w4a8    = W4A8 decode GEMV HBM GB/s on configs[2] at M=1 (K=4096, N=11008), with its HBM
               roofline; M=4 and M=8 are reported beside it.
 The remaining configurations (int8->int32 GEMM, W4A16, int8 implicit-GEMM conv), the packed
-siblings of W8A8, W4A8 and W4A16 on the same shapes (operands packed by the library's packers
+siblings of W8A8, W4A8, W4A16 and igemmcl on the same shapes (operands packed by the library's packers
 before timing), and the W4A8 decode step with its activation quantization on the GPU, are timed
 the same way and reported under "configs".
 
@@ -335,7 +335,9 @@ def bench_floor(torch, timer, warmup, steps, nbytes):
                 us_by_loads={b: round(v * 1e3, 3) for b, v in per_loads.items()})
 
 
-def bench_conv(torch, mod, lib, timer, warmup, steps, rng):
+def bench_conv(torch, mod, lib, timer, warmup, steps, rng, packed=False):
+    """packed: the igemmcl...qsi8cxp sibling on the same inputs (weights packed once before
+    timing)."""
     c = CONV
     ID, IH, IW, IC, OC, KH, KW, pad = (c["ID"], c["IH"], c["IW"], c["IC"], c["OC"], c["KH"],
                                        c["KW"], c["pad"])
@@ -352,11 +354,13 @@ def bench_conv(torch, mod, lib, timer, warmup, steps, rng):
     for _ in range(nc - 1):
         din.append(din[0].clone())
     dW = torch.from_numpy(W).cuda()
+    if packed:
+        dW = pack_dev(torch, lib, "igemmclp", "run_bt_pack", OC, K, dW, W.nbytes)
     dsb = torch.from_numpy(sb).cuda()
     dbias = torch.from_numpy(bias).cuda()
     dD = torch.empty((M, OC), dtype=torch.int8, device="cuda")
     p = mod.QAI8QSI8CXParams(0.02, 3, dsb.data_ptr(), OC, 0.05, 0)
-    f = lib.fn("igemmcl", "run_async")
+    f = lib.fn("igemmclp" if packed else "igemmcl", "run_async")
     s = timer.stream.cuda_stream
 
     def launch(i):
@@ -582,8 +586,8 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,w4a16p,w4a8dq,conv,"
-                         "clamp,copy,floor): "
+                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,"
+                         "w4a16p,w4a8dq,conv,convp,clamp,copy,floor): "
                          "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -614,6 +618,7 @@ def main():
             "w4a16p": lambda: bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True),
             "w4a8dq": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True),
             "conv": lambda: bench_conv(torch, mod, lib, timer, W, K, rng),
+            "convp": lambda: bench_conv(torch, mod, lib, timer, W, K, rng, packed=True),
             "clamp": lambda: bench_clamp(torch, mod, lib, timer, W, K, rng),
             "copy": lambda: bench_copy(torch, timer, W, K),
             "floor": lambda: bench_floor(torch, timer, W, K, W4A8_BYTES),
@@ -645,6 +650,8 @@ def main():
                        bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True))
         w416p = progress("w4a16 packed",
                          bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True))
+        cvp = progress("igemmcl packed", bench_conv(torch, mod, lib, timer, W, K, rng,
+                                                    packed=True))
         w4dq = progress("w4a8 decode step",
                         bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True))
         fl = progress("read floor", bench_floor(torch, timer, W, K, w4[1]["bytes"]))
@@ -724,6 +731,9 @@ def main():
             "packed f16p_qsi4c2p 32x14336x4096 bl32": {
                 "us": round(w416p["ms"] * 1e3, 3), "GB/s": round(w416p["gbs"], 2),
                 "hbm_frac": round(w416p["gbs"] / HBM_PEAK_GBS, 4)},
+            "packed igemmcl qsi8cxp 8x56x56x128 3x3 OC128": {
+                "us": round(cvp["ms"] * 1e3, 3), "TOPS": round(cvp["tops"], 3),
+                "mfma_frac": round(cvp["tops"] / INT8_PEAK_TOPS, 4)},
         },
     }
     if traffic:

@@ -1538,20 +1538,24 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
         }
     }
     // Weights: block `wave` of tap t is rows 8 wave .. 8 wave + 7 of the tile's 64, tap t's 128
-    // channels (bytes 128 t of the row). Packed weights (panels of 128 rows, 16-byte chunks
-    // chunk-major): chunk c of row r at the row's base plus 16 c w (w = the panel's height; the
-    // tile's 64 rows lie in one panel), so a block still reads 8 whole 128-byte lines (one per
-    // chunk, the 8 rows' chunks side by side) and a tap steps by 128 w.
-    const int w_nr = wave * 8 + sub;
-    const int w_row = min(n0 + w_nr, a.N - 1);
-    const int w_c16 = (slot ^ ((w_nr >> 1) & 7)) * 16;
+    // channels (bytes 128 t of the row), read as 8 whole 128-byte lines, one per 8-lane group
+    // (LDS-DMA puts lane i's 16 bytes at byte 16 i of the block). Plain weights: group `sub`
+    // reads row 8 wave + sub, its chunks in slots XOR-swizzled by the row. Packed weights
+    // (panels of 128 rows, 16-byte chunks chunk-major: chunk c of row r at the row's base plus
+    // 16 c w, w = the panel's height; the tile's 64 rows lie in one panel): group `sub` reads
+    // chunk sub ^ (wave & 1) of the 8 rows, which lie side by side, so the block is chunk-major
+    // with its 128-byte chunk pairs swapped in odd blocks; a tap steps by 128 w.
     int w_off, w_tap;
     if constexpr (PK == PK_B) {
+        const int w_row = min(n0 + wave * 8 + slot, a.N - 1);
         int mul;
-        w_off = static_cast<int>(pack_row_fixed<kPackI8NStep>(a.pb, w_row, mul)) + w_c16 * mul;
+        w_off = static_cast<int>(pack_row_fixed<kPackI8NStep>(a.pb, w_row, mul)) +
+                (sub ^ (wave & 1)) * 16 * mul;
         w_tap = g.ICg * mul;
     } else {
-        w_off = w_row * static_cast<int>(a.ldb) + w_c16;
+        const int w_nr = wave * 8 + sub;
+        const int w_row = min(n0 + w_nr, a.N - 1);
+        w_off = w_row * static_cast<int>(a.ldb) + (slot ^ ((w_nr >> 1) & 7)) * 16;
         w_tap = g.ICg;
     }
     auto issue_w = [&](int tp) {
@@ -1576,12 +1580,21 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
     const int jbase = wave >> 2;
     const int r32 = lane & 31;
     const int h = lane >> 5;
-    // the lane's unit of k-step k is (address ^ 32 k): the XOR touches chunk bits 5..6 only
+    // the lane's unit of k-step k is (address ^ 32 k) in a pixel row and (address ^ WKX k) in
+    // a weight block: the XOR touches the chunk bits above h's only. A 16-lane pass of a
+    // ds_read_b128 (16 rows of one chunk) covers the 16 slots of 256 bytes once in either
+    // weight layout.
+    constexpr int WKX = PK == PK_B ? 256 : 32;
     int w_addr[RW];  // + 8192 tap
 #pragma unroll
     for (int jj = 0; jj < RW; ++jj) {
         const int nr = (jbase + jj) * 32 + r32;
-        w_addr[jj] = w_base + nr * 128 + ((16 * h) ^ (16 * ((nr >> 1) & 7)));
+        if constexpr (PK == PK_B) {
+            const int blk = nr >> 3;
+            w_addr[jj] = w_base + blk * 1024 + (h ^ (blk & 1)) * 128 + (nr & 7) * 16;
+        } else {
+            w_addr[jj] = w_base + nr * 128 + ((16 * h) ^ (16 * ((nr >> 1) & 7)));
+        }
     }
     // per fragment: the halo pixel of tap (0, 0), and whether the top / bottom kernel rows lie in
     // this pixel's image
@@ -1668,7 +1681,7 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
 #pragma unroll
             for (int jj = 0; jj < RW; ++jj) {
                 fw[u][jj] = *reinterpret_cast<const i32x4 *>(
-                    lds + ((w_addr[jj] + (st * kHaloTPS + tt) * 8192) ^ kx));
+                    lds + ((w_addr[jj] + (st * kHaloTPS + tt) * 8192) ^ (WKX * (u % KPW))));
             }
 #pragma unroll
             for (int i = 0; i < RP; ++i) {
