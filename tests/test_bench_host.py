@@ -13,7 +13,8 @@ NS = "tqt::(anonymous namespace)::"
 
 
 @pytest.mark.parametrize("name,leg", [
-    ("void %sconv_halo_kernel(%sInt8Args, %sHaloPlan)" % (NS, NS, NS), "conv"),
+    ("void %sconv_halo_kernel<0>(%sInt8Args, %sHaloPlan)" % (NS, NS, NS), "conv"),
+    ("void %sconv_halo_kernel<2>(%sInt8Args, %sHaloPlan)" % (NS, NS, NS), "conv"),
     ("void %sint8_stream_kernel<128, 1, 0, true>(%sInt8Args, int, int, int)" % (NS, NS), "conv"),
     ("void %sint8_stream_kernel<64, 1, 0, false>(%sInt8Args, int, int, int)" % (NS, NS), "w8a8"),
     ("void %sw4a8_mfma_kernel<1, 0, 0>(%sW4A8Args)" % (NS, NS), "w4a8"),
