@@ -15,7 +15,8 @@ byte tail of the dword stores); two and three groups with each group selected; c
 group other than 128 (the other kernels); the caller's m_idx tiling with tiles that do not start on
 a 256-pixel boundary; a padded D row stride (the bytes past n stay untouched) and an odd one (not
 dword-aligned: the other kernels); output zero point with a narrow clamp; a per-tensor weight
-scale; no bias; accumulators near 2^24 from extreme inputs."""
+scale; no bias; accumulators near 2^24 from extreme inputs; a seeded sweep of random geometries,
+channel counts, weight layouts and caller tilings."""
 
 import ctypes
 
@@ -173,3 +174,31 @@ def test_conv_halo_extreme_accumulators(gpu):
     2^24 ahead of the bias and the requantization multiply."""
     d = gen((2, 7, 9), 128, 64, 1, seed=9, extreme=True)
     np.testing.assert_array_equal(run(d), expected(d))
+
+
+def test_conv_halo_random_geometries(gpu):
+    """A seeded sweep over 3 x 3 "same" convolutions with 128 channels per group: image counts,
+    heights and widths (rows up to the halo's width limit and past it), output channels, one or
+    two groups, plain or packed weights, and the caller's pixel tiling (whole calls or tiles of a
+    random size), each bit-exact against the oracle."""
+    rng = np.random.default_rng(2024)
+    for case in range(16):
+        ID = int(rng.integers(1, 5))
+        IH = int(rng.integers(1, 21))
+        IW = int(rng.integers(1, 121))
+        groups = int(rng.integers(1, 3))
+        oc = groups * int(rng.integers(1, 97))
+        packed = bool(rng.integers(0, 2))
+        d = gen((ID, IH, IW), 128 * groups, oc, groups, seed=500 + case)
+        M = m_all(d["conv"])
+        tile = M if rng.integers(0, 2) else int(rng.integers(1, M + 1))
+        gi = int(rng.integers(0, groups))
+        print("case %d: %dx%dx%d oc %d groups %d (group %d) packed %d tile %d" % (
+            case, ID, IH, IW, oc, groups, gi, packed, tile), flush=True)
+        D = np.full((M, oc), SENTINEL, np.int8)
+        E = D.copy()
+        for m_idx in range(0, M, tile):
+            m = min(tile, M - m_idx)
+            D = run(d, group_idx=gi, m=m, m_idx=m_idx, D=D, packed=packed)
+            E = expected(d, group_idx=gi, m=m, m_idx=m_idx, D=E)
+        np.testing.assert_array_equal(D, E)
