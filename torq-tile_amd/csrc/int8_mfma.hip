@@ -796,19 +796,31 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
     const int wn = wave % kStreamWavesN;
 
     // Epilogue inputs are loaded now and used after the main loop, so their latency hides under
-    // it: the multipliers' scale_b (finished into s_mult / s_shift after the loop: computing
-    // them here would hold back this wave's first loads by a memory round trip) and the biases.
+    // it: the per-row multipliers' scale_b (EPI_REQUANT_ROW: finished into s_mult / s_shift
+    // after the loop: computing them here would hold back this wave's first loads by a memory
+    // round trip; the per-column ones are below) and the biases.
     constexpr bool kRow = EPI == EPI_REQUANT_ROW;
     [[maybe_unused]] float pre_sb = 0.f;
     [[maybe_unused]] int32_t pre_rbias = 0;  // per-row bias (EPI_REQUANT_ROW)
     [[maybe_unused]] uint32_t pre_cbias[NF] = {};
     [[maybe_unused]] const bool mult_lane = kRow ? (tid < BM && m0 + tid < a.M)
                                                  : (tid < kBN && n0 + tid < a.N);
-    if constexpr (EPI == EPI_REQUANT_I8 || kRow) {
+    // Per-column requantization (W8A8, the convolution mode): the tile's 128 weight scales come
+    // into LDS by LDS-DMA from waves 0 and 1 ahead of their ring loads (the first stage's wait
+    // covers them, and the compiler places no wait of its own), and those lanes turn them into
+    // multipliers after stage 1's compute, while its MFMAs run.
+    __shared__ __attribute__((aligned(16))) float s_sbv[EPI == EPI_REQUANT_I8 ? kBN : 1];
+    if constexpr (EPI == EPI_REQUANT_I8) {
+        if (tid < kBN) {  // whole waves: kBN is a multiple of 64
+            const int idx = min(n0 + tid, a.N - 1);
+            dma_lds4(a.scale_b + (a.quant_channel_b == 1 ? 0 : idx),
+                     reinterpret_cast<int8_t *>(s_sbv) + (tid & ~63) * 4);
+        }
+    } else if constexpr (kRow) {
         if (mult_lane) {
-            const int idx = kRow ? m0 + tid : n0 + tid;
+            const int idx = m0 + tid;
             pre_sb = a.scale_b[a.quant_channel_b == 1 ? 0 : idx];
-            if (kRow && a.bias) {
+            if (a.bias) {
                 pre_rbias = a.bias[idx];
             }
         }
@@ -1048,6 +1060,11 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
             issue(st + NS - 1, nxt, nxt + SA);
         }
         compute(cur, cur + SA);
+        if constexpr (EPI == EPI_REQUANT_I8) {
+            if (st == 1 && tid < kBN) {
+                column_multiplier_val(a.scale_a, s_sbv[tid], a.scale_d, s_mult[tid], s_shift[tid]);
+            }
+        }
     };
 
 #pragma unroll
@@ -1068,15 +1085,26 @@ __global__ __launch_bounds__(kStreamThreads) void int8_stream_kernel(Int8Args a,
     // each of those waits would drain the previous output's store (measured: 4.5 us of a
     // 22.4 us W8A8 M512 launch).
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
-    if constexpr (EPI == EPI_REQUANT_I8 || kRow) {
-        if (mult_lane) {
-            column_multiplier_val(a.scale_a, pre_sb, a.scale_d, s_mult[tid], s_shift[tid]);
-            if constexpr (kRow) {
+    if constexpr (EPI == EPI_REQUANT_I8) {
+        // With three stages or more, stage 2's wait (lgkmcnt(0)) and barrier already order the
+        // multipliers' LDS stores before every wave's epilogue (no barrier here: 0.47 us less per
+        // W8A8 M512 launch with the multipliers moved into the loop); shorter k computes them
+        // here.
+        if (nst < 2 && tid < kBN) {
+            column_multiplier_val(a.scale_a, s_sbv[tid], a.scale_d, s_mult[tid], s_shift[tid]);
+        }
+        if (nst < 3) {
+            __syncthreads();
+        }
+    } else {
+        if constexpr (kRow) {
+            if (mult_lane) {
+                column_multiplier_val(a.scale_a, pre_sb, a.scale_d, s_mult[tid], s_shift[tid]);
                 s_rbias[tid] = pre_rbias;
             }
         }
+        __syncthreads();  // s_mult / s_shift / s_rbias visible to every wave
     }
-    __syncthreads();  // s_mult / s_shift / s_rbias visible to every wave
 
     if constexpr (is_dyn(EPI)) {
         // lanes r32 and r32 + 32 summed the two 16-byte halves of every k-step of column r32
