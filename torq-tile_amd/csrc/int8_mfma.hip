@@ -776,7 +776,8 @@ constexpr int kStreamThreads = kStreamWaves * 64;
 
 // LDS ring depth of the streaming kernel (stages of 128 bytes of k for BM + 128 rows). Four
 // stages: a 5- or 6-stage ring (which 64-row tiles would fit) measured no faster at the W8A8
-// configuration (cold operands 17.6-18.0 us with four, 18.2 with six).
+// configuration (cold operands 17.6-18.0 us with four, 18.2 with six), and three slower (17.6-17.7
+// vs 16.8 us).
 constexpr int kStreamStages = 4;
 
 template <int BM, int EPI, int PK, bool kConv = false>
