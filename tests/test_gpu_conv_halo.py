@@ -202,3 +202,35 @@ def test_conv_halo_random_geometries(gpu):
             D = run(d, group_idx=gi, m=m, m_idx=m_idx, D=D, packed=packed)
             E = expected(d, group_idx=gi, m=m, m_idx=m_idx, D=E)
         np.testing.assert_array_equal(D, E)
+
+
+@pytest.mark.parametrize("oc", [200, 72])
+def test_conv_halo_packed_k_idx(gpu, oc):
+    """Packed weights that are the k-range [16, 16 + K) of a wider packed buffer (ld_packed =
+    K + 16, packed with k_idx = 16, so a narrower last panel starts 16 * (128 - w) bytes earlier
+    by the packers' tail rule), run with the same ldb and k_idx_b: the halo kernel's
+    chunk-major weight loads address the shifted tail panel like the packers."""
+    import torch
+
+    g = _g()
+    d = gen((2, 11, 13), 128, oc, 1, seed=31 + oc)
+    conv, W = d["conv"], d["W"]
+    n, K = W.shape
+    kx = 16
+    L = g.lib()
+    ns = L.fn("igemmclp", "get_n_step")()
+    Bp = torch.zeros(n * (K + kx), dtype=torch.int8, device="cuda:0")
+    b_off = L.fn("igemmclp", "get_b_packed_offset")(0, kx, K + kx, min(n, ns))
+    dW = g.dev(W)
+    L.fn("igemmclp", "run_bt_pack")(n, K, K, K + kx, kx, dW.data_ptr(), Bp.data_ptr() + b_off)
+    M = m_all(conv)
+    dD = g.dev(np.full((M, n), SENTINEL, np.int8))
+    din, dbias, dsb = g.dev(d["inp"]), g.dev(d["bias"]), g.dev(d["scale_b"])
+    p = g.w8a8_params(dict(d, B=W), dsb)
+    cp = g._mod.ConvParams()
+    ctypes.memmove(ctypes.byref(cp), ctypes.byref(conv), ctypes.sizeof(cp))
+    L.fn("igemmclp", "run")(M, n, K, din.data_ptr(), 0, 0, 0, Bp.data_ptr() + b_off, K + kx, kx,
+                            None, 0, dD.data_ptr(), n, dbias.data_ptr(), -128, 127,
+                            ctypes.byref(cp), ctypes.byref(p))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dD.cpu().numpy(), expected(d))

@@ -809,10 +809,10 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
 
     // This lane's outputs of a tile (MFMA layout): rows mt * 16 + fg * 4 + r, column fr. D and C
     // are addressed through buffer resources based at this workgroup's first row and ending at
-    // its last row (the launcher keeps 32 rows of either under 2^31 bytes): a lane's offset is
-    // (fg * 4 * ld + column) elements, each output row adds a wave-uniform offset, and rows past
-    // m fall outside the resource (columns past n get an offset past it), so no output is
-    // guarded by a branch.
+    // its last row (the launcher keeps 32 rows of either under 2^31 bytes): each output's offset
+    // is (row * ld + column) elements, and an output in a row past m or a column past n gets the
+    // resource's size as its offset, which the range check drops, so no output is guarded by a
+    // branch.
     constexpr uint32_t kOutBytes = OUT == OUT_F32 ? 4u : 2u;
     const uint32_t rows_here = static_cast<uint32_t>(min(kMRows, a.M - mg0));
     const uint32_t d_bytes = rows_here * static_cast<uint32_t>(a.ldd) * kOutBytes;
@@ -903,18 +903,15 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
         }
     };
     // Tile tl's outputs, once all 16 waves have added their partials: the sums rounded to f32
-    // once, then C, bias, clamp.
-    auto finish = [&](int tl) {
+    // once, then C, bias, clamp. `counted`: false when the arrival wait gave up, and then every
+    // output of the tile is written as NaN, so a lost count-in cannot leave stale outputs.
+    // Each output's whole offset is the lane's vector offset (scalar offset 0): an output row
+    // past m or a column past n gets the resource's size, which the range check drops.
+    auto finish = [&](int tl, bool counted) {
         const double *sum = &s_acc[tl][0];
         const int gn = (t_begin + tl) * kNTile + fr;
         const float bias = a.bias ? s_bias[tl * kNTile + fr] : 0.f;
         const bool col_ok = gn < a.N;
-        const uint32_t d_off = col_ok ? (static_cast<uint32_t>(fg * 4) * static_cast<uint32_t>(a.ldd) +
-                                         static_cast<uint32_t>(gn)) * kOutBytes
-                                      : d_bytes;
-        const uint32_t c_off = col_ok ? (static_cast<uint32_t>(fg * 4) * static_cast<uint32_t>(a.ldc) +
-                                         static_cast<uint32_t>(gn)) * kOutBytes
-                                      : c_bytes;
         // all eight sums read at once (one LDS round trip), rounded to f32
         float v[8];
 #pragma unroll
@@ -923,17 +920,25 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const uint32_t row = (e >> 2) * 16 + (e & 3);  // plus fg * 4 (in the lane offsets)
+            const uint32_t row = static_cast<uint32_t>(fg * 4 + (e >> 2) * 16 + (e & 3));
+            const bool ok = col_ok && row < rows_here;
+            const uint32_t d_off =
+                ok ? (row * static_cast<uint32_t>(a.ldd) + static_cast<uint32_t>(gn)) * kOutBytes
+                   : d_bytes;
             float x = v[e];
             if (a.C) {
-                x += load_out_buf<OUT>(c_rsrc, c_off, row * static_cast<uint32_t>(a.ldc) * kOutBytes);
+                const uint32_t c_off =
+                    ok ? (row * static_cast<uint32_t>(a.ldc) + static_cast<uint32_t>(gn)) * kOutBytes
+                       : c_bytes;
+                x += load_out_buf<OUT>(c_rsrc, c_off, 0u);
             }
             if (a.bias) {
                 x += bias;
             }
             x = fmaxf(x, a.cmin);
             x = fminf(x, a.cmax);
-            store_out_buf<OUT>(d_rsrc, d_off, row * static_cast<uint32_t>(a.ldd) * kOutBytes, x);
+            store_out_buf<OUT>(d_rsrc, d_off, 0u,
+                               counted ? x : __builtin_bit_cast(float, 0x7fc00000u));
         }
     };
     tile(0, std::true_type{});
@@ -944,7 +949,8 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     // Wave w < ntl finishes tile w once the last wave has counted itself in. Waves 0-3 get their
     // A first and finish their own tiles first, so the tiles' epilogues overlap the slower
     // waves' math; only the last tile's stays on the path. Every wave counts itself in for every
-    // tile without waiting for anyone, so the wait ends; the iteration cap only bounds it.
+    // tile without waiting for anyone, so the wait ends; the iteration cap only bounds it, and a
+    // tile whose count never completes is written as NaN (the parity checks then fail).
     if (wave < ntl) {
         uint32_t in = 0;
         for (int it = 0; it < (1 << 24); ++it) {
@@ -954,10 +960,8 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        if (in == NW) {
-            asm volatile("" ::: "memory");
-            finish(wave);
-        }
+        asm volatile("" ::: "memory");
+        finish(wave, in == NW);
     }
     __builtin_amdgcn_s_waitcnt(waitcnt_vm0(0));
 }
@@ -1070,7 +1074,7 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
                        ldsb % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(scale_b) &&
                        ldd < (1ull << 24) && ldc < (1ull << 24);
     if (strip) {
-        static int cus = device_cu_count();
+        const int cus = device_cu_count();  // the current device, per call (no cached state)
         const long long need = (a.ntiles + kStripTiles - 1) / kStripTiles;
         const long long nwg = need > cus ? need : (a.ntiles < cus ? a.ntiles : cus);
         const unsigned long long gy = (m + kMRows - 1) / kMRows;
@@ -1096,7 +1100,7 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
             }
         }
     } else if (fast) {
-        static int cus = device_cu_count();
+        const int cus = device_cu_count();  // the current device, per call (no cached state)
         const int gx = a.ntiles < cus ? a.ntiles : cus;
         const unsigned long long gy = (m + kMRows - 1) / kMRows;
         TQT_REQUIRE(gy < 65536, "m too large");

@@ -1565,7 +1565,9 @@ __global__ __launch_bounds__(kStreamThreads) void conv_halo_kernel(Int8Args a, H
         // input offset of (row R0 - 1 + jr, column col - 1): row-major pixels, IC bytes each;
         // unsigned (wrapping) arithmetic: outside the input (row -1, rows past the last, the
         // border columns) the value is not used, and where it is used it is below 2^31
-        uint32_t off = static_cast<uint32_t>(((R0 - 1 + jr) * g.IW + col - 1) * g.IC) +
+        uint32_t off = (static_cast<uint32_t>(R0 - 1 + jr) * static_cast<uint32_t>(g.IW) +
+                        static_cast<uint32_t>(col - 1)) *
+                           static_cast<uint32_t>(g.IC) +
                        static_cast<uint32_t>((slot ^ ((q0 >> 1) & 7)) * 16);
         const uint32_t doff = static_cast<uint32_t>((djr * g.IW + dcol) * g.IC);
         // a row wrap: HC pixels back, IW forward
