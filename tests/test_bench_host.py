@@ -18,7 +18,7 @@ NS = "tqt::(anonymous namespace)::"
     ("void %sint8_stream_kernel<128, 1, 0, true>(%sInt8Args, int, int, int)" % (NS, NS), "conv"),
     ("void %sint8_stream_kernel<64, 1, 0, false>(%sInt8Args, int, int, int)" % (NS, NS), "w8a8"),
     ("void %sw4a8_mfma_kernel<1, 0, 0>(%sW4A8Args)" % (NS, NS), "w4a8"),
-    ("void %sw4a16_lds_kernel<4096, 0, 1>(%sW4A16Args, int)" % (NS, NS), "w4a16"),
+    ("void %sw4a16_chunk_kernel<0, 1, 3>(%sW4A16Args, int)" % (NS, NS), "w4a16"),
     ("void at::native::vectorized_elementwise_kernel<4, at::native::bitwise_not_kernel_cuda>",
      "copy"),
     ("void %squantize_qai8dx_kernel(float const*)" % NS, None),

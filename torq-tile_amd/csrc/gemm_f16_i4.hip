@@ -1,9 +1,8 @@
 // gemm_1xnbias_clamp_f16_f16_qsi4c2t (W4A16, block-quantized int4 weights) on gfx950.
 //
-// Three MFMA kernels share the math below: w4a16_lds_kernel (k 2048 and 4096: 16 waves per CU,
-// weights streamed through per-wave LDS rings, no per-tile meeting of the waves; see its own
-// comment), w4a16_regs_kernel (k 3072: whole CUs, at most four tiles each, two tiles in flight)
-// and w4a16_mfma_kernel (any other k % 128 == 0, k <= 4096). In w4a16_mfma_kernel a workgroup of
+// Two MFMA kernels share the math below: w4a16_chunk_kernel (k % 512 == 0: 16 waves per CU walk
+// k in 512-wide chunks streamed through a shared LDS ring; see its own comment) and
+// w4a16_mfma_kernel (any other k % 128 == 0, k <= 4096). In w4a16_mfma_kernel a workgroup of
 // 8 wave64s owns a strip of
 // 16-channel weight tiles for one group of 32 activation rows. Wave w owns a fixed slice of k
 // (a run of 32-wide scale blocks) and keeps its slice of A (32 rows, f16) in registers for the
@@ -137,73 +136,6 @@ __device__ __forceinline__ f16x8 permute_a(u32x4 v)
     o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
     o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
     return __builtin_bit_cast(f16x8, o);
-}
-
-// A slice of a strip kernel's wave: 2 * BPW 16-byte loads per lane covering 32 rows x BPW 32-k
-// blocks. Plain A is loaded in whole cache lines -- load j = 2 * jp + rh of row tile mt gives lane
-// L row mt * 16 + rh * 8 + L / 8, 16-byte chunk L % 8 of block pair jp -- because 16 rows x 64 B
-// per instruction (the MFMA layout) runs at well under half the rate when every row is a separate
-// line. Packed A is loaded straight in the MFMA layout (lane (r, g): row mt * 16 + r, chunk g of
-// block j), which its chunk-major panels already make whole lines. Rows past m read row m - 1.
-template <int BPW, int PK>
-__device__ __forceinline__ const uint8_t *a_slice_addr(const W4A16Args &a, int mg0, int wave,
-                                                       int lane, int j, int mt)
-{
-    int row, k;
-    if constexpr ((PK & PK_A) != 0) {
-        row = mg0 + mt * 16 + (lane & 15);
-        k = (wave * BPW + j) * 32 + (lane >> 4) * 8;
-    } else {
-        row = mg0 + mt * 16 + (j & 1) * 8 + (lane >> 3);
-        k = (wave * BPW + (j & ~1)) * 32 + (lane & 7) * 8;
-    }
-    int mul;
-    const uint8_t *arow = a_row_ptr<PK>(a, min(row, a.M - 1), mul);
-    return arow + 2ll * k * mul;
-}
-
-// The slice as a_slice_addr loaded it -> MFMA A fragments (k in permute_a's slot order). Plain A
-// passes through `stage`, 2 KiB of LDS private to the wave: per (jp, mt) 16 rows x 128 B written
-// as loaded (chunk c of row r at 16-byte slot c ^ (r & 7): conflict-free both ways) and read back
-// as block 2 jp + jj, lane (r, g) taking chunk 4 jj + g of row r. Blocks [J0, J1) only (even
-// bounds).
-template <int BPW, int PK, int J0 = 0, int J1 = BPW>
-__device__ __forceinline__ void a_slice_to_mfma(const u32x4 (&ra)[BPW][2], f16x8 (&fa)[BPW][2],
-                                                int8_t *stage, int lane)
-{
-    static_assert(J0 % 2 == 0 && J1 % 2 == 0 && 0 <= J0 && J0 < J1 && J1 <= BPW, "block range");
-    if constexpr ((PK & PK_A) != 0) {
-#pragma unroll
-        for (int j = J0; j < J1; ++j) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                fa[j][mt] = permute_a(ra[j][mt]);
-            }
-        }
-    } else {
-        const int wr = lane >> 3;
-        const int wc = lane & 7;
-        const int fr = lane & 15;
-        const int fg = lane >> 4;
-#pragma unroll
-        for (int jp = J0 / 2; jp < J1 / 2; ++jp) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-                for (int rh = 0; rh < 2; ++rh) {
-                    const int r = rh * 8 + wr;
-                    *reinterpret_cast<u32x4 *>(stage + r * 128 + ((wc ^ (r & 7)) << 4)) =
-                        ra[2 * jp + rh][mt];
-                }
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(
-                        stage + fr * 128 + (((4 * jj + fg) ^ (fr & 7)) << 4));
-                    fa[2 * jp + jj][mt] = permute_a(v);
-                }
-            }
-        }
-    }
 }
 
 template <int PK, int OUT>
@@ -348,255 +280,46 @@ __global__ __launch_bounds__(512) void w4a16_mfma_kernel(W4A16Args a)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Strip kernel (bl == 32, k 3072 here; any n): one workgroup of NW wave64s per CU owns up to four
-// consecutive 16-channel tiles for one group of 32 activation rows. It loads its A slice once
-// (into registers, wave w owning k-blocks [w * BPW, (w + 1) * BPW)) and streams the tiles'
-// weights and scales from global memory straight into registers, 16 bytes per lane (one 32-k
-// block of one channel); a 4x4 lane-group transpose gives each lane its 8-k slice of four
-// consecutive blocks. NW = 8 at k 3072: two waves per SIMD, two tiles in flight (k 2048 and 4096
-// take the LDS-staged kernel below: 19.3 us at the bench's k 4096 against 20.7 for this kernel
-// with 16 waves, 22.4 with 8). Per tile the math is the one of w4a16_mfma_kernel above; the
-// waves' f32 partials meet in LDS. The register sets rotate by unrolling, since a register copy
-// would wait for the load still filling it.
+// Chunk-stream kernel (bl == 32, k % 512 == 0): one workgroup of 16 wave64s per CU owns up to
+// four consecutive 16-channel tiles for one group of 32 activation rows and walks k in chunks of
+// 512 (sixteen 32-k scale blocks). A chunk -- the 32 rows' 512 activations (32 KiB of f16), the
+// tiles' 256 weight bytes per channel (16 KiB) and their 16 scales per channel (2 KiB) -- lands
+// in one slot of a three-slot LDS ring by direct global -> LDS loads, two chunks ahead of the one
+// being computed, so the whole CU computes behind one stream. Every wave loads two KiB of each
+// chunk's activations and a quarter of one tile's weights; waves 0 and 1 also load the scales.
+// Wave w computes scale block w of every chunk for all the tiles, so each activation byte is
+// read from LDS once and its fragment (permuted once) serves four tiles: per block and tile one
+// weight dword per lane (its 8-k slice of the block for one channel), the exact nibble -> f16
+// q - 8 decode, two v_mfma_f32_16x16x32_f16 (rows 0-15, 16-31) and the block's f32 partials
+// times the block's f16 scale accumulated in f32 -- the per-block scaling of the reference
+// test's oracle. At the end the sixteen block partials of each output are added in f64 in block
+// order (a fixed order: the result does not depend on timing) and rounded to f32 once; then C,
+// bias (both read before the loop), clamp, store.
+// LDS layout of a slot (bank-conflict-free reads):
+//   activations: row r's 16-byte chunk c (k 8c .. 8c + 7 of the chunk) at slot r * 64 + (c ^ (r & 15)),
+//     packed activations chunk-major (chunk c of row r at slot c * 32 + r, as in the panel);
+//   plain weights: channel ch of tile t at t * 4096 + ch * 256, block b's 16 bytes at slot b ^ ch;
+//   packed weights: the tile's 4 KiB of the chunk as they lie in the panel (16-byte chunk s of
+//     row r at (16 s + r) * 16; chunk s holds dword s & 3 of blocks 4 (s >> 2) .. + 3);
+//   scales: channel ch's 8 f16 of blocks 8h .. 8h + 7 at h * 1024 + ch * 16.
+// Loads are inline asm (no compiler-placed waits, see dma_lds16); the loop waits for its own
+// loads with an explicit vmcnt and meets the other waves at one barrier per chunk, after which
+// the slot everyone finished in the previous chunk is refilled.
 // ---------------------------------------------------------------------------------------------
-constexpr int kStripTiles = 4;
-constexpr int kStripMaxK = 4096;
+constexpr int kCsWaves = 16;                         // wave64s per workgroup
+constexpr int kCsTiles = 4;                          // tiles per workgroup at most
+constexpr int kCsK = 512;                            // k per chunk
+constexpr int kCsBlocks = kCsK / 32;                 // scale blocks per chunk (one per wave)
+constexpr int kCsA = kMRows * kCsK * 2;              // activation bytes per chunk (32 KiB)
+constexpr int kCsW = kCsTiles * kNTile * (kCsK / 2); // weight bytes per chunk (16 KiB)
+constexpr int kCsS = kCsTiles * kNTile * kCsBlocks * 2;  // scale bytes per chunk (2 KiB)
+constexpr int kCsSlot = kCsA + kCsW + kCsS;
+constexpr int kCsRing = 3;                           // ring slots (chunks in flight + 1)
 
 // 8 nibbles (k = 0..7 of one block slice, nibble i at bits 4i) -> 8 exact f16 values q - 8 in
-// slot order k = 0, 4, 1, 5, 2, 6, 3, 7 (the order permute_a gives the activations).
-// `magic` is 0x64006400 held in an SGPR, so each insert is one v_bfi_b32.
-__device__ __forceinline__ f16x8 unpack_q8_sgpr(uint32_t x, uint32_t magic)
-{
-    const f16x2 bias = f16x2{static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
-    f16x8 out;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t d = ((x >> (4 * j)) & 0x000f000fu) | (magic & ~0x000f000fu);
-        const f16x2 h = __builtin_bit_cast(f16x2, d) + bias;
-        out[2 * j] = h[0];
-        out[2 * j + 1] = h[1];
-    }
-    return out;
-}
-
-template <int K, int PK, int OUT, int NW>
-__global__ __launch_bounds__(NW * 64) void w4a16_regs_kernel(W4A16Args a, int nwg)
-{
-    constexpr int BPW = K / (32 * NW);  // 32-k blocks per wave
-    constexpr int NG = BPW / 4;         // 4-block groups per wave
-    static_assert(BPW % 4 == 0 && BPW >= 4 && K <= kStripMaxK, "strip kernel k");
-    __shared__ float s_part[NW * kMRows * kNTile];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int fr = lane & 15;
-    const int fg = lane >> 4;
-    const int mg0 = blockIdx.y * kMRows;
-
-    const int t_begin = static_cast<int>((static_cast<long long>(blockIdx.x) * a.ntiles) / nwg);
-    const int t_end = static_cast<int>((static_cast<long long>(blockIdx.x + 1) * a.ntiles) / nwg);
-    const int ntl = t_end - t_begin;  // 1 .. kStripTiles
-
-    // A slice of this wave (unconditional loads: all in flight together).
-    u32x4 ra[BPW][2];
-#pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            ra[j][mt] = *reinterpret_cast<const u32x4 *>(
-                a_slice_addr<BPW, PK>(a, mg0, wave, lane, j, mt));
-        }
-    }
-
-    struct TileRegs
-    {
-        u32x4 w[NG];
-        uint64_t s[NG];
-    };
-    // Tile tl (clamped to the strip, so every call loads: a repeat hits the cache).
-    auto load = [&](int tl, TileRegs &r) {
-        const int t = t_begin + min(tl, ntl - 1);
-        const int n = min(t * kNTile + fr, a.N - 1);
-        int wmul;
-        const uint8_t *wrow = b_row_ptr<PK>(a, n, wmul);
-        const _Float16 *srow = a.scale_b + static_cast<long long>(n) * a.ldsb;
-#pragma unroll
-        for (int q = 0; q < NG; ++q) {
-            const int b0 = wave * BPW + 4 * q;
-            r.w[q] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4 *>(wrow + static_cast<long long>((b0 + fg) * 16) * wmul));
-            r.s[q] = *reinterpret_cast<const uint64_t *>(srow + b0);
-        }
-    };
-    // register sets in rotation: three (two tiles' loads in flight while one is computed) at
-    // 8 waves; two at 16 waves, where four waves per SIMD hide the latency instead
-    constexpr int kAhead = NW >= 16 ? 1 : 2;
-    TileRegs r0, r1, r2;
-    load(0, r0);
-    if constexpr (kAhead == 2) {
-        load(1, r1);
-    }
-
-    // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
-    // The wave's own partials area of s_part stages its A (no other wave touches it).
-    f16x8 fa[BPW][2];
-    a_slice_to_mfma<BPW, PK>(ra, fa, reinterpret_cast<int8_t *>(&s_part[wave * kMRows * kNTile]),
-                             lane);
-    uint32_t magic;
-    asm volatile("s_mov_b32 %0, 0x64006400" : "=s"(magic));
-
-    auto tile = [&](int tl, const TileRegs &cur, TileRegs &nxt) {
-        load(tl + kAhead, nxt);
-        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-        for (int q = 0; q < NG; ++q) {
-            uint32_t p[4] = {cur.w[q][0], cur.w[q][1], cur.w[q][2], cur.w[q][3]};
-            if constexpr ((PK & PK_B) == 0) {
-                transpose_lane_groups(p);  // packed weights are stored transposed already
-            }
-            // 8 waves: all four blocks' MFMAs first, then their scale FMAs (latency hidden in
-            // the wave); 16 waves: block by block (fewer registers; other waves hide it)
-            constexpr int JB = NW >= 16 ? 1 : 4;
-#pragma unroll
-            for (int j0 = 0; j0 < 4; j0 += JB) {
-                f32x4 part[JB][2];
-#pragma unroll
-                for (int jj = 0; jj < JB; ++jj) {
-                    const f16x8 wq = unpack_q8_sgpr(p[j0 + jj], magic);
-#pragma unroll
-                    for (int mt = 0; mt < 2; ++mt) {
-                        part[jj][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            fa[4 * q + j0 + jj][mt], wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    }
-                }
-#pragma unroll
-                for (int jj = 0; jj < JB; ++jj) {
-                    const uint16_t sbits = static_cast<uint16_t>(cur.s[q] >> (16 * (j0 + jj)));
-                    const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sbits));
-#pragma unroll
-                    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            acc[mt][r] = __builtin_fmaf(part[jj][mt][r], sf, acc[mt][r]);
-                        }
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                s_part[(wave * kMRows + mt * 16 + 4 * fg + r) * kNTile + fr] = acc[mt][r];
-            }
-        }
-        __syncthreads();
-        const int orow = tid >> 4;
-        const int ocol = tid & 15;
-        const int gm = mg0 + orow;
-        const int gn = (t_begin + tl) * kNTile + ocol;
-        if (orow < kMRows && gm < a.M && gn < a.N) {
-            float v = 0.f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                v += s_part[(w * kMRows + orow) * kNTile + ocol];
-            }
-            if (a.C) {
-                v += load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
-            }
-            if (a.bias) {
-                v += load_out<OUT>(a.bias, gn);
-            }
-            v = fmaxf(v, a.cmin);
-            v = fminf(v, a.cmax);
-            store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn, v);
-        }
-        __syncthreads();  // s_part is rewritten by the next tile
-    };
-    if constexpr (kAhead == 2) {
-        tile(0, r0, r2);
-        if (ntl > 1) {
-            tile(1, r1, r0);
-        }
-        if (ntl > 2) {
-            tile(2, r2, r1);
-        }
-        if (ntl > 3) {
-            tile(3, r0, r2);
-        }
-    } else {
-        tile(0, r0, r1);
-        if (ntl > 1) {
-            tile(1, r1, r0);
-        }
-        if (ntl > 2) {
-            tile(2, r0, r1);
-        }
-        if (ntl > 3) {
-            tile(3, r1, r0);
-        }
-    }
-}
-
-// One C / bias element loaded by asm (no compiler-placed wait; the caller waits with s_waitcnt and
-// ties the register with an empty asm): 32 bits for f32 outputs, the 16-bit pattern otherwise.
-template <int OUT>
-__device__ __forceinline__ uint32_t load_out_bits_async(const void *p, long long i)
-{
-    uint32_t v;
-    if constexpr (OUT == OUT_F32) {
-        asm volatile("global_load_dword %0, %1, off"
-                     : "=v"(v)
-                     : "v"(static_cast<const float *>(p) + i)
-                     : "memory");
-    } else {
-        asm volatile("global_load_ushort %0, %1, off"
-                     : "=v"(v)
-                     : "v"(static_cast<const uint16_t *>(p) + i)
-                     : "memory");
-    }
-    return v;
-}
-
-template <int OUT>
-__device__ __forceinline__ float out_bits_to_f32(uint32_t v)
-{
-    if constexpr (OUT == OUT_F32) {
-        return __builtin_bit_cast(float, v);
-    } else if constexpr (OUT == OUT_F16) {
-        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v)));
-    } else {
-        return bf16_bits_to_f32(static_cast<uint16_t>(v));
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
-// LDS-staged strip kernel (bl == 32, k 2048 or 4096): the strip kernel's math with the weight
-// stream moved off the registers. One workgroup of 16 wave64s per CU owns up to four consecutive
-// 16-channel tiles for one group of 32 activation rows; wave w keeps its k-slice of A (BPW 32-k
-// blocks) in registers and streams that same k-slice of every tile -- 16 channels x BPW blocks of
-// weights, 16 x BPW f16 scales -- into a three-slot LDS ring of its own with direct global -> LDS
-// loads, three tiles ahead. No wave reads another wave's ring, so a wave starts a tile as soon as
-// its own loads of it have landed and refills the slot as soon as it has read it.
-// What bounds it: every CU takes in all of A (256 KiB at k 4096) besides its tiles, and the CU
-// serves its waves' requests about group by group (four waves at a time), so the four wave
-// groups get their A slices microseconds apart. No wave therefore waits for another: each adds
-// its partials of a tile into that tile's f64 sums in LDS (ds_add_f64; the sum of 16 f32
-// partials is exact in f64, so the order of arrival does not change it) and counts itself in,
-// and goes on to its next tile; wave t finishes tile t (the f32 rounding of the sums, C, bias,
-// clamp, store) once all 16 have counted in. Waves 0-3 get their A first and finish their own
-// tiles first, so those epilogues overlap the slower waves' math. Every wave requests the first
-// half of its A, tile 0, the second half, then its next tiles.
-// Plain weights: one load instruction takes 8 channels x 128 B (whole lines), lane i fetching
-// block (i & 7) ^ (c & 7) of channel c = i / 8, so block b of channel c lies at 16-byte slot
-// b ^ (c & 7) of the channel's 128 bytes and a wave's ds_read_b128 of one block for 16 channels
-// hits distinct slots; a whole packed panel's k-slice is contiguous (2 KiB) and is copied as it
-// lies. Per tile: the strip kernel's decode, v_mfma_f32_16x16x32_f16 per block and scale FMA.
-// ---------------------------------------------------------------------------------------------
-
-// unpack_q8_sgpr with one shift instead of three: nibbles 1, 3 (5, 7) are inserted at bits 4-7
-// (20-23), giving 1024 + 16 q, and scaled back by an exact fma (h / 16 - 72 = q - 8).
+// permute_a's slot order k = 0, 4, 1, 5, 2, 6, 3, 7. Nibbles 0, 4 (2, 6) keep their place and
+// become 1024 + q; nibbles 1, 5 (3, 7) stay at bits 4-7 / 20-23 and become 1024 + 16 q, which
+// one exact fma scales back (h / 16 - 72 = q - 8).
 __device__ __forceinline__ f16x8 unpack_q8_lds(uint32_t x, uint32_t magic)
 {
     const f16x2 bias = f16x2{static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
@@ -630,33 +353,15 @@ __device__ __forceinline__ void wait_vm_upto(int n)
     asm volatile("" ::: "memory");
 }
 
-template <int K, int PK, int OUT>
-__global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
+template <int PK, int OUT, int NS>
+__global__ __launch_bounds__(1024) void w4a16_chunk_kernel(W4A16Args a, int nwg)
 {
-    constexpr int NW = 16;
-    constexpr int BPW = K / (32 * NW);        // 32-k blocks per wave (8 or 4)
-    constexpr int NG = BPW / 4;               // 4-block groups per wave
-    constexpr int HB = BPW / 2;               // blocks per half of the A slice
-    constexpr int CB = BPW * 16;              // weight bytes of one channel's k-slice
-    constexpr int WSLOT = kNTile * CB;        // weight bytes per wave per tile
-    constexpr int SSLOT = 256;                // scale bytes per wave per tile (one dword load)
-    constexpr int SLOT = WSLOT + SSLOT;
-    constexpr int NSLOT = 3;
-    constexpr int NDW = WSLOT / 1024 + 1;     // loads per wave per tile
-    constexpr int OUTS = kMRows * kNTile;     // outputs per tile
-    static_assert(K == 2048 || K == 4096, "LDS strip kernel k");
-    static_assert(kPackW4A16NStep == kNTile, "a packed weight panel is one tile");
-    static_assert(kMRows == 32 && kNTile == 16 && OUTS == 8 * 64, "8 outputs per lane per tile");
-    static_assert(kStripTiles * kNTile == 64, "one bias per lane of wave 0");
-    static_assert(NSLOT * NDW + BPW <= 23, "wait counts");
-    __shared__ __attribute__((aligned(16))) int8_t s_ring[NW][NSLOT][SLOT];
-    // A staging area of each wave (2 KiB, private)
-    __shared__ __attribute__((aligned(16))) int8_t s_stage[NW][2048];
-    // per tile of the strip: the 16 waves' partials summed in f64 (output (mt, r) of lane L at
-    // (4 mt + r) 64 + L: consecutive lanes, consecutive words) and how many waves added theirs
-    __shared__ __attribute__((aligned(16))) double s_acc[kStripTiles][OUTS];
-    __shared__ uint32_t s_arrived[kStripTiles];
-    __shared__ float s_bias[kStripTiles * kNTile];
+    static_assert(NS >= 2 && 4 * (NS - 1) <= 23, "ring depth");
+    static_assert(kCsWaves == kCsBlocks && kCsA == 2 * kCsWaves * 1024 &&
+                      kCsW == kCsWaves * 1024 && kCsS == 2 * 1024, "load roles");
+    static_assert(NS * kCsSlot >= kCsBlocks * kCsTiles * kMRows * kNTile * 4,
+                  "partials fit the ring");
+    __shared__ __attribute__((aligned(16))) int8_t s_ring[NS][kCsSlot];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -664,306 +369,213 @@ __global__ __launch_bounds__(1024) void w4a16_lds_kernel(W4A16Args a, int nwg)
     const int fr = lane & 15;
     const int fg = lane >> 4;
     const int mg0 = blockIdx.y * kMRows;
-
     const int t_begin = static_cast<int>((static_cast<long long>(blockIdx.x) * a.ntiles) / nwg);
     const int t_end = static_cast<int>((static_cast<long long>(blockIdx.x + 1) * a.ntiles) / nwg);
-    const int ntl = t_end - t_begin;  // 1 .. kStripTiles
-    const int npro = min(ntl, NSLOT);
+    const int ntl = t_end - t_begin;  // 1 .. kCsTiles
+    const int nch = a.K / kCsK;
 
-    // Zero the tiles' sums and arrival counts before any wave can add to them. The meeting comes
-    // before any load is issued: placed after them it would wait for the last wave's last issue,
-    // which the CU's address unit delays by microseconds while it takes every wave's loads.
-#pragma unroll
-    for (int i = tid; i < kStripTiles * OUTS; i += NW * 64) {
-        (&s_acc[0][0])[i] = 0.0;
-    }
-    if (tid < kStripTiles) {
-        s_arrived[tid] = 0u;
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-
-    // A slice of this wave, loaded by asm so that the compiler adds no wait for it: the waits
-    // below count these loads with the ring's (all of them in issue order).
-    u32x4 ra[BPW][2];
-    auto load_a = [&](int j) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            asm volatile("global_load_dwordx4 %0, %1, off"
-                         : "=v"(ra[j][mt])
-                         : "v"(a_slice_addr<BPW, PK>(a, mg0, wave, lane, j, mt))
-                         : "memory");
+    // This thread's outputs (local tile t = tid / 256, rows u / 16 and u / 16 + 16, column
+    // u % 16): bias and C read now, ahead of every ring load, so the epilogue waits for nothing.
+    const int et = tid >> 8;
+    const int erow = (tid >> 4) & 15;
+    const int gn = (t_begin + et) * kNTile + (tid & 15);
+    const bool out_col = et < ntl && gn < a.N;
+    float e_bias = 0.f, e_c[2] = {0.f, 0.f};
+    if (out_col) {
+        if (a.bias) {
+            e_bias = load_out<OUT>(a.bias, gn);
         }
-    };
+        if (a.C) {
 #pragma unroll
-    for (int j = 0; j < HB; ++j) {
-        load_a(j);
-    }
-    // The bias of every tile's 16 channels, loaded by wave 0 with A for the same reason as A (a
-    // compiler-placed wait for a load issued later would drain the whole ring; C, when given, is
-    // read that way in the epilogue, at that cost) and parked in LDS.
-    uint32_t rb = 0;
-    if (wave == 0 && a.bias) {
-        const int gn = (t_begin + (lane >> 4)) * kNTile + (lane & 15);
-        if ((lane >> 4) < ntl && gn < a.N) {
-            rb = load_out_bits_async<OUT>(a.bias, gn);
-        }
-    }
-
-    // Tiles whose weights are one whole packed panel (16 channels); a narrower last panel is
-    // gathered channel by channel like plain rows, into the plain slot layout.
-    auto packed_tile = [&](int t) { return (PK & PK_B) != 0 && (t + 1) * kNTile <= a.N; };
-    // This wave's k-slice of tile tl into its slot sl: NDW loads.
-    auto issue = [&](int tl, int sl) {
-        const int t = t_begin + tl;
-        int8_t *slot = &s_ring[wave][sl][0];
-#pragma unroll
-        for (int h = 0; h < WSLOT / 1024; ++h) {
-            const uint8_t *src;
-            if (packed_tile(t)) {
-                int wmul;
-                src = b_row_ptr<PK>(a, t * kNTile, wmul) + wave * (kNTile * CB) + h * 1024 +
-                      lane * 16;
-            } else {
-                int c, b;
-                if constexpr (BPW == 8) {
-                    c = 8 * h + (lane >> 3);
-                    b = (lane & 7) ^ (c & 7);
-                } else {
-                    c = lane >> 2;
-                    b = (lane & 3) ^ (c & 3);
+            for (int mt = 0; mt < 2; ++mt) {
+                const int gm = mg0 + mt * 16 + erow;
+                if (gm < a.M) {
+                    e_c[mt] = load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
                 }
-                const int n = min(t * kNTile + c, a.N - 1);
-                int wmul;
-                src = b_row_ptr<PK>(a, n, wmul) + static_cast<long long>(wave * BPW + b) * 16 * wmul;
             }
-            dma_lds16(reinterpret_cast<const int8_t *>(src), slot + h * 1024);
         }
-        // scales: channel c's BPW f16 at c * 2 BPW (lanes past the 16 channels repeat them)
-        constexpr int LPC = BPW / 2;  // lanes (dwords) per channel
-        const int c = (lane / LPC) & 15;
-        const int n = min(t * kNTile + c, a.N - 1);
-        dma_lds4(a.scale_b + static_cast<long long>(n) * a.ldsb + wave * BPW + (lane % LPC) * 2,
-                 slot + WSLOT);
+    }
+
+    // Load roles. Activations, two KiB per wave: plain rows 2w, 2w + 1 (lane i takes the row's
+    // chunk i ^ (r & 15)); packed panels chunk-major, so chunks 4w .. 4w + 3 of all 32 rows
+    // (lane i of load h takes chunk 4w + 2h + i / 32 of row i % 32: one contiguous KiB). Rows
+    // past m read row m - 1 (their outputs are not stored).
+    const uint8_t *a_src[2];
+    long long a_step;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        int amul;
+        if constexpr ((PK & PK_A) != 0) {
+            const int r = lane & 31;
+            const int ck = 4 * wave + 2 * h + (lane >> 5);
+            a_src[h] = a_row_ptr<PK>(a, min(mg0 + r, a.M - 1), amul) +
+                       static_cast<long long>(ck * 16) * amul;
+        } else {
+            const int r = 2 * wave + h;
+            a_src[h] = a_row_ptr<PK>(a, min(mg0 + r, a.M - 1), amul) +
+                       static_cast<long long>((lane ^ (r & 15)) * 16) * amul;
+        }
+        a_step = 1024ll * amul;  // bytes per chunk (the same for both loads)
+    }
+    // Weights: quarter p = w & 3 of tile w >> 2. A workgroup with fewer than four tiles loads
+    // its last tile again in place of the missing ones, so every wave issues the same loads for
+    // every chunk (and computes four tiles; the missing tiles' outputs are not stored).
+    const uint8_t *w_src;
+    long long w_step;
+    {
+        const int t = t_begin + min(wave >> 2, ntl - 1);
+        const int p = wave & 3;
+        int wmul;
+        if constexpr ((PK & PK_B) != 0) {
+            // packed chunk 4p + i / 16 of row i % 16: one contiguous KiB of a whole panel
+            const uint8_t *rb = b_row_ptr<PK>(a, min(t * kNTile + fr, a.N - 1), wmul);
+            w_src = rb + static_cast<long long>(16 * (4 * p + (lane >> 4))) * wmul;
+            w_step = 256ll * wmul;
+        } else {
+            // channel ch = 4p + i / 16, block (i % 16) ^ ch: four whole 256-byte row pieces
+            const int ch = 4 * p + (lane >> 4);
+            const uint8_t *rb = b_row_ptr<PK>(a, min(t * kNTile + ch, a.N - 1), wmul);
+            w_src = rb + 16 * ((lane & 15) ^ ch);
+            w_step = 256;
+        }
+    }
+    // Scales: waves 0 and 1, lane i -> channel i % 16 of tile i / 16, blocks 8w .. 8w + 7.
+    const _Float16 *s_src = a.scale_b;
+    if (wave < 2) {
+        const int t = min(t_begin + (lane >> 4), t_end - 1);
+        s_src = a.scale_b + static_cast<long long>(min(t * kNTile + fr, a.N - 1)) * a.ldsb +
+                8 * wave;
+    }
+    const bool s_role = wave < 2;
+
+    auto issue = [&](int c, int sl) {
+        int8_t *base = &s_ring[sl][0];
+        dma_lds16(reinterpret_cast<const int8_t *>(a_src[0] + c * a_step), base + wave * 2048);
+        dma_lds16(reinterpret_cast<const int8_t *>(a_src[1] + c * a_step),
+                  base + wave * 2048 + 1024);
+        dma_lds16(reinterpret_cast<const int8_t *>(w_src + c * w_step), base + kCsA + wave * 1024);
+        if (s_role) {
+            dma_lds16(reinterpret_cast<const int8_t *>(s_src + kCsBlocks * c),
+                      base + kCsA + kCsW + wave * 1024);
+        }
     };
 
-    // the first half of A, tile 0, the second half, then the next tiles: tile 0's first blocks
-    // compute while the second half lands
-    issue(0, 0);
+    // Compute role: block b = w of every chunk, every tile of the workgroup.
+    const int b = wave;
+    // rows 0-15 and 16-31 of chunk 4b + fg (plain: row-major, swizzled; packed: chunk-major)
+    const int a_off0 = (PK & PK_A) != 0 ? ((4 * b + fg) * 32 + fr) * 16
+                                        : (fr * 64 + ((4 * b + fg) ^ fr)) * 16;
+    const int a_off1 = a_off0 + ((PK & PK_A) != 0 ? 16 * 16 : 16 * 64 * 16);
+    int w_off[kCsTiles], s_off[kCsTiles];
 #pragma unroll
-    for (int j = HB; j < BPW; ++j) {
-        load_a(j);
-    }
-    for (int i = 1; i < npro; ++i) {
-        issue(i, i);
-    }
-    // In flight, oldest first: A[0, HB) + bias, tile 0 (NDW), A[HB, BPW) (BPW loads), tiles
-    // 1 .. npro - 1. First half of A in:
-    wait_vm_upto(npro * NDW + BPW);
-#pragma unroll
-    for (int j = 0; j < HB; ++j) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            asm volatile("" : "+v"(ra[j][mt]));
+    for (int t = 0; t < kCsTiles; ++t) {
+        if constexpr ((PK & PK_B) != 0) {
+            w_off[t] = kCsA + t * 4096 + ((4 * (b >> 2) + fg) * 16 + fr) * 16 + 4 * (b & 3);
+        } else {
+            w_off[t] = kCsA + t * 4096 + fr * 256 + ((b ^ fr) * 16) + 4 * fg;
         }
+        s_off[t] = kCsA + kCsW + (b >> 3) * 1024 + (t * kNTile + fr) * 16 + (b & 7) * 2;
     }
-    asm volatile("" : "+v"(rb));
-    if (wave == 0) {
-        // read by the wave that finishes a tile, which counts itself in after wave 0 did
-        s_bias[lane] = out_bits_to_f32<OUT>(rb);
-    }
-    // Rows past m hold a copy of row m - 1: they only reach output rows that are not stored.
-    // The empty asm keeps the fragments as computed (no re-permutation inside the tile loop).
-    int8_t *stage = &s_stage[wave][0];
-    f16x8 fa[BPW][2];
-    a_slice_to_mfma<BPW, PK, 0, HB>(ra, fa, stage, lane);
-#pragma unroll
-    for (int j = 0; j < HB; ++j) {
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            asm volatile("" : "+v"(fa[j][mt]));
-        }
-    }
-    // the second half, once it is in (tile 0 only)
-    auto second_half = [&]() {
-        wait_vm_upto((npro - 1) * NDW);
-#pragma unroll
-        for (int j = HB; j < BPW; ++j) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                asm volatile("" : "+v"(ra[j][mt]));
-            }
-        }
-        a_slice_to_mfma<BPW, PK, HB, BPW>(ra, fa, stage, lane);
-#pragma unroll
-        for (int j = HB; j < BPW; ++j) {
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                asm volatile("" : "+v"(fa[j][mt]));
-            }
-        }
-    };
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
 
-    // This lane's outputs of a tile (MFMA layout): rows mt * 16 + fg * 4 + r, column fr. D and C
-    // are addressed through buffer resources based at this workgroup's first row and ending at
-    // its last row (the launcher keeps 32 rows of either under 2^31 bytes): each output's offset
-    // is (row * ld + column) elements, and an output in a row past m or a column past n gets the
-    // resource's size as its offset, which the range check drops, so no output is guarded by a
-    // branch.
-    constexpr uint32_t kOutBytes = OUT == OUT_F32 ? 4u : 2u;
-    const uint32_t rows_here = static_cast<uint32_t>(min(kMRows, a.M - mg0));
-    const uint32_t d_bytes = rows_here * static_cast<uint32_t>(a.ldd) * kOutBytes;
-    const uint32_t c_bytes = rows_here * static_cast<uint32_t>(a.ldc) * kOutBytes;
-    const __amdgpu_buffer_rsrc_t d_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        static_cast<uint8_t *>(a.D) + static_cast<long long>(mg0) * a.ldd * kOutBytes, 0,
-        static_cast<int>(d_bytes), 0x00020000);
-    const __amdgpu_buffer_rsrc_t c_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void *>(a.C) == nullptr
-            ? static_cast<void *>(a.D)
-            : static_cast<uint8_t *>(const_cast<void *>(a.C)) +
-                  static_cast<long long>(mg0) * a.ldc * kOutBytes,
-        0, static_cast<int>(a.C ? c_bytes : 0u), 0x00020000);
+    f32x4 acc[kCsTiles][2];
+#pragma unroll
+    for (int t = 0; t < kCsTiles; ++t) {
+        acc[t][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int npro = min(NS - 1, nch);
+    for (int c = 0; c < npro; ++c) {
+        issue(c, c);
+    }
+#pragma unroll 1
+    for (int c = 0; c < nch; ++c) {
+        // this wave's loads of chunk c are in (later chunks may still be in flight), and every
+        // wave's reads of chunk c - 1 are done: meet, then refill chunk c - 1's slot
+        // (loads per chunk: 3, and 4 for the scale loaders; 0 pending after the last chunk)
+        const int ahead = min(NS - 2, nch - 1 - c);
+        if (ahead == 0) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm0(0));
+        } else if (s_role) {
+            wait_vm_upto(4 * ahead);
+        } else {
+            wait_vm_upto(3 * ahead);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (c + NS - 1 < nch) {
+            issue(c + NS - 1, (c + NS - 1) % NS);
+        }
+        const int8_t *slot = &s_ring[c % NS][0];
+        const f16x8 fa0 = permute_a(*reinterpret_cast<const u32x4 *>(slot + a_off0));
+        const f16x8 fa1 = permute_a(*reinterpret_cast<const u32x4 *>(slot + a_off1));
+        uint32_t wd[kCsTiles];
+        uint16_t sb[kCsTiles];
+#pragma unroll
+        for (int t = 0; t < kCsTiles; ++t) {
+            wd[t] = *reinterpret_cast<const uint32_t *>(slot + w_off[t]);
+            sb[t] = *reinterpret_cast<const uint16_t *>(slot + s_off[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < kCsTiles; ++t) {
+            const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sb[t]));
+            const f16x8 wq = unpack_q8_lds(wd[t], magic);
+            const f32x4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                fa0, wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            const f32x4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                fa1, wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc[t][0][r] = __builtin_fmaf(p0[r], sf, acc[t][0][r]);
+                acc[t][1][r] = __builtin_fmaf(p1[r], sf, acc[t][1][r]);
+            }
+        }
+    }
 
-    // One tile; tile 0 (FIRST, peeled off the loop) brings in the second half of A on the way.
-    auto tile = [&](int tl, auto first) {
-        constexpr bool FIRST = decltype(first)::value;
-        const int sl = tl % NSLOT;
-        // this wave's loads of tile tl have landed (later ones may still be in flight; for tile
-        // 0, the second half of A too)
-        wait_vm_upto(FIRST ? BPW + (npro - 1) * NDW : min(ntl - 1 - tl, NSLOT - 1) * NDW);
-        const int8_t *slot = &s_ring[wave][sl][0];
-        const bool panel = packed_tile(t_begin + tl);
-        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    // Partials of block b for local tile t: output (mt, r) of lane L at
+    // ((b * kCsTiles + t) * 8 + 4 mt + r) * 64 + L (consecutive lanes, consecutive words).
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    float *part = reinterpret_cast<float *>(&s_ring[0][0]);
 #pragma unroll
-        for (int q = 0; q < NG; ++q) {
-            if constexpr (FIRST) {
-                if (q == NG / 2) {
-                    second_half();  // before the first group that uses it
-                }
-            }
-            const int j = 4 * q + fg;
-            int off;
-            if constexpr (BPW == 8) {
-                off = panel ? j * 256 + fr * 16 : fr * CB + ((j ^ (fr & 7)) << 4);
-            } else {
-                off = panel ? j * 256 + fr * 16 : fr * CB + ((j ^ (fr & 3)) << 4);
-            }
-            const u32x4 wv = *reinterpret_cast<const u32x4 *>(slot + off);
-            const uint64_t sc =
-                *reinterpret_cast<const uint64_t *>(slot + WSLOT + fr * (2 * BPW) + q * 8);
-            uint32_t p[4] = {wv[0], wv[1], wv[2], wv[3]};
-            if constexpr ((PK & PK_B) == 0) {
-                transpose_lane_groups(p);  // packed weights are stored transposed already
-            }
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                f16x8 wq = unpack_q8_lds(p[jj], magic);
-                // this block's MFMAs after the previous block's FMAs: one block's partials live
-                // at a time (four waves per SIMD hide the MFMA -> FMA latency instead)
-                asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(wq));
-                const uint16_t sbits = static_cast<uint16_t>(sc >> (16 * jj));
-                const float sf = static_cast<float>(__builtin_bit_cast(_Float16, sbits));
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
-                    const f32x4 part = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        fa[4 * q + jj][mt], wq, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        acc[mt][r] = __builtin_fmaf(part[r], sf, acc[mt][r]);
-                    }
-                }
-            }
-        }
-        // this wave has read its slot (the MFMAs consumed it): refill it with the tile NSLOT
-        // ahead
-        if (tl + NSLOT < ntl) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue(tl + NSLOT, sl);
-        }
-        // Add this wave's partials into the tile's f64 sums and count the wave in; no wave waits
-        // for another. The sums of the 16 f32 partials are exact in f64 (unless their exponents
-        // span more than 25 binades), so the order in which the waves add does not change them.
-        double *sum = &s_acc[tl][0];
+    for (int t = 0; t < kCsTiles; ++t) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                __hip_atomic_fetch_add(&sum[(mt * 4 + r) * 64 + lane],
-                                       static_cast<double>(acc[mt][r]), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+                part[((b * kCsTiles + t) * 8 + 4 * mt + r) * 64 + lane] = acc[t][mt][r];
             }
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (lane == 0) {
-            __hip_atomic_fetch_add(&s_arrived[tl], 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-    };
-    // Tile tl's outputs, once all 16 waves have added their partials: the sums rounded to f32
-    // once, then C, bias, clamp. `counted`: false when the arrival wait gave up, and then every
-    // output of the tile is written as NaN, so a lost count-in cannot leave stale outputs.
-    // Each output's whole offset is the lane's vector offset (scalar offset 0): an output row
-    // past m or a column past n gets the resource's size, which the range check drops.
-    auto finish = [&](int tl, bool counted) {
-        const double *sum = &s_acc[tl][0];
-        const int gn = (t_begin + tl) * kNTile + fr;
-        const float bias = a.bias ? s_bias[tl * kNTile + fr] : 0.f;
-        const bool col_ok = gn < a.N;
-        // all eight sums read at once (one LDS round trip), rounded to f32
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            v[e] = static_cast<float>(sum[e * 64 + lane]);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t row = static_cast<uint32_t>(fg * 4 + (e >> 2) * 16 + (e & 3));
-            const bool ok = col_ok && row < rows_here;
-            const uint32_t d_off =
-                ok ? (row * static_cast<uint32_t>(a.ldd) + static_cast<uint32_t>(gn)) * kOutBytes
-                   : d_bytes;
-            float x = v[e];
-            if (a.C) {
-                const uint32_t c_off =
-                    ok ? (row * static_cast<uint32_t>(a.ldc) + static_cast<uint32_t>(gn)) * kOutBytes
-                       : c_bytes;
-                x += load_out_buf<OUT>(c_rsrc, c_off, 0u);
-            }
-            if (a.bias) {
-                x += bias;
-            }
-            x = fmaxf(x, a.cmin);
-            x = fminf(x, a.cmax);
-            store_out_buf<OUT>(d_rsrc, d_off, 0u,
-                               counted ? x : __builtin_bit_cast(float, 0x7fc00000u));
-        }
-    };
-    tile(0, std::true_type{});
-#pragma unroll 1
-    for (int tl = 1; tl < ntl; ++tl) {
-        tile(tl, std::false_type{});
     }
-    // Wave w < ntl finishes tile w once the last wave has counted itself in. Waves 0-3 get their
-    // A first and finish their own tiles first, so the tiles' epilogues overlap the slower
-    // waves' math; only the last tile's stays on the path. Every wave counts itself in for every
-    // tile without waiting for anyone, so the wait ends; the iteration cap only bounds it, and a
-    // tile whose count never completes is written as NaN (the parity checks then fail).
-    if (wave < ntl) {
-        uint32_t in = 0;
-        for (int it = 0; it < (1 << 24); ++it) {
-            in = __hip_atomic_load(&s_arrived[wave], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (in == NW) {
-                break;
+    __syncthreads();
+
+    if (out_col) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int gm = mg0 + mt * 16 + erow;
+            if (gm < a.M) {
+                const int idx = (4 * mt + (erow & 3)) * 64 + (erow >> 2) * 16 + (tid & 15);
+                double s = 0.0;
+#pragma unroll
+                for (int bb = 0; bb < kCsBlocks; ++bb) {
+                    s += static_cast<double>(part[(bb * kCsTiles + et) * 8 * 64 + idx]);
+                }
+                float v = static_cast<float>(s);
+                if (a.C) {
+                    v += e_c[mt];
+                }
+                if (a.bias) {
+                    v += e_bias;
+                }
+                v = fmaxf(v, a.cmin);
+                v = fminf(v, a.cmax);
+                store_out<OUT>(a.D, static_cast<long long>(gm) * a.ldd + gn, v);
             }
-            __builtin_amdgcn_s_sleep(1);
         }
-        asm volatile("" ::: "memory");
-        finish(wave, in == NW);
     }
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm0(0));
 }
 
 // Generic path: the reference test oracle's operation order, one thread per output
@@ -1069,35 +681,23 @@ void w4a16_run(size_t m, size_t n, size_t k, size_t bl, const void *A, size_t ld
     const bool fast = bl == 32 && k % 128 == 0 && k <= 128u * kWaves * kMaxGroupsPerWave &&
                       layout_fast && ldsb % 4 == 0 && aligned16(A) && aligned16(B) &&
                       (reinterpret_cast<uintptr_t>(scale_b) & 7u) == 0;
-    // (the strip kernels address 32 rows of D and C through 32-bit buffer offsets)
-    const bool strip = bl == 32 && (k == 2048 || k == 3072 || k == 4096) && layout_fast &&
-                       ldsb % 8 == 0 && aligned16(A) && aligned16(B) && aligned16(scale_b) &&
-                       ldd < (1ull << 24) && ldc < (1ull << 24);
-    if (strip) {
+    // bl 32 and k % 512 == 0: the chunk-stream kernel
+    const bool chunk = bl == 32 && k % kCsK == 0 && k >= kCsK && layout_fast && ldsb % 8 == 0 &&
+                       aligned16(A) && aligned16(B) && aligned16(scale_b);
+    if (chunk) {
         const int cus = device_cu_count();  // the current device, per call (no cached state)
-        const long long need = (a.ntiles + kStripTiles - 1) / kStripTiles;
+        const long long need = (a.ntiles + kCsTiles - 1) / kCsTiles;
         const long long nwg = need > cus ? need : (a.ntiles < cus ? a.ntiles : cus);
         const unsigned long long gy = (m + kMRows - 1) / kMRows;
         TQT_REQUIRE(gy < 65536 && nwg < (1ll << 31), "grid too large");
         const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(gy));
         const int nw = static_cast<int>(nwg);
-        // k 2048 / 4096: weights staged through LDS; k 3072: the register strip kernel (8 waves)
         if (packed) {
-            if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_lds_kernel<4096, PK_AB, OUT>), grid, dim3(1024), 0, s, a, nw);
-            } else if (k == 3072) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_AB, OUT, 8>), grid, dim3(512), 0, s, a, nw);
-            } else {
-                hipLaunchKernelGGL((w4a16_lds_kernel<2048, PK_AB, OUT>), grid, dim3(1024), 0, s, a, nw);
-            }
+            hipLaunchKernelGGL((w4a16_chunk_kernel<PK_AB, OUT, kCsRing>), grid, dim3(1024), 0, s,
+                               a, nw);
         } else {
-            if (k == 4096) {
-                hipLaunchKernelGGL((w4a16_lds_kernel<4096, PK_NONE, OUT>), grid, dim3(1024), 0, s, a, nw);
-            } else if (k == 3072) {
-                hipLaunchKernelGGL((w4a16_regs_kernel<3072, PK_NONE, OUT, 8>), grid, dim3(512), 0, s, a, nw);
-            } else {
-                hipLaunchKernelGGL((w4a16_lds_kernel<2048, PK_NONE, OUT>), grid, dim3(1024), 0, s, a, nw);
-            }
+            hipLaunchKernelGGL((w4a16_chunk_kernel<PK_NONE, OUT, kCsRing>), grid, dim3(1024), 0,
+                               s, a, nw);
         }
     } else if (fast) {
         const int cus = device_cu_count();  // the current device, per call (no cached state)
