@@ -586,7 +586,7 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
-                    help="comma-separated legs (w8a8,w4a8,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,"
+                    help="comma-separated legs (w8a8,w4a8,w4a8m2,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,"
                          "w4a16p,w4a8dq,conv,convp,clamp,copy,floor): "
                          "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
@@ -610,6 +610,7 @@ def main():
         legs = {
             "w8a8": lambda: bench_w8a8(torch, mod, lib, timer, W, K, rng),
             "w4a8": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1),
+            "w4a8m2": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 2),
             "w4a8m4": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 4),
             "w4a8m8": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 8),
             "w4a16": lambda: bench_w4a16(torch, mod, lib, timer, W, K, rng),

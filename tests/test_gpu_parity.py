@@ -120,9 +120,17 @@ W4A8_FAST_SHAPES = [(1, 160, 256, dict(bias=True)), (4, 100, 512, dict(bias=True
                     (2, 24, 65536, dict()),
                     # k % 256 != 0 goes to the per-output path
                     (15, 48, 384, dict(bias=True)), (33, 37, 640, dict(bias=True))]
+# Decode strip path (m = 1, k = 2048 or 4096): channel counts that leave a wave partly (n % 4)
+# or wholly (n % 16) past n, C, bias, clamps; m = 2-4 at the same k take the MFMA kernel.
+W4A8_STRIP_SHAPES = [(1, 1, 2048, dict()), (1, 5, 4096, dict(bias=True)),
+                     (1, 37, 2048, dict(c=True, bias=True, clamp=(-0.25, 0.5))),
+                     (1, 16, 4096, dict(c=True)), (1, 1000, 4096, dict(bias=True)),
+                     (2, 18, 4096, dict(c=True)), (3, 53, 4096, dict(bias=True)),
+                     (3, 64, 2048, dict(c=True, bias=True)), (4, 23, 4096, dict(clamp=(-1.0, 0.0))),
+                     (4, 1000, 2048, dict(bias=True))]
 
 
-@pytest.mark.parametrize("m,n,k,opt", W4A8_REF_SHAPES + W4A8_FAST_SHAPES)
+@pytest.mark.parametrize("m,n,k,opt", W4A8_REF_SHAPES + W4A8_FAST_SHAPES + W4A8_STRIP_SHAPES)
 def test_w4a8_parity(gpu, m, n, k, opt):
     d = T.gen_w4a8(m, n, k, seed=42 + k, with_c=opt.get("c", False),
                    with_bias=opt.get("bias", False))
@@ -141,6 +149,26 @@ def test_w4a8_extreme_values(gpu):
     d["A"][1, ::2] = 127
     d["Bp"][:] = 0x00
     d["Bp"][5:9] = 0xff
+    got = _gr().run_w4a8(d)
+    exp = T.oracle_w4a8(d["A"], d["Bp"], None, d["bias"], -np.inf, np.inf, d["scale_a"],
+                        d["zp_a"], d["scale_b"])
+    np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+@pytest.mark.parametrize("zp", [-128, 127, 2**31 - 1, -2**31])
+def test_w4a8_strip_extreme_values(gpu, zp):
+    """Decode strip path (m = 1) at its extremes: activations -128 / 127 against weights -8 / 7
+    (the nibble split's widest terms), zero points at the int8 and int32 limits (the zero-point
+    correction wraps in 32 bits as the reference's does), k = 4096."""
+    n, k = 40, 4096
+    d = T.gen_w4a8(1, n, k, seed=11, with_bias=True)
+    d["A"][:] = -128
+    d["A"][:, 1::2] = 127
+    d["zp_a"][0] = zp
+    d["Bp"][:] = 0x00
+    d["Bp"][3:7] = 0xff
+    d["Bp"][9] = 0x0f
+    d["Bp"][10] = 0xf0
     got = _gr().run_w4a8(d)
     exp = T.oracle_w4a8(d["A"], d["Bp"], None, d["bias"], -np.inf, np.inf, d["scale_a"],
                         d["zp_a"], d["scale_b"])
