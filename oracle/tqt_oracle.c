@@ -1094,34 +1094,6 @@ void tqto_quantize_a_per_row_asym(const float *A, size_t m, size_t k, int8_t *A_
     }
 }
 
-void tqto_quantize_b_per_channel_sym_int4(const float *B, size_t n, size_t k, uint8_t *B_packed,
-                                          float *scale_b)
-{
-    /* test/gemm/test_gemm_i8_i4_rvv.cpp:82-118 */
-    for (size_t row = 0; row < n; ++row) {
-        const float *r = B + row * k;
-        float abs_max = 0.0f;
-        for (size_t i = 0; i < k; ++i) {
-            const float v = fabsf(r[i]);
-            if (v > abs_max) {
-                abs_max = v;
-            }
-        }
-        float s = abs_max / 8.0f;
-        if (s == 0.0f) {
-            s = 1.0f;
-        }
-        scale_b[row] = s;
-        for (size_t kp = 0; kp < k / 2; ++kp) {
-            int32_t q0 = (int32_t)nearbyintf(r[2 * kp] / s);
-            int32_t q1 = (int32_t)nearbyintf(r[2 * kp + 1] / s);
-            q0 = q0 < -8 ? -8 : (q0 > 7 ? 7 : q0);
-            q1 = q1 < -8 ? -8 : (q1 > 7 ? 7 : q1);
-            B_packed[row * (k / 2) + kp] = (uint8_t)((q0 + 8) | ((q1 + 8) << 4));
-        }
-    }
-}
-
 void tqto_quantize_fp16_to_int4(size_t n, size_t k, size_t bl, const uint16_t *src,
                                 uint8_t *dst, uint16_t *scale, size_t ld_scale)
 {

@@ -182,9 +182,6 @@ void tqto_compute_sym_quant_params_i8(const float *data, size_t size, float *sca
 /* test/gemm/test_gemm_i8_i4_rvv.cpp:40-77 */
 void tqto_quantize_a_per_row_asym(const float *A, size_t m, size_t k, int8_t *A_i8,
                                   float *scale_a, int32_t *zp_a);
-/* test/gemm/test_gemm_i8_i4_rvv.cpp:82-118 */
-void tqto_quantize_b_per_channel_sym_int4(const float *B, size_t n, size_t k, uint8_t *B_packed,
-                                          float *scale_b);
 /* test/common/quantize_utils.h:34-72 (src and scale are f16 bit patterns) */
 void tqto_quantize_fp16_to_int4(size_t n, size_t k, size_t bl, const uint16_t *src,
                                 uint8_t *dst, uint16_t *scale, size_t ld_scale);

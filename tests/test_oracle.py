@@ -860,3 +860,117 @@ def test_per_row_quantize_properties_reject_planted_mistakes():
     for plant in (dict(scale_div=256.0), dict(zp_off=-127.0), dict(zp_off=0.0),
                   dict(round_zp=np.floor)):
         assert per_row_violations(X, *quantizer(**plant)), plant
+
+
+# ------------------------------------------------------------------------------------------
+# Tensor-wide quantization parameters of the reference runner
+# (test/common/quantized_gemm_test_runner.h:37-63 asymmetric, :67-86 symmetric)
+# ------------------------------------------------------------------------------------------
+
+def oracle_asym_params(x):
+    x = np.ascontiguousarray(x, np.float32)
+    s, z = ctypes.c_float(), ctypes.c_int32()
+    T.oracle().tqto_compute_asym_quant_params_i8(T.ptr(x), x.size, ctypes.byref(s),
+                                                 ctypes.byref(z))
+    return s.value, z.value
+
+
+def oracle_sym_param(x):
+    x = np.ascontiguousarray(x, np.float32)
+    s = ctypes.c_float()
+    T.oracle().tqto_compute_sym_quant_params_i8(T.ptr(x), x.size, ctypes.byref(s))
+    return s.value
+
+
+# Hand-worked inputs whose range is a binary-exact multiple of 255, so the scale is exact and
+# the zero point follows from nearbyint (half to even) and the -128 -> -127 rule alone.
+ASYM_KNOWN = [
+    ([0.0] * 5, 1.0, 0),                  # all zero: (1, 0)
+    ([-100.75, 3.0, 154.25], 1.0, -27),   # nearbyint(-27.25) = -27 (floor: -28)
+    ([-100.25, 154.75], 1.0, -28),        # nearbyint(-27.75) = -28 (truncation: -27)
+    ([-127.5, 127.5], 1.0, 0),            # nearbyint(-0.5) = -0 (half away from zero: -1)
+    ([-1.5, 253.5], 1.0, -126),           # nearbyint(-126.5) = -126 (half away: -127)
+    ([0.0, 17.0, 255.0], 1.0, -127),      # zp -128 becomes -127
+    ([2.0, 510.0], 2.0, -127),            # all >= 0: the minimum clamps to 0, then -128 -> -127
+    ([-510.0, -2.0], 2.0, 127),           # all <= 0: the maximum clamps to 0; -128 + 255
+    ([-63.75, 63.75], 0.5, 0),            # s = 127.5 / 255 = 0.5
+    ([-0.5, 63.25], 0.25, -126),          # s = 63.75 / 255 = 0.25; nearbyint(-128 + 2)
+]
+# Symmetric: s = 2 max|x| / 255 (1 for all zeros), whichever of the extremes is larger.
+SYM_KNOWN = [
+    ([0.0, 0.0, 0.0], 1.0),
+    ([-127.5, 3.0], 1.0),
+    ([1.0, 2.0, -255.0], 2.0),            # |min| > |max|
+    ([255.0, -1.0], 2.0),                 # |max| > |min|
+    ([-63.75, 63.75], 0.5),               # tie
+    ([0.5, 25.5], float(np.float32(51.0) / np.float32(255.0))),     # positives only
+    ([-25.5, -0.5], float(np.float32(51.0) / np.float32(255.0))),   # negatives only
+]
+
+
+def asym_known_failures(fn):
+    return [x for x, s, z in ASYM_KNOWN if fn(np.array(x, np.float32)) != (s, z)]
+
+
+def sym_known_failures(fn):
+    return [x for x, s in SYM_KNOWN if fn(np.array(x, np.float32)) != s]
+
+
+def test_asym_quant_params_known_answers():
+    assert asym_known_failures(oracle_asym_params) == []
+
+
+def test_sym_quant_params_known_answers():
+    assert sym_known_failures(oracle_sym_param) == []
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_quant_params_properties(seed):
+    """On random tensors: 255 s spans [min(x, 0), max(x, 0)] to f32 rounding, the zero point is
+    within half a step of -128 - min / s (or is the -127 that replaces -128) and maps real 0
+    exactly (golden-pinned quantize_i8); the symmetric scale covers max|x| with 127.5 steps."""
+    rng = np.random.default_rng(seed)
+    o = T.oracle()
+    for x in (rng.standard_normal(4096), rng.uniform(-3, 9, 1000), rng.uniform(0.5, 2, 300),
+              -rng.uniform(0.5, 2, 300), rng.standard_normal(77) * 1e5):
+        x = x.astype(np.float32)
+        lo, hi = min(float(x.min()), 0.0), max(float(x.max()), 0.0)
+        s, z = oracle_asym_params(x)
+        assert abs(255.0 * s - (hi - lo)) <= 4e-7 * (hi - lo)
+        assert -127 <= z <= 127
+        exact = -128.0 - lo / s
+        assert abs(z - exact) <= 0.5 + 1e-6 or (z == -127 and abs(-128 - exact) <= 0.5 + 1e-6)
+        assert int(o.tqto_quantize_i8(0.0, s, z)) == z
+        amax = float(np.abs(x).max())
+        ss = oracle_sym_param(x)
+        assert abs(127.5 * ss - amax) <= 4e-7 * amax
+
+
+def test_quant_params_known_answers_reject_planted_mistakes():
+    """The known answers have teeth: restatements with one step changed (numpy, f32) each miss
+    at least one of them, while the unplanted restatement meets all."""
+    f32 = np.float32
+
+    def asym(x, div=255.0, rnd=np.rint, rule=True, off=-128.0):
+        lo, hi = min(f32(x.min()), f32(0)), max(f32(x.max()), f32(0))
+        s = f32(f32(hi - lo) / f32(div))
+        if s == 0:
+            return 1.0, 0
+        z = int(rnd(f32(f32(off) - f32(lo / s))))
+        if rule and z == -128:
+            z = -127
+        return float(s), z
+
+    def sym(x, div=255.0, mode="both"):
+        a = {"both": max(abs(f32(x.max())), abs(f32(x.min()))), "max": abs(f32(x.max())),
+             "min": abs(f32(x.min()))}[mode]
+        s = f32(f32(2.0) * f32(a) / f32(div))
+        return float(s) if s != 0 else 1.0
+
+    assert asym_known_failures(asym) == []
+    for plant in (dict(div=256.0), dict(rnd=np.floor), dict(rnd=np.trunc), dict(rule=False),
+                  dict(off=-127.0), dict(rnd=lambda v: np.sign(v) * np.floor(abs(v) + 0.5))):
+        assert asym_known_failures(lambda x: asym(x, **plant)), plant
+    assert sym_known_failures(sym) == []
+    for plant in (dict(div=254.0), dict(mode="max"), dict(mode="min")):
+        assert sym_known_failures(lambda x: sym(x, **plant)), plant

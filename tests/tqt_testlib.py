@@ -137,7 +137,6 @@ def oracle():
         "tqto_compute_asym_quant_params_i8": (None, [c_vp, c_size, c_vp, c_vp]),
         "tqto_compute_sym_quant_params_i8": (None, [c_vp, c_size, c_vp]),
         "tqto_quantize_a_per_row_asym": (None, [c_vp, c_size, c_size, c_vp, c_vp, c_vp]),
-        "tqto_quantize_b_per_channel_sym_int4": (None, [c_vp, c_size, c_size, c_vp, c_vp]),
         "tqto_quantize_fp16_to_int4": (None, [c_size, c_size, c_size, c_vp, c_vp, c_vp, c_size]),
     }
     for name, (res, args) in sig.items():
