@@ -262,6 +262,13 @@ def load_support():
     sz, vp = ctypes.c_size_t, ctypes.c_void_p
     sup.tqtb_read_floor_async.restype = ctypes.c_int
     sup.tqtb_read_floor_async.argtypes = [vp, sz, vp, sz, ctypes.c_int, vp]
+    sup.tqtb_stream_floor_async.restype = ctypes.c_int
+    sup.tqtb_stream_floor_async.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, vp, sz, vp]
+    sup.tqtb_empty_async.restype = ctypes.c_int
+    sup.tqtb_empty_async.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp]
+    sup.tqtb_stream_lds_bytes.restype = ctypes.c_int
+    sup.tqtb_stream_lds_bytes.argtypes = []
     sup.tqtb_run_w4a16_async.restype = None
     sup.tqtb_run_w4a16_async.argtypes = ([sz] * 4 + [vp, sz, vp, sz, vp, sz, vp, sz, vp, sz, vp,
                                                     ctypes.c_uint16, ctypes.c_uint16, vp])
@@ -333,6 +340,116 @@ def bench_floor(torch, timer, warmup, steps, nbytes):
     ms = per_loads[best]
     return dict(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes, copies=nc, loads=best,
                 us_by_loads={b: round(v * 1e3, 3) for b, v in per_loads.items()})
+
+
+def bench_stream_floor(torch, timer, warmup, steps, resident=False):
+    """The W8A8 stream kernel's load schedule alone (tqtb_stream_floor_async: same grid, tile
+    order, LDS-DMA roles, four-slot ring, waits and barriers; no MFMA, no epilogue) on cfg 2's
+    A and B: the per-CU L2 -> LDS stream floor of that kernel's shape. Cold: rotating copies
+    like the W8A8 leg; resident: every workgroup reads the first tile's 192 rows (768 KiB, held
+    in each XCD's L2 after first touch)."""
+    sup = load_support()
+    m, n, k = W8A8["m"], W8A8["n"], W8A8["k"]
+    nc = 1 if resident else copies_for((m + n) * k)
+    dA = [torch.zeros((m, k), dtype=torch.int8, device="cuda") for _ in range(nc)]
+    dB = [torch.zeros((n, k), dtype=torch.int8, device="cuda") for _ in range(nc)]
+    sink_words = 8 * ((m // 64) * (n // 128) // 8 + 1)
+    sink = torch.zeros(sink_words, dtype=torch.int32, device="cuda")
+    s = timer.stream.cuda_stream
+
+    def launch(i):
+        if sup.tqtb_stream_floor_async(dA[i].data_ptr(), dB[i].data_ptr(), m, n, k,
+                                       1 if resident else 0, sink.data_ptr(), sink_words, s):
+            raise RuntimeError("stream floor launch failed")
+
+    ms = timer.run(launch, nc, warmup, steps)
+    per_cu = (64 + 128) * k
+    return dict(ms=ms, bytes=per_cu, copies=nc, per_cu_bytes=per_cu,
+                per_cu_gbs=per_cu / (ms * 1e-3) / 1e9)
+
+
+def bench_empty(torch, timer, warmup, steps):
+    """An empty kernel with the W8A8 stream kernel's launch shape (256 workgroups of 512
+    threads, its LDS size): the per-launch cost of that shape in a graph."""
+    sup = load_support()
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    lds = sup.tqtb_stream_lds_bytes() + 1536  # the ring and the multiplier arrays
+    s = timer.stream.cuda_stream
+
+    def launch(i):
+        if sup.tqtb_empty_async(256, lds, sink.data_ptr(), s):
+            raise RuntimeError("empty launch failed")
+
+    ms = timer.run(launch, 1, warmup, steps)
+    return dict(ms=ms, bytes=0, copies=1)
+
+
+def bench_caller(torch, mod, lib, kind, reps=5):
+    """The reference's caller pattern (test/common/quantized_gemm_test_runner.h:273-292,
+    examples/gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_rvv/...rvv.cpp:194-210): walk the output in
+    get_m_step() x get_n_step() tiles and call the synchronous run once per tile, with the
+    tile's operands found by the offset getters (and the per-row / per-channel parameter arrays
+    advanced to the tile, since a run indexes them from its own first row and column). kind:
+    "w8a8" (cfg 2) or "w4a8" (cfg 3, M = 1). Host wall clock over whole GEMMs, warm operands;
+    also the same tiles issued with the stream-ordered run and one synchronization per GEMM."""
+    rng = np.random.default_rng(3)
+    if kind == "w8a8":
+        m, n, k = W8A8["m"], W8A8["n"], W8A8["k"]
+        A, B, sb, bias, zp_a = inputs_w8a8(rng, m, n, k)
+        dA, dB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+        dsb, dbias = torch.from_numpy(sb).cuda(), torch.from_numpy(bias).cuda()
+        dD = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    else:
+        m, n, k = 1, W4A8["n"], W4A8["k"]
+        A, Bp, sa, za, sb, bias = inputs_w4a8(rng, m, n, k)
+        dA, dB = torch.from_numpy(A).cuda(), torch.from_numpy(Bp).cuda()
+        dsa, dza = torch.from_numpy(sa).cuda(), torch.from_numpy(za).cuda()
+        dsb, dbias = torch.from_numpy(sb).cuda(), torch.from_numpy(bias).cuda()
+        dD = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ms_, ns_ = lib.fn(kind, "get_m_step")(), lib.fn(kind, "get_n_step")()
+    a_off, b_off = lib.fn(kind, "get_a_offset"), lib.fn(kind, "get_b_offset")
+    bias_off, d_off = lib.fn(kind, "get_bias_offset"), lib.fn(kind, "get_d_offset")
+    tiles = []
+    for mi in range(0, m, ms_):
+        for ni in range(0, n, ns_):
+            am, an = min(ms_, m - mi), min(ns_, n - ni)
+            if kind == "w8a8":
+                p = mod.QAI8QSI8CXParams(0.02, zp_a, dsb.data_ptr() + 4 * ni, n, 0.05, 0)
+                args = (am, an, k, dA.data_ptr() + a_off(mi, 0, k), k, 0,
+                        dB.data_ptr() + b_off(ni, 0, k), k, 0, None, n,
+                        dD.data_ptr() + d_off(mi, ni, n), n, dbias.data_ptr() + bias_off(ni),
+                        -128, 127)
+            else:
+                p = mod.QAI8DXQSI4CXParams(dsa.data_ptr() + 4 * mi, dza.data_ptr() + 4 * mi,
+                                           dsb.data_ptr() + 4 * ni)
+                args = (am, an, k, dA.data_ptr() + a_off(mi, 0, k), k, 0,
+                        dB.data_ptr() + b_off(ni, 0, k), k, 0, None, n,
+                        dD.data_ptr() + d_off(mi, ni, n), n, dbias.data_ptr() + bias_off(ni),
+                        -math.inf, math.inf)
+            tiles.append((args, p))
+    run, run_async = lib.fn(kind, "run"), lib.fn(kind, "run_async")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def gemm_sync():
+        for args, p in tiles:
+            run(*args, ctypes.byref(p))
+
+    def gemm_async():
+        for args, p in tiles:
+            run_async(*args, ctypes.byref(p), stream)
+        torch.cuda.synchronize()
+
+    out = {}
+    for name, fn in (("sync", gemm_sync), ("async", gemm_async)):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        out[name] = (time.perf_counter() - t0) / reps
+    return dict(ms=out["sync"] * 1e3, ms_async=out["async"] * 1e3, calls=len(tiles),
+                m_step=ms_, n_step=ns_, bytes=0, copies=1)
 
 
 def bench_conv(torch, mod, lib, timer, warmup, steps, rng, packed=False):
@@ -587,7 +704,8 @@ def main():
                     help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs (w8a8,w4a8,w4a8m2,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,"
-                         "w4a16p,w4a8dq,conv,convp,clamp,copy,floor): "
+                         "w4a16p,w4a8dq,conv,convp,clamp,copy,floor,sfloor,sfloor_l2,empty,"
+                         "caller_w8a8,caller_w4a8): "
                          "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -623,14 +741,22 @@ def main():
             "clamp": lambda: bench_clamp(torch, mod, lib, timer, W, K, rng),
             "copy": lambda: bench_copy(torch, timer, W, K),
             "floor": lambda: bench_floor(torch, timer, W, K, W4A8_BYTES),
+            "sfloor": lambda: bench_stream_floor(torch, timer, W, K),
+            "sfloor_l2": lambda: bench_stream_floor(torch, timer, W, K, resident=True),
+            "empty": lambda: bench_empty(torch, timer, W, K),
+            "caller_w8a8": lambda: bench_caller(torch, mod, lib, "w8a8"),
+            "caller_w4a8": lambda: bench_caller(torch, mod, lib, "w4a8"),
         }
         with torch.cuda.stream(stream):
             for leg in args.only.split(","):
                 r = legs[leg]()
                 line = {"leg": leg, "us_per_launch": round(r["ms"] * 1e3, 3),
                         "bytes": r["bytes"], "copies": r["copies"]}
-                if "us_by_loads" in r:
-                    line["us_by_loads"] = r["us_by_loads"]
+                for key in ("us_by_loads", "calls", "m_step", "n_step", "per_cu_gbs"):
+                    if key in r:
+                        line[key] = r[key]
+                if "ms_async" in r:
+                    line["us_async"] = round(r["ms_async"] * 1e3, 3)
                 print(json.dumps(line), flush=True)
         return
 
@@ -656,6 +782,12 @@ def main():
         w4dq = progress("w4a8 decode step",
                         bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True))
         fl = progress("read floor", bench_floor(torch, timer, W, K, w4[1]["bytes"]))
+        sf = progress("w8a8 stream floor", bench_stream_floor(torch, timer, W, K))
+        sfr = progress("w8a8 stream floor L2-resident",
+                       bench_stream_floor(torch, timer, W, K, resident=True))
+        em = progress("empty launch", bench_empty(torch, timer, W, K))
+        cw8 = progress("reference caller w8a8", bench_caller(torch, mod, lib, "w8a8"))
+        cw4 = progress("reference caller w4a8", bench_caller(torch, mod, lib, "w4a8"))
 
     w41 = w4[1]
     traffic = None if args.no_traffic else hbm_traffic()
@@ -685,6 +817,24 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(w8["tops"], 3), "peak": INT8_PEAK_TOPS,
                      "unit": "TOPS", "frac": round(w8["tops"] / INT8_PEAK_TOPS, 4),
                      "traffic": tr["w8a8"], "algorithmic_bytes": w8["bytes"]},
+        # the W8A8 kernel's own load schedule alone (no MFMA, no epilogue), cold and with every
+        # workgroup reading one L2-resident tile, and an empty launch of its shape
+        "w8a8_floors": {
+            "stream_us": round(sf["ms"] * 1e3, 3),
+            "stream_per_cu_GBs": round(sf["per_cu_gbs"], 2),
+            "stream_l2_resident_us": round(sfr["ms"] * 1e3, 3),
+            "stream_l2_resident_per_cu_GBs": round(sfr["per_cu_gbs"], 2),
+            "per_cu_bytes": sf["per_cu_bytes"],
+            "empty_launch_us": round(em["ms"] * 1e3, 3),
+            "frac_of_stream_floor": round(sf["ms"] / w8["ms"], 4),
+        },
+        # the reference's caller pattern: one synchronous run per m_step x n_step tile
+        # (host wall clock per whole GEMM, warm operands), and the same tiles through the
+        # stream-ordered runs with one synchronization
+        "reference_caller": {
+            name: {"calls": r["calls"], "m_step": r["m_step"], "n_step": r["n_step"],
+                   "us_sync": round(r["ms"] * 1e3, 2), "us_async": round(r["ms_async"] * 1e3, 2)}
+            for name, r in (("w8a8 cfg2", cw8), ("w4a8 cfg3 M=1", cw4))},
         "w4a8": {
             "workload": "gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt M=1 K=4096 N=11008 (W4A8 decode)",
             "value": round(w41["gbs"], 2), "unit": "GB/s", "us_per_launch": round(w41["ms"] * 1e3, 3),

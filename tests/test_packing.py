@@ -203,24 +203,35 @@ def test_packed_sizes_equal_unpacked_sizes(lib, mod):
     assert g("w4a16fp", "get_a_packed_size")(m, k) == 2 * m * k
     assert g("w4a16fp", "get_b_packed_size")(n, k) == n * k // 2
     for kind in ("w4a16f", "w4a16fp"):
+        ms = _getter(lib, sym(mod, kind, "get_m_step"), 0)()
+        ns = _getter(lib, sym(mod, kind, "get_n_step"), 0)()
+        assert (ms, ns) == ((_getter(lib, sym(mod, "w4a16", "get_m_step"), 0)(),
+                             _getter(lib, sym(mod, "w4a16", "get_n_step"), 0)()) if kind == "w4a16f"
+                            else (_getter(lib, sym(mod, "w4a16p", "get_m_step"), 0)(),
+                                  _getter(lib, sym(mod, "w4a16p", "get_n_step"), 0)()))
         assert g(kind, "get_d_size")(m, n) == 4 * m * n
-        assert _getter(lib, sym(mod, kind, "get_c_offset"), 3)(32, 16, n) == 4 * (32 * n + 16)
-        assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(48) == 4 * 48
-        assert (_getter(lib, sym(mod, kind, "get_scale_b_offset"), 3)(16, 3, 128) ==
-                _getter(lib, sym(mod, "w4a16", "get_scale_b_offset"), 3)(16, 3, 128))
+        assert _getter(lib, sym(mod, kind, "get_c_offset"), 3)(ms, ns, n) == 4 * (ms * n + ns)
+        assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(3 * ns) == 4 * 3 * ns
+        base = "w4a16" if kind == "w4a16f" else "w4a16p"
+        assert (_getter(lib, sym(mod, kind, "get_scale_b_offset"), 3)(ns, 3, 128) ==
+                _getter(lib, sym(mod, base, "get_scale_b_offset"), 3)(ns, 3, 128))
     for kind in ("w8dynp", "w8dynhp"):
         assert g(kind, "get_a_packed_size")(m, k) == m * k
         assert g(kind, "get_b_packed_size")(n, k) == n * k
     for kind, es in (("w8dyn", 4), ("w8dynp", 4), ("w8dynh", 2), ("w8dynhp", 2)):
+        ms = _getter(lib, sym(mod, kind, "get_m_step"), 0)()
+        ns = _getter(lib, sym(mod, kind, "get_n_step"), 0)()
         assert g(kind, "get_d_size")(m, n) == es * m * n
-        assert _getter(lib, sym(mod, kind, "get_d_offset"), 3)(128, 128, n) == es * (128 * n + 128)
-        assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(256) == es * 256
+        assert _getter(lib, sym(mod, kind, "get_d_offset"), 3)(ms, ns, n) == es * (ms * n + ns)
+        assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(2 * ns) == es * 2 * ns
     for kind in ("w4a8h", "w4a8b", "w4a8hp", "w4a8bp"):
         assert g(kind, "get_d_size")(m, n) == 2 * m * n
         ms = _getter(lib, sym(mod, kind, "get_m_step"), 0)()
         ns = _getter(lib, sym(mod, kind, "get_n_step"), 0)()
-        assert (ms, ns) == (_getter(lib, sym(mod, "w4a8", "get_m_step"), 0)(),
-                            _getter(lib, sym(mod, "w4a8", "get_n_step"), 0)())
+        # each output-type sibling advertises its f32 type's steps (plain or packed)
+        base = "w4a8p" if kind.endswith("p") else "w4a8"
+        assert (ms, ns) == (_getter(lib, sym(mod, base, "get_m_step"), 0)(),
+                            _getter(lib, sym(mod, base, "get_n_step"), 0)())
         off = _getter(lib, sym(mod, kind, "get_d_offset"), 3)(3 * ms, 2 * ns, n)
         assert off == 2 * (3 * ms * n + 2 * ns)
         assert _getter(lib, sym(mod, kind, "get_bias_offset"), 1)(2 * ns) == 2 * 2 * ns

@@ -731,8 +731,10 @@ using namespace tqt;
 
 extern "C" {
 
+// Steps set only a caller's tile stride and the getters' alignment check (the run accepts any m
+// and n), so they are launch-sized: 32 rows by 16384 channels.
 static const size_t kW4A16MStep = 32;
-static const size_t kW4A16NStep = 16;
+static const size_t kW4A16NStep = 16384;
 
 size_t tqt_get_m_step_gemm_1xnbias_clamp_f16_f16_qsi4c2t_mfma_gfx950(void)
 {

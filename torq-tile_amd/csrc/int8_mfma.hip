@@ -2222,8 +2222,13 @@ using namespace tqt;
 // =============================================================================================
 extern "C" {
 
-static const size_t kClampMStep = 128;
-static const size_t kClampNStep = 128;
+// Steps of a non-packed type set only a caller's tile stride and the getters' alignment check
+// (the run accepts any m and n), so they are launch-sized: one step fills the GPU, and a caller
+// that walks m_step x n_step tiles the reference's way (test/common/gemm_test_runner.h:314-340)
+// makes one launch where 128 x 128 tiles took 128 synchronous calls (measured 3.0 ms against
+// 17.6 us for one W8A8 M512 call).
+static const size_t kClampMStep = 512;
+static const size_t kClampNStep = 4096;
 
 size_t tqt_get_m_step_gemm_clamp_i32_i8_i8_mfma_gfx950(void)
 {
@@ -2310,8 +2315,9 @@ void tqt_run_gemm_clamp_i32_i8_i8_mfma_gfx950(size_t m, size_t n, size_t k, cons
 // gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt (reference …qsi8cxt_4x1vl_rvv.cpp:26-198)
 // =============================================================================================
 
-static const size_t kReqMStep = 128;
-static const size_t kReqNStep = 128;
+// launch-sized steps (see kClampMStep)
+static const size_t kReqMStep = 512;
+static const size_t kReqNStep = 4096;
 
 size_t tqt_get_m_step_gemm_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxt_mfma_gfx950(void)
 {
@@ -2649,8 +2655,9 @@ void tqt_run_igemm_igemmcl_1xnbias_reqi32toi8_clamp_qai8_qai8_qsi8cxp_mfma_gfx95
 // gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8 (reference …/gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_4x1vl_rvv.cpp): weights A [m, k] (per-row
 // scale) times activations B [k, n], int32 C (optional) and Mx1 bias, per-row requantization
 // =============================================================================================
-static const size_t kMx1MStep = 128;
-static const size_t kMx1NStep = 128;
+// launch-sized steps (see kClampMStep)
+static const size_t kMx1MStep = 512;
+static const size_t kMx1NStep = 4096;
 
 size_t tqt_get_m_step_gemm_mx1bias_reqi32toi8_clamp_qai8_qsi8dx_qai8_mfma_gfx950(void)
 {
@@ -2993,8 +3000,9 @@ void tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx95
     finish_sync(nullptr, "tqt_run_igemm_igemmcf_mx1bias_reqi32toi8_clamp_qai8_qsi8dxp_qai8_mfma_gfx950");
 }
 
-static const size_t kDynMStep = 128;
-static const size_t kDynNStep = 128;
+// launch-sized steps (see kClampMStep)
+static const size_t kDynMStep = 512;
+static const size_t kDynNStep = 4096;
 
 // =============================================================================================
 // gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt (reference …/gemm_1xnbias_clamp_f32_qai8dx_qsi8cxt_4x1vl_rvv.cpp; kernel semantics
