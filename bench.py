@@ -213,8 +213,10 @@ def bench_w8a8(torch, mod, lib, timer, warmup, steps, rng, packed=False):
 
 def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m, packed=False, dynq=False):
     """packed: the qai8dxp_qsi4cxp sibling on the same inputs (packed once before timing).
-    dynq: each step is the decode pair "quantize the f32 activations on the GPU, then the W4A8
-    GEMV" (tqt_run_quantize_qai8dx_f32_gfx950 + the W4A8 run), both on the stream."""
+    dynq: each step is the decode step "quantize the f32 activations on the GPU, then the W4A8
+    GEMV": "fused" through tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950 (one
+    launch at M = 1), any other true value as the two launches (tqt_run_quantize_qai8dx_f32_gfx950
+    + the W4A8 run), both on the stream."""
     n, k = W4A8["n"], W4A8["k"]
     A, Bp, sa, za, sb, bias = inputs_w4a8(rng, m, n, k)
     nc = copies_for(Bp.nbytes)
@@ -237,6 +239,12 @@ def bench_w4a8(torch, mod, lib, timer, warmup, steps, rng, m, packed=False, dynq
         dAf = [torch.from_numpy(Af).cuda() for _ in range(nc)]
 
     def launch(i):
+        if dynq == "fused":
+            lib.quantize_gemm_async(m, n, k, dAf[i].data_ptr(), k, dA[i].data_ptr(), k,
+                                    dsa.data_ptr(), dza.data_ptr(), dB[i].data_ptr(), k, None, n,
+                                    dD.data_ptr(), n, dbias.data_ptr(), -math.inf, math.inf,
+                                    dsb.data_ptr(), s)
+            return
         if dynq:
             lib.quantize_async(m, k, dAf[i].data_ptr(), k, dA[i].data_ptr(), k, dsa.data_ptr(),
                                dza.data_ptr(), s)
@@ -704,7 +712,7 @@ def main():
                     help="time launches issued one by one on the stream instead of a HIP graph")
     ap.add_argument("--only", default=None,
                     help="comma-separated legs (w8a8,w4a8,w4a8m2,w4a8m4,w4a8m8,w4a16,w8a8p,w4a8p,"
-                         "w4a16p,w4a8dq,conv,convp,clamp,copy,floor,sfloor,sfloor_l2,empty,"
+                         "w4a16p,w4a8dq,w4a8dqf,conv,convp,clamp,copy,floor,sfloor,sfloor_l2,empty,"
                          "caller_w8a8,caller_w4a8): "
                          "time just those and print one JSON line each (profiling runs)")
     args = ap.parse_args()
@@ -736,6 +744,7 @@ def main():
             "w4a8p": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, packed=True),
             "w4a16p": lambda: bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True),
             "w4a8dq": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True),
+            "w4a8dqf": lambda: bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq="fused"),
             "conv": lambda: bench_conv(torch, mod, lib, timer, W, K, rng),
             "convp": lambda: bench_conv(torch, mod, lib, timer, W, K, rng, packed=True),
             "clamp": lambda: bench_clamp(torch, mod, lib, timer, W, K, rng),
@@ -779,8 +788,10 @@ def main():
                          bench_w4a16(torch, mod, lib, timer, W, K, rng, packed=True))
         cvp = progress("igemmcl packed", bench_conv(torch, mod, lib, timer, W, K, rng,
                                                     packed=True))
-        w4dq = progress("w4a8 decode step",
+        w4dq = progress("w4a8 decode step (two launches)",
                         bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq=True))
+        w4dqf = progress("w4a8 decode step (fused)",
+                         bench_w4a8(torch, mod, lib, timer, W, K, rng, 1, dynq="fused"))
         fl = progress("read floor", bench_floor(torch, timer, W, K, w4[1]["bytes"]))
         sf = progress("w8a8 stream floor", bench_stream_floor(torch, timer, W, K))
         sfr = progress("w8a8 stream floor L2-resident",
@@ -877,8 +888,11 @@ def main():
                 "us": round(w4p["ms"] * 1e3, 3), "GB/s": round(w4p["gbs"], 2),
                 "hbm_frac": round(w4p["gbs"] / HBM_PEAK_GBS, 4)},
             "W4A8 decode step with GPU activation quantization, M=1 K=4096 N=11008": {
-                "us": round(w4dq["ms"] * 1e3, 3), "GB/s": round(w4dq["gbs"], 2),
-                "hbm_frac": round(w4dq["gbs"] / HBM_PEAK_GBS, 4)},
+                "us": round(w4dqf["ms"] * 1e3, 3), "GB/s": round(w4dqf["gbs"], 2),
+                "hbm_frac": round(w4dqf["gbs"] / HBM_PEAK_GBS, 4),
+                "entry_point": "tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950 "
+                               "(one launch)",
+                "two_launches_us": round(w4dq["ms"] * 1e3, 3)},
             "packed f16p_qsi4c2p 32x14336x4096 bl32": {
                 "us": round(w416p["ms"] * 1e3, 3), "GB/s": round(w416p["gbs"], 2),
                 "hbm_frac": round(w416p["gbs"] / HBM_PEAK_GBS, 4)},

@@ -2,8 +2,10 @@
 oracle's restatement of the reference harness step (test/gemm/test_gemm_i8_i4_rvv.cpp:40-77,
 itself pinned to the reference's golden vectors in test_oracle.py): int8 values, scales and zero
 points bit-exact, on random rows, the special rows the formula branches on, round-half-even
-ties, unaligned and strided rows; and the decode pipeline quantize -> W4A8 GEMV against the
-oracle's pipeline."""
+ties, unaligned and strided rows; the decode pipeline quantize -> W4A8 GEMV against the
+oracle's pipeline; and the fused decode step
+(tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950: one launch at m = 1, k = 2048 or
+4096, else the two launches) against the same oracle pipeline, outputs and side outputs bit-exact."""
 
 import ctypes
 
@@ -134,3 +136,81 @@ def test_decode_pipeline_quantize_then_w4a8(gpu, m):
     eq, es, ez = oracle_quant(Af)
     exp = T.oracle_w4a8(eq, Bp, None, bias, -np.inf, np.inf, es, ez, sb)
     np.testing.assert_array_equal(dD.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+
+
+def run_fused(Af, Bp, sb, bias=None, C=None, cmin=-np.inf, cmax=np.inf, a_offset=0, ldq=None):
+    """The fused decode step on the GPU: (D, A_q, scale_a, zero_point_a)."""
+    import torch
+
+    m, k = Af.shape
+    n = Bp.shape[0]
+    ldq = k if ldq is None else ldq
+    src = np.zeros(a_offset + m * k, np.float32)
+    src[a_offset:] = Af.reshape(-1)
+    dA = _g().dev(src)
+    dB, dsb = _g().dev(Bp), _g().dev(sb)
+    dbias, dC = _g().dev(bias), _g().dev(C)
+    dQ = torch.full((m * ldq,), 77, dtype=torch.int8, device="cuda:0")
+    dS = torch.full((m,), -1.0, dtype=torch.float32, device="cuda:0")
+    dZ = torch.full((m,), 999, dtype=torch.int32, device="cuda:0")
+    dD = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+    _g().lib().quantize_gemm(m, n, k, dA.data_ptr() + 4 * a_offset, k, dQ.data_ptr(), ldq,
+                             dS.data_ptr(), dZ.data_ptr(), dB.data_ptr(), k, _g().dp(dC), n,
+                             dD.data_ptr(), n, _g().dp(dbias), float(cmin), float(cmax),
+                             dsb.data_ptr())
+    q = dQ.cpu().numpy().reshape(m, ldq)
+    if ldq > k:
+        assert (q[:, k:] == 77).all()
+    return dD.cpu().numpy(), q[:, :k], dS.cpu().numpy(), dZ.cpu().numpy()
+
+
+def check_fused(Af, Bp, sb, bias=None, C=None, cmin=-np.inf, cmax=np.inf, **kw):
+    D, q, s, z = run_fused(Af, Bp, sb, bias, C, cmin, cmax, **kw)
+    eq, es, ez = oracle_quant(Af)
+    np.testing.assert_array_equal(q, eq)
+    np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
+    np.testing.assert_array_equal(z, ez)
+    exp = T.oracle_w4a8(eq, Bp, C, bias, cmin, cmax, es, ez, sb)
+    np.testing.assert_array_equal(D.view(np.uint32), exp.view(np.uint32))
+
+
+def fused_inputs(m, n, k, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    Af = (rng.standard_normal((m, k)) * scale).astype(np.float32)
+    Bp = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    sb = rng.uniform(0.005, 0.02, size=n).astype(np.float32)
+    bias = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    return Af, Bp, sb, bias
+
+
+# (m, n, k, extra): m = 1 with k = 2048 / 4096 takes the one-launch kernel (n tails that leave
+# a wave partly or wholly past n, C, clamps, a strided A_q); the rest the two launches
+FUSED_CASES = [(1, 11008, 4096, {}), (1, 37, 2048, dict(c=True, clamp=(-0.3, 0.4))),
+               (1, 5, 4096, {}), (1, 1000, 2048, dict(c=True)), (1, 64, 4096, dict(ldq=4160)),
+               (3, 40, 4096, dict(c=True)), (1, 48, 1024, {}), (2, 17, 2048, {})]
+
+
+@pytest.mark.parametrize("m,n,k,opt", FUSED_CASES)
+def test_fused_decode_step(gpu, m, n, k, opt):
+    Af, Bp, sb, bias = fused_inputs(m, n, k, seed=m * 7 + k + n)
+    C = (np.random.default_rng(n).uniform(-1, 1, (m, n)).astype(np.float32)
+         if opt.get("c") else None)
+    cmin, cmax = opt.get("clamp", (-np.inf, np.inf))
+    check_fused(Af, Bp, sb, bias, C, cmin, cmax, ldq=opt.get("ldq"))
+
+
+def test_fused_decode_step_special_rows(gpu):
+    """The fused kernel's quantization branches: an all-zero row (scale 1, zero point 0, all-zero
+    values), a one-signed row (zero point -128), exact half-step ties (round half to even), and a
+    row whose f32 source is not 16-byte aligned (the two launches)."""
+    n, k = 40, 2048
+    _, Bp, sb, bias = fused_inputs(1, n, k, seed=5)
+    check_fused(np.zeros((1, k), np.float32), Bp, sb, bias)
+    pos = np.abs(np.random.default_rng(1).standard_normal((1, k))).astype(np.float32)
+    check_fused(pos, Bp, sb, bias)
+    ties = np.zeros((1, k), np.float32)
+    ties[0, 0], ties[0, 1] = -127.5, 127.5  # s = 1: x / s lands on .5 exactly
+    ties[0, 2:200] = np.arange(198, dtype=np.float32) * 0.5 - 49.5
+    check_fused(ties, Bp, sb, bias)
+    Af, _, _, _ = fused_inputs(1, n, k, seed=9)
+    check_fused(Af, Bp, sb, bias, a_offset=1)

@@ -27,6 +27,8 @@
 //     only what it wrote. Slices too large for that are loaded per step from global memory.
 // The eight waves' partial sums meet in LDS and the reference's f32 epilogue (zero-point
 // correction, two scale multiplies, C, bias, clamp; no FMA) runs per output.
+#include <cfloat>
+
 #include "tqt_hip_common.hpp"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950.h"
@@ -34,6 +36,8 @@
 #include "tqt_gemm_1xnbias_clamp_bf16_qai8dx_qsi4cxt_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_f16_qai8dxp_qsi4cxp_mfma_gfx950.h"
 #include "tqt_gemm_1xnbias_clamp_bf16_qai8dxp_qsi4cxp_mfma_gfx950.h"
+#include "tqt_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950.h"
+#include "tqt_quantize_qai8dx_gfx950.h"
 
 namespace tqt {
 namespace {
@@ -432,6 +436,41 @@ __device__ __forceinline__ uint32_t row16_sum_u32(uint32_t v)
     return v;
 }
 
+// Minimum / maximum of v over the 64 lanes, wave-uniform (exact: any order): DPP steps inside
+// each row of 16 lanes, then the four row results read by readlane. (With the same value in
+// both operands of v_permlane{16,32}_swap, the compiler dropped the min / max that combines the
+// swapped halves, so the rows are combined through scalar reads instead.)
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x)
+{
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
+}
+
+template <bool kMax>
+__device__ __forceinline__ float wave_minmax_f32(float v)
+{
+    auto op = [](float x, float y) { return kMax ? fmaxf(x, y) : fminf(x, y); };
+    v = op(v, dpp_f32<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_f32<0x4e>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_f32<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_f32<0x140>(v));  // row_mirror
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return op(op(r0, r1), op(r2, r3));
+}
+__device__ __forceinline__ float wave_min_f32(float v)
+{
+    return wave_minmax_f32<false>(v);
+}
+__device__ __forceinline__ float wave_max_f32(float v)
+{
+    return wave_minmax_f32<true>(v);
+}
+
 // Four per-lane values -> row c of the result holds the 64-lane sum of v[c] in every lane.
 __device__ __forceinline__ uint32_t wave_sum4_u32(const uint32_t (&v)[4])
 {
@@ -456,58 +495,17 @@ __device__ __forceinline__ void act_nibbles(uint32_t x0, uint32_t x1, uint32_t &
     l = (e & 0x0f0f0f0fu) | ((o << 4) & 0xf0f0f0f0u);
 }
 
+// The strip kernel's math and epilogue for one wave: its lanes' activation bytes av (load j:
+// k = 2048 j + 32 lane + 0..31), its channels' weight loads wv (channel n0 + c, load j), the
+// row's zero point and scale and this lane's epilogue operands (channel n0 + lane / 16).
 template <int L, int OUT>
-__global__ __launch_bounds__(kStripWaves * 64) void w4a8_strip_kernel(W4A8Args a)
+__device__ __forceinline__ void strip_finish(const W4A8Args &a, int n0, int lane,
+                                             const u32x4 (&av)[L][2], u32x4 (&wv)[kStripC][L],
+                                             int32_t zp, float p_sa, float p_sb, float p_bias,
+                                             float p_c)
 {
     static_assert(kStripC == 4, "one channel per row of 16 lanes");
     constexpr uint32_t kTerms = 32 * L;  // k values per lane
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int n0 = (blockIdx.x * kStripWaves + wave) * kStripC;
-    if (n0 >= a.N) {
-        return;  // a whole wave past the last channel (waves never wait for each other)
-    }
-
-    // the zero point (a wave-uniform scalar load: it waits on its own counter, so the vector
-    // loads below are not held behind it)
-    const int32_t zp = a.zp_a[0];
-    // activations first, then the weights, so that the activations are decoded while the
-    // weights stream (vector loads complete in order): load j holds the 32 bytes at
-    // k = 2048 j + 32 lane
-    u32x4 av[L][2];
-    const int8_t *ap = a.A + 32 * lane;
-#pragma unroll
-    for (int j = 0; j < L; ++j) {
-        av[j][0] = *reinterpret_cast<const u32x4 *>(ap + j * kStripK);
-        av[j][1] = *reinterpret_cast<const u32x4 *>(ap + j * kStripK + 16);
-    }
-    // weights: channel c, load j: 16 bytes at byte 1024 j + 16 lane of its row (channels past
-    // n reload the last channel)
-    u32x4 wv[kStripC][L];
-#pragma unroll
-    for (int c = 0; c < kStripC; ++c) {
-        const uint8_t *p =
-            a.B + static_cast<long long>(min(n0 + c, a.N - 1)) * a.bstride + 16 * lane;
-#pragma unroll
-        for (int j = 0; j < L; ++j) {
-            wv[c][j] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4 *>(p + j * (kStripK / 2)));
-        }
-    }
-    // keep every weight load ahead of what follows (the scheduler would sink them to their
-    // uses and serialize the stream); emits no instruction
-    asm volatile("" ::: "memory");
-
-    // epilogue operands of channel n0 + lane / 16 (stored by lane 16 c), requested behind the
-    // stream since they are needed last (channels past n read the last channel, not stored)
-    const int oc = lane >> 4;
-    const bool out_ok = (lane & 15) == 0 && n0 + oc < a.N;
-    const int gn = min(n0 + oc, a.N - 1);
-    const float p_sb = a.scale_b[gn];
-    const float p_sa = a.scale_a[0];
-    const float p_bias = a.bias ? load_out<OUT>(a.bias, gn) : 0.f;
-    const float p_c = a.C ? load_out<OUT>(a.C, gn) : 0.f;
-
     // activation nibbles and the constant 8 (zp n - S) of this lane
     uint32_t ah[L][4], al[L][4];
     int32_t sa = 0;
@@ -550,12 +548,181 @@ __global__ __launch_bounds__(kStripWaves * 64) void w4a8_strip_kernel(W4A8Args a
     }
     // acc - zp rsum of the reference (mod 2^32) of channel n0 + lane / 16
     const uint32_t tot = wave_sum4_u32(part);
-    if (out_ok) {
+    const int oc = lane >> 4;
+    if ((lane & 15) == 0 && n0 + oc < a.N) {
         store_out<OUT>(a.D, n0 + oc,
                        epilogue_f32(static_cast<int32_t>(tot), 0, 0, p_sa, p_sb,
                                     a.C ? &p_c : nullptr, a.bias ? &p_bias : nullptr, a.cmin,
                                     a.cmax));
     }
+}
+
+// This wave's weight loads: channel c, load j: 16 bytes at byte 1024 j + 16 lane of its row
+// (channels past n reload the last channel; their outputs are not stored).
+template <int L>
+__device__ __forceinline__ void strip_load_weights(const W4A8Args &a, int n0, int lane,
+                                                   u32x4 (&wv)[kStripC][L])
+{
+#pragma unroll
+    for (int c = 0; c < kStripC; ++c) {
+        const uint8_t *p =
+            a.B + static_cast<long long>(min(n0 + c, a.N - 1)) * a.bstride + 16 * lane;
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            wv[c][j] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(p + j * (kStripK / 2)));
+        }
+    }
+}
+
+template <int L, int OUT>
+__global__ __launch_bounds__(kStripWaves * 64) void w4a8_strip_kernel(W4A8Args a)
+{
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * kStripWaves + wave) * kStripC;
+    if (n0 >= a.N) {
+        return;  // a whole wave past the last channel (waves never wait for each other)
+    }
+
+    // the zero point (a wave-uniform scalar load: it waits on its own counter, so the vector
+    // loads below are not held behind it)
+    const int32_t zp = a.zp_a[0];
+    // activations first, then the weights, so that the activations are decoded while the
+    // weights stream (vector loads complete in order): load j holds the 32 bytes at
+    // k = 2048 j + 32 lane
+    u32x4 av[L][2];
+    const int8_t *ap = a.A + 32 * lane;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        av[j][0] = *reinterpret_cast<const u32x4 *>(ap + j * kStripK);
+        av[j][1] = *reinterpret_cast<const u32x4 *>(ap + j * kStripK + 16);
+    }
+    u32x4 wv[kStripC][L];
+    strip_load_weights<L>(a, n0, lane, wv);
+    // keep every weight load ahead of what follows (the scheduler would sink them to their
+    // uses and serialize the stream); emits no instruction
+    asm volatile("" ::: "memory");
+
+    // epilogue operands of channel n0 + lane / 16 (stored by lane 16 c), requested behind the
+    // stream since they are needed last (channels past n read the last channel, not stored)
+    const int gn = min(n0 + (lane >> 4), a.N - 1);
+    const float p_sb = a.scale_b[gn];
+    const float p_sa = a.scale_a[0];
+    const float p_bias = a.bias ? load_out<OUT>(a.bias, gn) : 0.f;
+    const float p_c = a.C ? load_out<OUT>(a.C, gn) : 0.f;
+    strip_finish<L, OUT>(a, n0, lane, av, wv, zp, p_sa, p_sb, p_bias, p_c);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Fused decode step (m = 1, k = 2048 or 4096): the row's qai8dx quantization and the strip
+// kernel in one launch. Each workgroup requests the f32 row (8 L floats per thread) ahead of its
+// weights, reduces the row's minimum and maximum (wave shuffles, then LDS across the four waves),
+// computes the scale and zero point exactly as tqt_run_quantize_qai8dx_f32 does, quantizes its
+// threads' values into an LDS copy of the int8 row, and after one more barrier each wave reads
+// its lanes' activation bytes from that copy and runs the strip math. Every workgroup computes
+// the same row (min and max are exact, the per-value steps are elementwise); workgroup 0 also
+// writes it, with its scale and zero point, to the caller's A_q, scale_a and zero_point_a. The
+// weight loads are in flight throughout. Measured (one box, M = 1, K 4096, N 11008): 7.49 us
+// against 8.3-8.5 us for the two launches and 5.6 us for the GEMV alone; the redundant per-
+// workgroup quantization is what remains (16 correctly rounded divisions per thread, about
+// 1 us: a copy with a plain conversion in their place took 6.5 us); a multiply by the rounded
+// reciprocal with a division only near rounding ties measured slower (8.0 us, divergent
+// branches), and shuffles through ds_bpermute for the min / max 0.1 us slower than DPP.
+// ---------------------------------------------------------------------------------------------
+template <int L, int OUT>
+__global__ __launch_bounds__(kStripWaves * 64) void w4a8_qstrip_kernel(W4A8Args a,
+                                                                       const float *X,
+                                                                       int8_t *Aq, float *sa_out,
+                                                                       int32_t *za_out)
+{
+    constexpr int kThreads = kStripWaves * 64;
+    constexpr int kF4 = kStripK * L / (4 * kThreads);  // float4 of the row per thread
+    __shared__ float s_lo[kStripWaves], s_hi[kStripWaves];
+    __shared__ __attribute__((aligned(16))) int8_t s_q[kStripK * L];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    // waves past the last channel still take part in the workgroup's barriers (they reload
+    // the last channel and store nothing)
+    const int n0 = (blockIdx.x * kStripWaves + wave) * kStripC;
+
+    // the f32 row first (its wait then leaves the weights in flight): float4 tid + 256 j
+    f32x4 xv[kF4];
+#pragma unroll
+    for (int j = 0; j < kF4; ++j) {
+        xv[j] = reinterpret_cast<const f32x4 *>(X)[tid + kThreads * j];
+    }
+    u32x4 wv[kStripC][L];
+    strip_load_weights<L>(a, n0, lane, wv);
+    asm volatile("" ::: "memory");
+    const int gn = min(n0 + (lane >> 4), a.N - 1);
+    const float p_sb = a.scale_b[gn];
+    const float p_bias = a.bias ? load_out<OUT>(a.bias, gn) : 0.f;
+    const float p_c = a.C ? load_out<OUT>(a.C, gn) : 0.f;
+
+    // the row's minimum and maximum (exact: any order)
+    float lo = FLT_MAX, hi = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < kF4; ++j) {
+        const f32x4 v = xv[j];
+        lo = fminf(lo, fminf(fminf(v[0], v[1]), fminf(v[2], v[3])));
+        hi = fmaxf(hi, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    }
+    lo = wave_min_f32(lo);
+    hi = wave_max_f32(hi);
+    if (lane == 0) {
+        s_lo[wave] = lo;
+        s_hi[wave] = hi;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    lo = s_lo[0];
+    hi = s_hi[0];
+#pragma unroll
+    for (int w = 1; w < kStripWaves; ++w) {
+        lo = fminf(lo, s_lo[w]);
+        hi = fmaxf(hi, s_hi[w]);
+    }
+    float s;
+    int32_t zp;
+    const bool nonzero = qai8dx_row_params(lo, hi, s, zp);
+    const float zpf = static_cast<float>(zp);
+    const bool writer = blockIdx.x == 0;
+#pragma unroll
+    for (int j = 0; j < kF4; ++j) {
+        uint32_t word = 0;
+        if (nonzero) {
+            const f32x4 v = xv[j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                word |= static_cast<uint32_t>(static_cast<uint8_t>(qai8dx_quantize(v[e], s, zpf)))
+                        << (8 * e);
+            }
+        }
+        const int i = tid + kThreads * j;
+        *reinterpret_cast<uint32_t *>(&s_q[4 * i]) = word;
+        if (writer) {
+            reinterpret_cast<uint32_t *>(Aq)[i] = word;
+        }
+    }
+    if (writer && tid == 0) {
+        sa_out[0] = s;
+        za_out[0] = zp;
+    }
+    // LDS stores visible to every wave; the weight loads stay in flight (a __syncthreads()
+    // would wait for them too)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    u32x4 av[L][2];
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        av[j][0] = *reinterpret_cast<const u32x4 *>(&s_q[j * kStripK + 32 * lane]);
+        av[j][1] = *reinterpret_cast<const u32x4 *>(&s_q[j * kStripK + 32 * lane + 16]);
+    }
+    strip_finish<L, OUT>(a, n0, lane, av, wv, zp, s, p_sb, p_bias, p_c);
 }
 
 // Launches the strip kernel when m and k suit it (m = 1, k = 2048 or 4096); false otherwise.
@@ -573,6 +740,25 @@ bool launch_w4a8_strip(const W4A8Args &a, hipStream_t s)
     case 2: hipLaunchKernelGGL((w4a8_strip_kernel<2, OUT>), grid, block, 0, s, a); return true;
     default: return false;
     }
+}
+
+// Launches the fused decode step when it applies (m = 1, k = 2048 or 4096); false otherwise.
+template <int OUT>
+bool launch_w4a8_qstrip(const W4A8Args &a, const float *X, int8_t *Aq, float *sa, int32_t *za,
+                        hipStream_t s)
+{
+    if (a.M != 1 || a.K % kStripK != 0 || a.K / kStripK > 2) {
+        return false;
+    }
+    const int per_block = kStripWaves * kStripC;
+    const dim3 grid(static_cast<unsigned>((a.N + per_block - 1) / per_block));
+    const dim3 block(kStripWaves * 64);
+    if (a.K == kStripK) {
+        hipLaunchKernelGGL((w4a8_qstrip_kernel<1, OUT>), grid, block, 0, s, a, X, Aq, sa, za);
+    } else {
+        hipLaunchKernelGGL((w4a8_qstrip_kernel<2, OUT>), grid, block, 0, s, a, X, Aq, sa, za);
+    }
+    return true;
 }
 
 // Generic path: one thread per output, any alignment, any even k.
@@ -830,6 +1016,79 @@ void tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950(
         m, n, k, A_packed, lda, k_idx_a, B_packed, ldb, k_idx_b, C, ldc, D, ldd, bias, clamp_min,
         clamp_max, params, nullptr);
     finish_sync(nullptr, "tqt_run_gemm_1xnbias_clamp_f32_qai8dxp_qsi4cxp_mfma_gfx950");
+}
+
+// The fused decode step (include/tqt_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950.h):
+// tqt_run_quantize_qai8dx_f32 of A into A_q, scale_a, zero_point_a, then the W4A8 GEMV on them,
+// in one launch when m = 1 and k = 2048 or 4096 (16-byte aligned A and B, 4-byte aligned A_q,
+// ldb / 2 a multiple of 16), else as those two launches; the results are the same either way.
+void tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950_async(
+    size_t m, size_t n, size_t k, const float *A, size_t lda, int8_t *A_q, size_t lda_q,
+    float *scale_a, int32_t *zero_point_a, const void *B, size_t ldb, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, float clamp_min, float clamp_max,
+    const float *scale_b, void *stream)
+{
+    static const char *where = "tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950";
+    if (m == 0) {
+        return;
+    }
+    TQT_REQUIRE(k % 2 == 0, "k % 2 == 0");
+    TQT_REQUIRE(m < (1u << 31) && n < (1u << 31) && k < (1u << 31), "dimension exceeds 2^31-1");
+    TQT_REQUIRE(scale_a != nullptr && zero_point_a != nullptr && (scale_b != nullptr || n == 0),
+                "scale_a / zero_point_a / scale_b == NULL");
+    TQT_REQUIRE((A != nullptr && A_q != nullptr && (B != nullptr || n == 0)) || k == 0,
+                "A / A_q / B == NULL");
+    TQT_REQUIRE(D != nullptr || n == 0, "D == NULL");
+    TQT_REQUIRE(lda >= k && lda_q >= k, "lda or lda_q < k");
+    const hipStream_t s = as_stream(stream);
+    if (n > 0 && m == 1 && aligned16(A) && aligned16(B) && (reinterpret_cast<uintptr_t>(A_q) & 3) == 0 &&
+        (ldb / 2) % 16 == 0) {
+        W4A8Args a = {};
+        a.M = 1;
+        a.N = static_cast<int>(n);
+        a.K = static_cast<int>(k);
+        a.A = A_q;
+        a.lda = static_cast<long long>(lda_q);
+        a.B = static_cast<const uint8_t *>(B);
+        a.bstride = static_cast<long long>(ldb / 2);
+        a.C = C;
+        a.ldc = static_cast<long long>(ldc);
+        a.D = D;
+        a.ldd = static_cast<long long>(ldd);
+        a.bias = bias;
+        a.cmin = clamp_min;
+        a.cmax = clamp_max;
+        a.scale_a = scale_a;
+        a.zp_a = zero_point_a;
+        a.scale_b = scale_b;
+        if (launch_w4a8_qstrip<OUT_F32>(a, A, A_q, scale_a, zero_point_a, s)) {
+            check_launch(where);
+            return;
+        }
+    }
+    tqt_run_quantize_qai8dx_f32_gfx950_async(m, k, A, lda, A_q, lda_q, scale_a, zero_point_a,
+                                             stream);
+    if (n > 0) {
+        const struct tqt_qai8dx_qsi4cx_params p = {scale_a, zero_point_a, scale_b};
+        tqt_run_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_mfma_gfx950_async(
+            m, n, k, A_q, lda_q, 0, B, ldb, 0, C, ldc, D, ldd, bias, clamp_min, clamp_max, &p,
+            stream);
+    }
+}
+
+void tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950(
+    size_t m, size_t n, size_t k, const float *A, size_t lda, int8_t *A_q, size_t lda_q,
+    float *scale_a, int32_t *zero_point_a, const void *B, size_t ldb, const void *C, size_t ldc,
+    void *D, size_t ldd, const void *bias, float clamp_min, float clamp_max,
+    const float *scale_b)
+{
+    if (m == 0) {
+        return;
+    }
+    tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950_async(
+        m, n, k, A, lda, A_q, lda_q, scale_a, zero_point_a, B, ldb, C, ldc, D, ldd, bias,
+        clamp_min, clamp_max, scale_b, nullptr);
+    finish_sync(nullptr, "tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950");
 }
 
 // =============================================================================================

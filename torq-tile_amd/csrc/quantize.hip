@@ -24,10 +24,7 @@ constexpr int kQCache = 4;  // float4 per thread kept in registers (rows of k <=
 
 __device__ __forceinline__ int8_t quantize_one(float x, float s, float zpf)
 {
-    float q = __builtin_rintf(x / s) + zpf;  // rint: round half to even
-    q = q > 127.0f ? 127.0f : q;
-    q = q < -128.0f ? -128.0f : q;
-    return static_cast<int8_t>(q);
+    return qai8dx_quantize(x, s, zpf);
 }
 
 __global__ __launch_bounds__(kQThreads) void quantize_qai8dx_kernel(
@@ -88,10 +85,9 @@ __global__ __launch_bounds__(kQThreads) void quantize_qai8dx_kernel(
         lo = fminf(lo, s_min[w]);
         hi = fmaxf(hi, s_max[w]);
     }
-    hi = hi > 0.0f ? hi : 0.0f;
-    lo = lo < 0.0f ? lo : 0.0f;
-    const float s = (hi - lo) / 255.0f;
-    if (s == 0.0f) {
+    float s;
+    int32_t zp;
+    if (!qai8dx_row_params(lo, hi, s, zp)) {
         if (tid == 0) {
             scale_a[row] = 1.0f;
             zp_a[row] = 0;
@@ -101,8 +97,6 @@ __global__ __launch_bounds__(kQThreads) void quantize_qai8dx_kernel(
         }
         return;
     }
-    int32_t zp = static_cast<int32_t>(__builtin_rintf(-128.0f - lo / s));
-    zp = zp < -128 ? -128 : (zp > 127 ? 127 : zp);
     if (tid == 0) {
         scale_a[row] = s;
         zp_a[row] = zp;

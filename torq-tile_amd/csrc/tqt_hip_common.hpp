@@ -539,4 +539,37 @@ __device__ __forceinline__ int8_t requant_dev(int32_t acc, int32_t mult, int32_t
     return static_cast<int8_t>(requant_clamped_dev(acc, mult, shift, zp, min(cmin, cmax), cmax));
 }
 
+// ---------------------------------------------------------------------------------------------
+// qai8dx: dynamic per-row asymmetric int8 quantization of f32 activations (reference test-side
+// quantize_a_per_row_asym, test/gemm/test_gemm_i8_i4_rvv.cpp:40-77, with quantize_i8 from
+// test/common/test_common.h:232-240), in float arithmetic with correctly rounded divisions and
+// round-half-even nearbyint (the library is built with -ffp-contract=off).
+// ---------------------------------------------------------------------------------------------
+
+// Scale and zero point of a row from its minimum and maximum; false when the scale is 0 (then
+// the row quantizes to scale 1, zero point 0 and all-zero values).
+__device__ __forceinline__ bool qai8dx_row_params(float lo, float hi, float &s, int32_t &zp)
+{
+    hi = hi > 0.0f ? hi : 0.0f;
+    lo = lo < 0.0f ? lo : 0.0f;
+    s = (hi - lo) / 255.0f;
+    if (s == 0.0f) {
+        s = 1.0f;
+        zp = 0;
+        return false;
+    }
+    zp = static_cast<int32_t>(__builtin_rintf(-128.0f - lo / s));
+    zp = zp < -128 ? -128 : (zp > 127 ? 127 : zp);
+    return true;
+}
+
+// One value: clamp(nearbyint(x / s) + zp, -128, 127) (rint: round half to even).
+__device__ __forceinline__ int8_t qai8dx_quantize(float x, float s, float zpf)
+{
+    float q = __builtin_rintf(x / s) + zpf;
+    q = q > 127.0f ? 127.0f : q;
+    q = q < -128.0f ? -128.0f : q;
+    return static_cast<int8_t>(q);
+}
+
 }  // namespace tqt

@@ -216,6 +216,12 @@ class Lib:
         # dynamic per-row activation quantization (include/tqt_quantize_qai8dx_gfx950.h)
         self.quantize = self._fns["tqt_run_quantize_qai8dx_f32_gfx950"]
         self.quantize_async = self._fns["tqt_run_quantize_qai8dx_f32_gfx950_async"]
+        # the fused decode step: quantization + W4A8 GEMV
+        # (include/tqt_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950.h)
+        self.quantize_gemm = self._fns[
+            "tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950"]
+        self.quantize_gemm_async = self._fns[
+            "tqt_run_quantize_gemm_1xnbias_clamp_f32_qai8dx_qsi4cxt_gfx950_async"]
 
     def fn(self, kind, action):
         return self._fns[_sym(kind, action)]
