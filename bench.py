@@ -545,7 +545,7 @@ def leg_of_kernel(name):
     """Which bench leg a (demangled) kernel name belongs to, for the legs in PMC_LEGS."""
     if "bitwise_not" in name:
         return "copy"
-    if "w4a8_mfma_kernel" in name:
+    if "w4a8_mfma_kernel" in name or "w4a8_strip_kernel" in name:
         return "w4a8"
     if "w4a16_" in name:
         return "w4a16"

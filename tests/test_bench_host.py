@@ -18,6 +18,10 @@ NS = "tqt::(anonymous namespace)::"
     ("void %sint8_stream_kernel<128, 1, 0, true>(%sInt8Args, int, int, int)" % (NS, NS), "conv"),
     ("void %sint8_stream_kernel<64, 1, 0, false>(%sInt8Args, int, int, int)" % (NS, NS), "w8a8"),
     ("void %sw4a8_mfma_kernel<1, 0, 0>(%sW4A8Args)" % (NS, NS), "w4a8"),
+    ("void %sw4a8_strip_kernel<2, 0>(%sW4A8Args)" % (NS, NS), "w4a8"),
+    # the fused decode step is not one of the traffic legs
+    ("void %sw4a8_qstrip_kernel<2, 0>(%sW4A8Args, float const*, signed char*, float*, int*)"
+     % (NS, NS), None),
     ("void %sw4a16_chunk_kernel<0, 1, 3>(%sW4A16Args, int)" % (NS, NS), "w4a16"),
     ("void at::native::vectorized_elementwise_kernel<4, at::native::bitwise_not_kernel_cuda>",
      "copy"),
