@@ -42,6 +42,20 @@ def test_clamp_i32_parity(gpu, m, n, k, with_c):
         np.testing.assert_array_equal(got, exp)
 
 
+# The small-problem kernel (32 x 32 tiles, k split over the four waves; M, N multiples of 32,
+# k % 128 == 0, k <= 2048, few regular tiles): one to sixteen 32-k steps per wave, with and
+# without C, full-range and narrow clamps (and an inverted one: max then min leaves cmax).
+@pytest.mark.parametrize("m,n,k,with_c", [(32, 32, 128, False), (32, 160, 384, True),
+                                          (96, 64, 2048, True), (64, 256, 1152, False),
+                                          (128, 96, 256, True)])
+def test_clamp_i32_small_kernel(gpu, m, n, k, with_c):
+    A, B, C = T.gen_clamp(m, n, k, seed=m + n + k, with_c=with_c)
+    for cmin, cmax in [(-2**31, 2**31 - 1), (-50000, 70000), (1000, -1000)]:
+        got = _gr().run_clamp(A, B, C, cmin, cmax)
+        exp = T.oracle_clamp(A, B, C, cmin, cmax)
+        np.testing.assert_array_equal(got, exp)
+
+
 def test_clamp_i32_config1(gpu):
     """BASELINE cfg 1: A [64,512], B [512,256] uniform in [-128,127], no C, full int32 clamp."""
     A, B, C = T.gen_clamp(64, 256, 512, seed=42)

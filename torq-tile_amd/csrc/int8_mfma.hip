@@ -1876,6 +1876,114 @@ bool halo_plan(const Int8Args &a, bool packed, HaloPlan &hp)
     return true;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Small clamp_i32 problems ([k, n] B; M, N multiples of 32, k % 128 == 0, k <= 2048) that would
+// give int8_mfma_kernel's 64 x 128 tiles only a few workgroups (the reference's shape list and
+// the 64 x 256 x 512 configuration: 2): 32 x 32 output tiles, and the four waves of a workgroup
+// split k, so every load of the workgroup is issued at once. Wave w takes k in
+// [w k / 4, (w + 1) k / 4): A fragments straight from global memory (lane (r, h): 16 bytes of
+// row r per 32-k step), B rows (32 columns x 32 bytes) loaded whole and transposed byte by byte
+// into the wave's own [n][k] LDS block, read back as the MFMA's 16-k column slices;
+// v_mfma_i32_32x32x32_i8. The four int32 partial tiles are added in LDS (exact: wrapping int32),
+// then C, the reference's max-then-min clamp, int32 stores.
+// ---------------------------------------------------------------------------------------------
+constexpr int kSmallT = 32;                    // output tile edge
+constexpr int kSmallMaxK = 2048;               // k per workgroup
+constexpr int kSmallKW = kSmallMaxK / 4;       // k per wave at most
+constexpr int kSmallPitch = kSmallKW + 16;     // bytes per LDS column row (16-byte aligned)
+
+__global__ __launch_bounds__(256) void int8_small_clamp_kernel(Int8Args a)
+{
+    __shared__ __attribute__((aligned(16))) int8_t s_b[4][kSmallT][kSmallPitch];
+    __shared__ __attribute__((aligned(16))) int32_t s_part[4][kSmallT * kSmallT];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int tiles_n = a.N / kSmallT;
+    const int m0 = (blockIdx.x / tiles_n) * kSmallT;
+    const int n0 = (blockIdx.x % tiles_n) * kSmallT;
+    const int kw = a.K / 4;          // a multiple of 32
+    const int k0 = wave * kw;
+    const int steps = kw / 32;       // 1 .. 16
+    const int r32 = lane & 31;
+    const int h = lane >> 5;
+
+    // A fragments of this wave's k-slice, and its B rows (lane: row k0 + 32 it + lane / 2,
+    // columns n0 + 16 (lane & 1) .. + 15), all requested before any is used
+    i32x4 fa[kSmallKW / 32];
+    i32x4 bb[kSmallKW / 32];
+    const int8_t *arow = a.A + static_cast<long long>(m0 + r32) * a.lda + k0 + 16 * h;
+    const int8_t *bcol = a.B + static_cast<long long>(k0 + (lane >> 1)) * a.ldb + n0 + 16 * (lane & 1);
+#pragma unroll
+    for (int st = 0; st < kSmallKW / 32; ++st) {
+        if (st < steps) {
+            fa[st] = *reinterpret_cast<const i32x4 *>(arow + 32 * st);
+            bb[st] = *reinterpret_cast<const i32x4 *>(bcol + static_cast<long long>(32 * st) * a.ldb);
+        }
+    }
+    // B transposed into this wave's [n][k] block: byte j of the lane's chunk is column
+    // 16 (lane & 1) + j of row 32 st + lane / 2
+    int8_t(*sb)[kSmallPitch] = s_b[wave];
+#pragma unroll
+    for (int st = 0; st < kSmallKW / 32; ++st) {
+        if (st < steps) {
+            const int kk = 32 * st + (lane >> 1);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                sb[16 * (lane & 1) + j][kk] =
+                    static_cast<int8_t>(static_cast<uint32_t>(bb[st][j >> 2]) >> (8 * (j & 3)));
+            }
+        }
+    }
+    // the wave reads back only what it wrote: its own LDS stores are in order, no barrier
+    i32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        acc[r] = 0;
+    }
+#pragma unroll
+    for (int st = 0; st < kSmallKW / 32; ++st) {
+        if (st < steps) {
+            const i32x4 fb = *reinterpret_cast<const i32x4 *>(&sb[r32][32 * st + 16 * h]);
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[st], fb, acc, 0, 0, 0);
+        }
+    }
+    // lane (column r32, half h) holds rows 8 g + 4 h + e, e < 4, of its column
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        s_part[wave][(8 * (i >> 2) + 4 * h + (i & 3)) * kSmallT + r32] = acc[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kSmallT * kSmallT / 256; ++q) {
+        const int o = tid + 256 * q;
+        const int row = o / kSmallT, col = o % kSmallT;
+        uint32_t v = static_cast<uint32_t>(s_part[0][o]) + static_cast<uint32_t>(s_part[1][o]) +
+                     static_cast<uint32_t>(s_part[2][o]) + static_cast<uint32_t>(s_part[3][o]);
+        if (a.C) {
+            v += static_cast<uint32_t>(a.C[static_cast<long long>(m0 + row) * a.ldc + n0 + col]);
+        }
+        int32_t x = static_cast<int32_t>(v);
+        x = x < a.cmin ? a.cmin : x;
+        x = x > a.cmax ? a.cmax : x;
+        static_cast<int32_t *>(a.D)[static_cast<long long>(m0 + row) * a.ldd + n0 + col] = x;
+    }
+}
+
+// The small clamp_i32 kernel when the shape fits it and the regular tiles would be few.
+bool launch_small_clamp(const Int8Args &a, hipStream_t stream)
+{
+    const long long regular = ((a.M + 63) / 64) * static_cast<long long>((a.N + kBN - 1) / kBN);
+    if (regular >= 64 || a.M % kSmallT != 0 || a.N % kSmallT != 0 || a.K % 128 != 0 ||
+        a.K > kSmallMaxK || a.K == 0) {
+        return false;
+    }
+    const long long blocks = static_cast<long long>(a.M / kSmallT) * (a.N / kSmallT);
+    hipLaunchKernelGGL(int8_small_clamp_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, a);
+    return true;
+}
+
 template <int AM, int BMd, int EPI, int PK = PK_NONE>
 void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *where)
 {
@@ -1905,6 +2013,12 @@ void launch_int8(const Int8Args &a, bool fast, hipStream_t stream, const char *w
     if constexpr (BMd == B_NK && AM == A_CONV_CL && EPI == EPI_REQUANT_I8) {
         if (fast && a.conv_bytes > 0 && a.cv.ICg % kSK == 0 && stream_offsets_fit(a, 1)) {
             launch_stream<EPI, PK, true>(a, stream);
+            check_launch(where);
+            return;
+        }
+    }
+    if constexpr (AM == A_MATRIX && BMd == B_KN && EPI == EPI_CLAMP_I32 && PK == PK_NONE) {
+        if (fast && a.d_row0 == 0 && launch_small_clamp(a, stream)) {
             check_launch(where);
             return;
         }
