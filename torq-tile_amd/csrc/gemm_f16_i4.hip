@@ -380,20 +380,18 @@ __global__ __launch_bounds__(1024) void w4a16_chunk_kernel(W4A16Args a, int nwg)
     const int erow = (tid >> 4) & 15;
     const int gn = (t_begin + et) * kNTile + (tid & 15);
     const bool out_col = et < ntl && gn < a.N;
-    float e_bias = 0.f, e_c[2] = {0.f, 0.f};
-    if (out_col) {
-        if (a.bias) {
-            e_bias = load_out<OUT>(a.bias, gn);
-        }
-        if (a.C) {
+    // Read as raw bits from clamped addresses with no branch, so that no conversion, and no
+    // wait for these loads, stands before the ring loads; an absent operand reads the first
+    // activation instead (never used).
+    const int gn_ld = min(gn, a.N - 1);
+    const void *dummy = a.A;
+    const uint32_t e_bias = load_out_bits<OUT>(a.bias ? a.bias : dummy, a.bias ? gn_ld : 0);
+    uint32_t e_c[2];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const int gm = mg0 + mt * 16 + erow;
-                if (gm < a.M) {
-                    e_c[mt] = load_out<OUT>(a.C, static_cast<long long>(gm) * a.ldc + gn);
-                }
-            }
-        }
+    for (int mt = 0; mt < 2; ++mt) {
+        const int gm = min(mg0 + mt * 16 + erow, a.M - 1);  // rows past m are not stored
+        e_c[mt] = load_out_bits<OUT>(a.C ? a.C : dummy,
+                                     a.C ? static_cast<long long>(gm) * a.ldc + gn_ld : 0);
     }
 
     // Load roles. Activations, two KiB per wave: plain rows 2w, 2w + 1 (lane i takes the row's
@@ -565,10 +563,10 @@ __global__ __launch_bounds__(1024) void w4a16_chunk_kernel(W4A16Args a, int nwg)
                 }
                 float v = static_cast<float>(s);
                 if (a.C) {
-                    v += e_c[mt];
+                    v += out_from_bits<OUT>(e_c[mt]);
                 }
                 if (a.bias) {
-                    v += e_bias;
+                    v += out_from_bits<OUT>(e_bias);
                 }
                 v = fmaxf(v, a.cmin);
                 v = fminf(v, a.cmax);

@@ -426,6 +426,31 @@ __device__ __forceinline__ float load_out(const void *p, long long i)
     }
 }
 
+// load_out in two halves: the element's raw bits now, the conversion later. A kernel that reads
+// its epilogue operands ahead of its main loads keeps the bits, so that no conversion (and no
+// wait for the load) stands before those loads; all-zero bits are +0 in every output type.
+template <int OUT>
+__device__ __forceinline__ uint32_t load_out_bits(const void *p, long long i)
+{
+    if constexpr (OUT == OUT_F32) {
+        return static_cast<const uint32_t *>(p)[i];
+    } else {
+        return static_cast<const uint16_t *>(p)[i];
+    }
+}
+
+template <int OUT>
+__device__ __forceinline__ float out_from_bits(uint32_t bits)
+{
+    if constexpr (OUT == OUT_F32) {
+        return __builtin_bit_cast(float, bits);
+    } else if constexpr (OUT == OUT_F16) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+    } else {
+        return bf16_bits_to_f32(static_cast<uint16_t>(bits));
+    }
+}
+
 template <int OUT>
 __device__ __forceinline__ void store_out(void *p, long long i, float v)
 {
