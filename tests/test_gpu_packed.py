@@ -170,7 +170,8 @@ def test_packer_overlapping_tail_panel(gpu, kind, action, src, which):
 # --------------------------------------------------------------------------------------------
 
 INT8_SHAPES = [(64, 256, 512, False), (130, 260, 192, True), (200, 136, 80, False),
-               (3, 8, 11, False), (60, 63, 127, True), (257, 129, 1024, True), (1, 128, 64, False)]
+               (3, 8, 11, False), (60, 63, 127, True), (257, 129, 1024, True), (1, 128, 64, False),
+               (64, 256, 128, False), (130, 260, 384, True)]
 
 
 def packed_i8(kind, action, M, rows, k):
@@ -257,7 +258,8 @@ def test_w4a8_packed_run(gpu, m, n, k):
 
 W4A16_SHAPES = [(32, 96, 2048, 32), (32, 14336 // 64, 4096, 32), (33, 40, 3072, 32),
                 (32, 48, 384, 32), (7, 20, 64, 16), (5, 18, 96, 32),
-                (33, 8200, 2048, 32), (20, 4104, 4096, 32)]
+                (33, 8200, 2048, 32), (20, 4104, 4096, 32), (32, 96, 1024, 32),
+                (17, 300, 1536, 32)]
 
 
 def run_w4a16p(shim, d, lda_extra=0):

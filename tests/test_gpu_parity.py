@@ -24,7 +24,11 @@ INT8_REF_SHAPES = [(32, 32, 32, False), (3, 8, 11, False), (5, 11, 10, False), (
                    (15, 32, 25, False), (60, 63, 127, False), (32, 32, 32, True),
                    (60, 63, 127, True)]
 INT8_FAST_SHAPES = [(64, 256, 512, False), (130, 260, 192, True), (200, 136, 80, False),
-                    (1, 128, 64, False), (257, 129, 1024, True)]
+                    (1, 128, 64, False), (257, 129, 1024, True),
+                    # stream kernel with 1, 2, 3 and 5 k-stages of 128 (the column multipliers
+                    # after the loop, in the last stage, and the ring shorter than its depth)
+                    (64, 256, 128, False), (96, 200, 256, True), (130, 260, 384, False),
+                    (33, 129, 640, True)]
 
 
 def _gr():
@@ -272,7 +276,10 @@ W4A16_FAST_SHAPES = [(32, 256, 4096, 32, dict(bias=True)), (1, 48, 128, 32, dict
                      # rows past m (k 2048), and 1-2 tiles per workgroup ending in a partial
                      # tile (k 4096)
                      (33, 8200, 2048, 32, dict(c=True, bias=True)),
-                     (20, 4104, 4096, 32, dict(bias=True, clamp=(-0.5, 0.5)))]
+                     (20, 4104, 4096, 32, dict(bias=True, clamp=(-0.5, 0.5))),
+                     # chunk kernel with two and three 512-k chunks (the ring not yet full)
+                     (32, 96, 1024, 32, dict(bias=True)),
+                     (17, 300, 1536, 32, dict(c=True, clamp=(-0.5, 0.5)))]
 
 
 @pytest.mark.parametrize("m,n,k,bl,opt", W4A16_REF_SHAPES + W4A16_FAST_SHAPES)
