@@ -171,7 +171,7 @@ def test_packer_overlapping_tail_panel(gpu, kind, action, src, which):
 
 INT8_SHAPES = [(64, 256, 512, False), (130, 260, 192, True), (200, 136, 80, False),
                (3, 8, 11, False), (60, 63, 127, True), (257, 129, 1024, True), (1, 128, 64, False),
-               (64, 256, 128, False), (130, 260, 384, True)]
+               (64, 256, 128, False), (130, 260, 384, True), (1280, 2048, 256, False)]
 
 
 def packed_i8(kind, action, M, rows, k):

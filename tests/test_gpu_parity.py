@@ -28,7 +28,9 @@ INT8_FAST_SHAPES = [(64, 256, 512, False), (130, 260, 192, True), (200, 136, 80,
                     # stream kernel with 1, 2, 3 and 5 k-stages of 128 (the column multipliers
                     # after the loop, in the last stage, and the ring shorter than its depth)
                     (64, 256, 128, False), (96, 200, 256, True), (130, 260, 384, False),
-                    (33, 129, 640, True)]
+                    (33, 129, 640, True),
+                    # 128-row tiles (chosen once they still fill 160 or more CUs), ragged
+                    (1200, 2100, 384, True)]
 
 
 def _gr():
