@@ -109,7 +109,9 @@ def check(shim, d, f16, packed, **kw):
 # (m, n, k): k % 128 == 0 takes the streaming kernel, other k % 16 == 0 the double-buffered
 # kernel, the rest the generic one; m and n not multiples of the 128 tile leave partial tiles
 SHAPES = [(64, 256, 512), (257, 129, 1024), (1, 128, 4096), (130, 260, 192), (60, 63, 128),
-          (3, 8, 11), (60, 63, 127), (33, 70, 96)]
+          (3, 8, 11), (60, 63, 127), (33, 70, 96),
+          # stream kernel on 128-row tiles, ragged, three k-stages
+          (1200, 2100, 384)]
 
 
 @pytest.mark.parametrize("m,n,k", SHAPES)
