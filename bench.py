@@ -274,7 +274,7 @@ def load_support():
     sup.tqtb_stream_floor_async.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int, vp, sz, vp]
     sup.tqtb_empty_async.restype = ctypes.c_int
-    sup.tqtb_empty_async.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp]
+    sup.tqtb_empty_async.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
     sup.tqtb_stream_lds_bytes.restype = ctypes.c_int
     sup.tqtb_stream_lds_bytes.argtypes = []
     sup.tqtb_run_w4a16_async.restype = None
@@ -376,20 +376,39 @@ def bench_stream_floor(torch, timer, warmup, steps, resident=False):
                 per_cu_gbs=per_cu / (ms * 1e-3) / 1e9)
 
 
-def bench_empty(torch, timer, warmup, steps):
-    """An empty kernel with the W8A8 stream kernel's launch shape (256 workgroups of 512
-    threads, its LDS size): the per-launch cost of that shape in a graph."""
+def bench_empty(torch, timer, warmup, steps, blocks=256, threads=512, lds=None):
+    """An empty kernel with a kernel's launch shape (default: the W8A8 stream kernel's, 256
+    workgroups of 512 threads and its LDS size): the per-launch cost of that shape in a graph."""
     sup = load_support()
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
-    lds = sup.tqtb_stream_lds_bytes() + 1536  # the ring and the multiplier arrays
+    if lds is None:
+        lds = sup.tqtb_stream_lds_bytes() + 1536  # the ring and the multiplier arrays
     s = timer.stream.cuda_stream
 
     def launch(i):
-        if sup.tqtb_empty_async(256, lds, sink.data_ptr(), s):
+        if sup.tqtb_empty_async(blocks, threads, lds, sink.data_ptr(), s):
             raise RuntimeError("empty launch failed")
 
     ms = timer.run(launch, 1, warmup, steps)
     return dict(ms=ms, bytes=0, copies=1)
+
+
+def launch_shapes(torch):
+    """Grid, block and LDS bytes of the other headline kernels at their configurations, as the
+    library launches them: the W4A8 strip kernel (4 waves of 4 channels per workgroup, no LDS),
+    the W4A16 chunk kernel (at most one 1024-thread workgroup per CU, a three-slot ring of
+    50 KiB chunks) and the igemmcl halo kernel (256 pixels x 64 channels per workgroup, 152 KiB
+    of halo and weights plus four 64-entry epilogue arrays)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    w4a16_tiles = (W4A16["n"] + 15) // 16
+    w4a16_wgs = max((w4a16_tiles + 3) // 4, min(w4a16_tiles, cus))
+    conv_px = CONV["ID"] * CONV["IH"] * CONV["IW"]
+    return {
+        "w4a8 strip (M=1)": ((W4A8["n"] + 15) // 16, 256, 0),
+        "w4a16 chunk": (w4a16_wgs, 1024, 3 * (32768 + 16384 + 2048)),
+        "igemmcl halo": (8 * ((((conv_px + 255) // 256) * (CONV["OC"] // 64) + 7) // 8), 512,
+                         152 * 1024 + 4 * 64 * 4),
+    }
 
 
 def bench_caller(torch, mod, lib, kind, reps=5):
@@ -797,6 +816,9 @@ def main():
         sfr = progress("w8a8 stream floor L2-resident",
                        bench_stream_floor(torch, timer, W, K, resident=True))
         em = progress("empty launch", bench_empty(torch, timer, W, K))
+        ems = {name: progress("empty launch " + name,
+                              bench_empty(torch, timer, W, K, blocks=b, threads=t, lds=l))
+               for name, (b, t, l) in launch_shapes(torch).items()}
         cw8 = progress("reference caller w8a8", bench_caller(torch, mod, lib, "w8a8"))
         cw4 = progress("reference caller w4a8", bench_caller(torch, mod, lib, "w4a8"))
 
@@ -839,6 +861,10 @@ def main():
             "empty_launch_us": round(em["ms"] * 1e3, 3),
             "frac_of_stream_floor": round(sf["ms"] / w8["ms"], 4),
         },
+        # an empty kernel with each headline kernel's grid, block and LDS size, graph-replayed
+        # like the kernels: the fixed per-launch cost inside each kernel's figure
+        "launch_floors_us": dict([("w8a8 stream", round(em["ms"] * 1e3, 3))] +
+                                 [(name, round(r["ms"] * 1e3, 3)) for name, r in ems.items()]),
         # the reference's caller pattern: one synchronous run per m_step x n_step tile
         # (host wall clock per whole GEMM, warm operands), and the same tiles through the
         # stream-ordered runs with one synchronization

@@ -11,8 +11,8 @@
 //    tile order, LDS-DMA load roles, four-slot ring, per-stage waits and barriers; no MFMA, no
 //    epilogue): the per-CU L2 -> LDS stream floor of that kernel's shape, on cold operands or,
 //    with `resident`, with every workgroup reading the first tile's rows (L2-resident).
-//  * tqtb_empty_async: an empty kernel launched with the stream kernel's grid, block and LDS
-//    size: the launch cost of that shape.
+//  * tqtb_empty_async: an empty kernel launched with a given grid, block and LDS size (the
+//    headline kernels' shapes): the launch cost of that shape.
 //  * tqtb_run_w4a16*_async: the W4A16 entry points take their clamp bounds as _Float16 by
 //    value, which ctypes cannot pass (x86-64 passes them in SSE registers); these forward the
 //    bounds given as their 16-bit patterns.
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kSfWaves * 64) void stream_floor_kernel(
     }
 }
 
-__global__ __launch_bounds__(kSfWaves * 64) void empty_kernel(uint32_t *sink)
+__global__ __launch_bounds__(1024) void empty_kernel(uint32_t *sink)
 {
     extern __shared__ uint32_t dyn[];
     if (sink == nullptr) {
@@ -221,13 +221,15 @@ int tqtb_stream_floor_async(const void *A, const void *B, int M, int N, int K, i
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// An empty kernel with `blocks` workgroups of 512 threads and `lds_bytes` of LDS.
-int tqtb_empty_async(int blocks, int lds_bytes, void *sink, void *stream)
+// An empty kernel with `blocks` workgroups of `threads` threads (a multiple of 64, at most 1024)
+// and `lds_bytes` of LDS.
+int tqtb_empty_async(int blocks, int threads, int lds_bytes, void *sink, void *stream)
 {
-    if (blocks <= 0 || lds_bytes < 0 || lds_bytes > 160 * 1024 || sink == nullptr) {
+    if (blocks <= 0 || threads <= 0 || threads > 1024 || threads % 64 != 0 || lds_bytes < 0 ||
+        lds_bytes > 160 * 1024 || sink == nullptr) {
         return -1;
     }
-    hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(kSfWaves * 64), lds_bytes,
+    hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(threads), lds_bytes,
                        static_cast<hipStream_t>(stream), static_cast<uint32_t *>(sink));
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
