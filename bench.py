@@ -393,13 +393,12 @@ def bench_empty(torch, timer, warmup, steps, blocks=256, threads=512, lds=None):
     return dict(ms=ms, bytes=0, copies=1)
 
 
-def launch_shapes(torch):
+def launch_shapes(cus):
     """Grid, block and LDS bytes of the other headline kernels at their configurations, as the
     library launches them: the W4A8 strip kernel (4 waves of 4 channels per workgroup, no LDS),
     the W4A16 chunk kernel (at most one 1024-thread workgroup per CU, a three-slot ring of
     50 KiB chunks) and the igemmcl halo kernel (256 pixels x 64 channels per workgroup, 152 KiB
-    of halo and weights plus four 64-entry epilogue arrays)."""
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    of halo and weights plus four 64-entry epilogue arrays). cus: the GPU's CU count."""
     w4a16_tiles = (W4A16["n"] + 15) // 16
     w4a16_wgs = max((w4a16_tiles + 3) // 4, min(w4a16_tiles, cus))
     conv_px = CONV["ID"] * CONV["IH"] * CONV["IW"]
@@ -818,7 +817,8 @@ def main():
         em = progress("empty launch", bench_empty(torch, timer, W, K))
         ems = {name: progress("empty launch " + name,
                               bench_empty(torch, timer, W, K, blocks=b, threads=t, lds=l))
-               for name, (b, t, l) in launch_shapes(torch).items()}
+               for name, (b, t, l) in launch_shapes(
+                   torch.cuda.get_device_properties(0).multi_processor_count).items()}
         cw8 = progress("reference caller w8a8", bench_caller(torch, mod, lib, "w8a8"))
         cw4 = progress("reference caller w4a8", bench_caller(torch, mod, lib, "w4a8"))
 

@@ -1,5 +1,6 @@
 """Host logic of bench.py that needs no GPU: which bench leg each product kernel's counters are
-attributed to (the HBM traffic and counter summaries sum per leg by demangled kernel name)."""
+attributed to (the HBM traffic and counter summaries sum per leg by demangled kernel name), and
+the launch shapes the empty-launch floors use."""
 
 import os
 import sys
@@ -29,3 +30,18 @@ NS = "tqt::(anonymous namespace)::"
 ])
 def test_leg_of_kernel(name, leg):
     assert bench.leg_of_kernel(name) == leg
+
+
+def test_launch_shapes_mi355x():
+    """The launch shapes at the bench configurations on 256 CUs: W4A8 strip kernel 11008 / 16
+    workgroups of 4 waves; W4A16 chunk kernel one 1024-thread workgroup per CU (896 tiles need
+    224) with its 3 x 50 KiB ring; igemmcl halo kernel 196 tiles rounded up to the 8 XCDs (200)
+    with 152 KiB + 1 KiB of LDS."""
+    shapes = bench.launch_shapes(256)
+    assert shapes == {
+        "w4a8 strip (M=1)": (688, 256, 0),
+        "w4a16 chunk": (256, 1024, 153600),
+        "igemmcl halo": (200, 512, 156672),
+    }
+    # fewer CUs than W4A16 workgroups needed: one per 64 channels
+    assert bench.launch_shapes(200)["w4a16 chunk"][0] == 224
